@@ -1,0 +1,176 @@
+/*
+ * nt_moe.h -- C ABI of the MI355X (gfx950) mixture-of-experts layer forward.
+ *
+ * One shared library, libnt_moe.so, exports these entry points. Every entry point
+ *   - returns an int status: NT_MOE_OK (0) or a negative NT_MOE_E* code;
+ *   - records a message for the calling thread, read back with nt_moe_last_error();
+ *   - never throws, never allocates device memory, never synchronises the stream;
+ *   - takes caller-owned device buffers as plain pointers plus explicit sizes, and
+ *     enqueues its kernels on the caller's hipStream_t (0 = the null stream).
+ * Scratch memory is passed in as `workspace` and sized by the *_workspace_bytes queries.
+ *
+ * Element types: "bf16" buffers hold IEEE bfloat16 bit patterns (uint16_t); "e4m3" buffers
+ * hold OCP FP8 E4M3FN bytes (max finite 448, the gfx950 hardware format); all indices are
+ * int32 and all scales, weights and losses are fp32.
+ *
+ * Reference interfaces these replace (paths relative to the NextTransformer tree):
+ *   router      -> NativeRouter.gating + TopKRouter routing
+ *                  (nexttransformer/scaling/megatron_moe.py:86-102, :43-45),
+ *                  RoutedFFN router/topk/softmax (nexttransformer/scaling/reference_blocks.py:37-38)
+ *   route plan  -> mapping.T.nonzero / mapping.sum(0) / probs.T[mapping.T] / rows[ids]
+ *                  (nexttransformer/scaling/megatron_moe.py:142-145)
+ *   grouped ffn -> SequentialMLP over MasterLinear (megatron_moe.py:58-78, :145) and
+ *                  FlexibleMLP (nexttransformer/models/lm.py:29-35)
+ *   combine     -> zeros_like(rows).index_add(0, ids, output) + shared_experts
+ *                  (megatron_moe.py:148-150); RoutedFFN index_add loop (reference_blocks.py:39-44)
+ *   aux loss    -> TopKRouter aux/z loss with moe_aux_loss_coeff / moe_z_loss_coeff
+ *                  (megatron_moe.py:44-45; nexttransformer/scaling/moe_recipe.py:40-41)
+ */
+#ifndef NT_MOE_H
+#define NT_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NT_MOE_ABI_VERSION 1
+
+#define NT_MOE_OK 0
+#define NT_MOE_EINVAL (-22)  /* invalid argument: shape, pointer, enum, alignment */
+#define NT_MOE_ENOSPC (-28)  /* workspace smaller than the matching *_workspace_bytes query */
+#define NT_MOE_EDEVICE (-5)  /* HIP runtime error while launching */
+
+/* score_fn values (TopKRouter moe_router_score_function). */
+#define NT_MOE_SCORE_SOFTMAX 0 /* top-k on logits, softmax over the k selected */
+#define NT_MOE_SCORE_SIGMOID 1 /* top-k on logits, sigmoid scores normalised over the k selected */
+
+/* activation values of the expert FFN. */
+#define NT_MOE_ACT_SWIGLU 0 /* fc1 rows [0,H) are the gate, [H,2H) the value: silu(g) * u */
+#define NT_MOE_ACT_RELU2 1  /* fc1 has H rows: relu(g)^2 (megatron_moe.py:23-24) */
+
+/* Largest supported sizes. */
+#define NT_MOE_MAX_EXPERTS 256
+#define NT_MOE_MAX_TOPK 8
+#define NT_MOE_MAX_SEGMENTS 1024
+/* Tokens per router / histogram block: aux partial buffers have ceil(T / 64) rows. */
+#define NT_MOE_ROUTE_BLOCK 64
+
+typedef struct ihipStream_t* nt_moe_stream_t; /* a hipStream_t */
+
+int nt_moe_abi_version(void);
+const char* nt_moe_last_error(void);
+
+/*
+ * Router: logits = x . Wr^T (+ bias) in fp32 with a fixed reduction order, then scoring and
+ * top-k. Replaces NativeRouter.gating (megatron_moe.py:95-100) and TopKRouter's top-k /
+ * softmax-over-selected (megatron_moe.py:43; reference_blocks.py:37-38).
+ *
+ * Fixed order (the bit-exact contract): for each (t, e), c_j = fma-chain over the features
+ * k in [128 j, min(128 j + 128, d)) in ascending k, starting from 0.0f; logit = c_0 + c_1 + ...
+ * added left to right; then logit += bias[e] when bias is given. x is widened exactly.
+ * Top-k: descending logit; equal logits go to the lower expert index.
+ *
+ *   x           bf16 [T, ld_x], d used columns (d % 8 == 0, ld_x % 8 == 0)
+ *   w_router_t  fp32 [d, E]  (the router weight transposed, E contiguous)
+ *   logit_bias  fp32 [E] or NULL
+ *   logits      fp32 [T, E] or NULL (written when given)
+ *   topk_ids    int32 [T, k], topk_w fp32 [T, k]
+ *   prob_partial fp32 [ceil(T/64), E]: per 64-token block, sum over its tokens of the
+ *                full score s_te (softmax over all E, or sigmoid normalised over all E)
+ *   z_partial   fp32 [ceil(T/64)]: per block, sum of logsumexp(logits_t)^2
+ *   workspace   nt_moe_router_workspace_bytes(T, d, E, k) bytes (may be 0)
+ */
+size_t nt_moe_router_workspace_bytes(int64_t T, int32_t d, int32_t E, int32_t k);
+int nt_moe_router_fwd(const uint16_t* x, int64_t ld_x, const float* w_router_t,
+                      const float* logit_bias, int64_t T, int32_t d, int32_t E, int32_t k,
+                      int32_t score_fn, float* logits, int32_t* topk_ids, float* topk_w,
+                      float* prob_partial, float* z_partial, void* workspace,
+                      size_t workspace_bytes, nt_moe_stream_t stream);
+
+/*
+ * Top-k and scoring from caller-supplied fp32 logits [T, E] (no gating GEMM): the same
+ * selection, weights and partials as nt_moe_router_fwd. Lets routing be checked on logits
+ * computed elsewhere (e.g. the reference's own F.linear, megatron_moe.py:99).
+ */
+int nt_moe_topk_from_logits(const float* logits, int64_t T, int32_t E, int32_t k,
+                            int32_t score_fn, int32_t* topk_ids, float* topk_w,
+                            float* prob_partial, float* z_partial, nt_moe_stream_t stream);
+
+/*
+ * Route plan: per-expert histogram of topk_ids with an LDS prefix scan.
+ * Replaces counts = mapping.sum(0) (megatron_moe.py:143) and the offsets implied by the
+ * expert-major order of mapping.T.nonzero() (megatron_moe.py:142).
+ *   counts   int32 [E]    tokens routed to each expert
+ *   offsets  int32 [E+1]  exclusive prefix of counts (offsets[E] = T*k)
+ *   workspace nt_moe_route_workspace_bytes(T, k, E) bytes; pass the same buffer,
+ *            unmodified, to nt_moe_permute.
+ */
+size_t nt_moe_route_workspace_bytes(int64_t T, int32_t k, int32_t E);
+int nt_moe_histogram_scan(const int32_t* topk_ids, int64_t T, int32_t k, int32_t E,
+                          int32_t* counts, int32_t* offsets, void* workspace,
+                          size_t workspace_bytes, nt_moe_stream_t stream);
+
+/*
+ * Permute: the expert-major, token-ascending permutation (megatron_moe.py:142-145).
+ * Destination row of (t, j) = offsets[e] + #{t' < t routed to e}, e = topk_ids[t, j].
+ *   src_row       int32 [T*k]  token feeding each permuted row (ids of the reference)
+ *   perm_w        fp32 [T*k] or NULL  routing weight of each permuted row (selected_probs)
+ *   combine_dest  int32 [T, k] permuted rows of token t, in ascending expert order
+ *   combine_w     fp32  [T, k] matching routing weights
+ *   x_perm        bf16 [T*k, d] or NULL: the gathered rows rows[ids] (x read once per token)
+ */
+int nt_moe_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
+                   const float* topk_w, int64_t T, int32_t d, int32_t k, int32_t E,
+                   const void* workspace, size_t workspace_bytes, int32_t* src_row,
+                   float* perm_w, int32_t* combine_dest, float* combine_w, uint16_t* x_perm,
+                   nt_moe_stream_t stream);
+
+/*
+ * Grouped expert FFN over ragged segments, bf16 MFMA with fp32 accumulation:
+ *   h[r] = act(a_r . W1_s^T)  (bf16 [rows, H]),   y[r] = h[r] . W2_s^T  (bf16 [rows, d])
+ * for every row r of segment s, rows [seg_offsets[s], seg_offsets[s+1]).
+ * Replaces SequentialMLP's per-expert loop (megatron_moe.py:145) over MasterLinear
+ * fc1 -> activation -> fc2 (megatron_moe.py:58-78; lm.py:29-35).
+ *   a            bf16 [a_rows, ld_a]: row r reads a[src_row[r]] when src_row is given
+ *                (gather fused into the load; indices are clamped to [0, a_rows)), else a[r]
+ *   seg_offsets  int32 [num_segments+1], device memory, non-decreasing, [0] = 0; values are
+ *                clamped to [0, total_rows]
+ *   w1           bf16 [num_segments, F, d], F = 2H (SWIGLU) or H (RELU2)
+ *   w2           bf16 [num_segments, d, H]
+ *   h            bf16 [total_rows, H] (intermediate, caller-owned)
+ *   y            bf16 [total_rows, d]
+ *   total_rows   upper bound of seg_offsets[num_segments] used to size the launch
+ * Requirements: d % 64 == 0, H % 64 == 0, 16-byte aligned buffers.
+ */
+int nt_moe_grouped_ffn_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows, const int32_t* src_row,
+                            const int32_t* seg_offsets, int32_t num_segments,
+                            int64_t total_rows, const uint16_t* w1, const uint16_t* w2,
+                            int32_t d, int32_t H, int32_t activation, uint16_t* h,
+                            uint16_t* y, nt_moe_stream_t stream);
+
+/*
+ * Deterministic weighted combine plus the load-balance and z auxiliary losses.
+ *   out[t] = sum over j in ascending expert order of combine_w[t,j] * y[combine_dest[t,j]]
+ *            (+ shared_y[t] when given), accumulated in fp32, rounded once to bf16.
+ * Replaces zeros_like(rows).index_add(0, ids, output) + shared_experts(hidden)
+ * (megatron_moe.py:148-150) and RoutedFFN's per-expert index_add (reference_blocks.py:39-44).
+ * Aux (MCore "aux_loss" type, megatron_moe.py:44-45):
+ *   lb = aux_coeff * E / (k * T^2) * sum_e (sum_t s_te) * counts[e]
+ *   z  = z_coeff * mean_t logsumexp(logits_t)^2
+ *   aux_out fp32 [3] = {lb + z, lb, z}
+ */
+int nt_moe_combine_aux(const uint16_t* y, const int32_t* combine_dest, const float* combine_w,
+                       int64_t T, int32_t d, int32_t k, const uint16_t* shared_y,
+                       int64_t ld_shared, uint16_t* out, int64_t ld_out,
+                       const float* prob_partial, const float* z_partial,
+                       const int32_t* counts, int32_t E, float aux_coeff, float z_coeff,
+                       float* aux_out, nt_moe_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NT_MOE_H */

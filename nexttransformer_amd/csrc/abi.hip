@@ -1,0 +1,249 @@
+// C-ABI shim: argument validation, workspace layout and status codes around the kernel
+// launchers. Declarations and contracts: include/nt_moe.h.
+//
+// Error model (mirrors the reference's ValueError / RuntimeError split,
+// nexttransformer/scaling/moe_recipe.py:54-72, megatron_moe.py:97-98): invalid arguments give
+// NT_MOE_EINVAL, a short workspace NT_MOE_ENOSPC, a failed launch NT_MOE_EDEVICE; the message
+// is kept per thread for nt_moe_last_error(). Nothing here allocates device memory or
+// synchronises.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <atomic>
+
+#include "common.h"
+
+namespace ntmoe {
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof g_error, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_error[0] = '\0';
+  return NT_MOE_OK;
+}
+
+int launched(hipError_t err, const char* what) {
+  if (err != hipSuccess)
+    return fail(NT_MOE_EDEVICE, "%s: launch failed: %s", what, hipGetErrorString(err));
+  return ok();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
+
+constexpr int kHistBlock = 256;  // tokens per histogram block (route.hip)
+
+struct RouteWorkspace {
+  int32_t* ranks;
+  int32_t* block_counts;
+};
+
+size_t route_ws_bytes(int64_t T, int k, int E) {
+  int64_t nblk = (T + kHistBlock - 1) / kHistBlock;
+  return align256((size_t)T * k * 4) + align256((size_t)nblk * E * 4);
+}
+
+RouteWorkspace route_ws(void* ws, int64_t T, int k) {
+  RouteWorkspace r;
+  r.ranks = reinterpret_cast<int32_t*>(ws);
+  r.block_counts = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(ws) + align256((size_t)T * k * 4));
+  return r;
+}
+
+#define NT_REQUIRE(cond, ...) \
+  do {                        \
+    if (!(cond)) return fail(NT_MOE_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+int check_route_shape(int64_t T, int k, int E) {
+  NT_REQUIRE(T >= 0 && T <= (int64_t)1 << 26, "T must be in [0, 2^26], got %lld", (long long)T);
+  NT_REQUIRE(E >= 1 && E <= NT_MOE_MAX_EXPERTS, "E must be in [1, %d], got %d", NT_MOE_MAX_EXPERTS, E);
+  NT_REQUIRE(k >= 1 && k <= NT_MOE_MAX_TOPK && k <= E, "top-k must be in [1, min(%d, E)], got %d",
+             NT_MOE_MAX_TOPK, k);
+  NT_REQUIRE(T * k < ((int64_t)1 << 31), "T * k must fit int32");
+  return NT_MOE_OK;
+}
+
+}  // namespace
+
+int num_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+hipError_t allow_dynamic_lds(const void* kernel, size_t bytes) {
+  if (bytes <= 65536) return hipSuccess;
+  return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+}  // namespace ntmoe
+
+using namespace ntmoe;
+
+extern "C" {
+
+int nt_moe_abi_version(void) { return NT_MOE_ABI_VERSION; }
+
+const char* nt_moe_last_error(void) { return g_error; }
+
+size_t nt_moe_router_workspace_bytes(int64_t T, int32_t d, int32_t E, int32_t k) {
+  (void)k;
+  if (T <= 0 || d <= 0 || E <= 0) return 0;
+  int nchunk = router_split_chunks(T, d, E);
+  return (size_t)nchunk * (size_t)T * (size_t)E * sizeof(float);
+}
+
+int nt_moe_router_fwd(const uint16_t* x, int64_t ld_x, const float* w_router_t,
+                      const float* logit_bias, int64_t T, int32_t d, int32_t E, int32_t k,
+                      int32_t score_fn, float* logits, int32_t* topk_ids, float* topk_w,
+                      float* prob_partial, float* z_partial, void* workspace,
+                      size_t workspace_bytes, nt_moe_stream_t stream) {
+  int rc = check_route_shape(T, k, E);
+  if (rc) return rc;
+  NT_REQUIRE(d > 0 && d % 8 == 0, "router: d must be a positive multiple of 8, got %d", d);
+  NT_REQUIRE(ld_x >= d && ld_x % 8 == 0, "router: ld_x must be >= d and a multiple of 8");
+  NT_REQUIRE(score_fn == NT_MOE_SCORE_SOFTMAX || score_fn == NT_MOE_SCORE_SIGMOID,
+             "router: unknown score_fn %d", score_fn);
+  if (T == 0) return ok();
+  NT_REQUIRE(x && w_router_t && topk_ids && topk_w && prob_partial && z_partial,
+             "router: null buffer");
+  NT_REQUIRE(aligned16(x), "router: x must be 16-byte aligned");
+  int nchunk = router_split_chunks(T, d, E);
+  size_t need = (size_t)nchunk * (size_t)T * (size_t)E * sizeof(float);
+  bool split = nchunk > 0 && workspace && workspace_bytes >= need;
+  hipError_t err = launch_router(x, ld_x, w_router_t, logit_bias, T, d, E, k, score_fn, logits,
+                                 topk_ids, topk_w, prob_partial, z_partial,
+                                 reinterpret_cast<float*>(workspace), split,
+                                 reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "router");
+}
+
+int nt_moe_topk_from_logits(const float* logits, int64_t T, int32_t E, int32_t k,
+                            int32_t score_fn, int32_t* topk_ids, float* topk_w,
+                            float* prob_partial, float* z_partial, nt_moe_stream_t stream) {
+  int rc = check_route_shape(T, k, E);
+  if (rc) return rc;
+  NT_REQUIRE(score_fn == NT_MOE_SCORE_SOFTMAX || score_fn == NT_MOE_SCORE_SIGMOID,
+             "topk: unknown score_fn %d", score_fn);
+  if (T == 0) return ok();
+  NT_REQUIRE(logits && topk_ids && topk_w && prob_partial && z_partial, "topk: null buffer");
+  hipError_t err = launch_topk_from_logits(logits, T, E, k, score_fn, topk_ids, topk_w,
+                                           prob_partial, z_partial,
+                                           reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "topk");
+}
+
+size_t nt_moe_route_workspace_bytes(int64_t T, int32_t k, int32_t E) {
+  if (T < 0 || k <= 0 || E <= 0) return 0;
+  return route_ws_bytes(T, k, E);
+}
+
+int nt_moe_histogram_scan(const int32_t* topk_ids, int64_t T, int32_t k, int32_t E,
+                          int32_t* counts, int32_t* offsets, void* workspace,
+                          size_t workspace_bytes, nt_moe_stream_t stream) {
+  int rc = check_route_shape(T, k, E);
+  if (rc) return rc;
+  NT_REQUIRE(counts && offsets && workspace, "histogram: null buffer");
+  NT_REQUIRE(T == 0 || topk_ids, "histogram: null topk_ids");
+  if (workspace_bytes < route_ws_bytes(T, k, E))
+    return fail(NT_MOE_ENOSPC, "histogram: workspace %zu < %zu bytes", workspace_bytes,
+                route_ws_bytes(T, k, E));
+  RouteWorkspace ws = route_ws(workspace, T, k);
+  hipError_t err = launch_histogram_scan(topk_ids, T, k, E, counts, offsets, ws.ranks,
+                                         ws.block_counts, reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "histogram_scan");
+}
+
+int nt_moe_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
+                   const float* topk_w, int64_t T, int32_t d, int32_t k, int32_t E,
+                   const void* workspace, size_t workspace_bytes, int32_t* src_row,
+                   float* perm_w, int32_t* combine_dest, float* combine_w, uint16_t* x_perm,
+                   nt_moe_stream_t stream) {
+  int rc = check_route_shape(T, k, E);
+  if (rc) return rc;
+  if (T == 0) return ok();
+  NT_REQUIRE(topk_ids && topk_w && workspace && src_row && combine_dest && combine_w,
+             "permute: null buffer");
+  if (workspace_bytes < route_ws_bytes(T, k, E))
+    return fail(NT_MOE_ENOSPC, "permute: workspace %zu < %zu bytes", workspace_bytes,
+                route_ws_bytes(T, k, E));
+  if (x_perm) {
+    NT_REQUIRE(x, "permute: x_perm requested without x");
+    NT_REQUIRE(d > 0 && d % 8 == 0, "permute: d must be a positive multiple of 8, got %d", d);
+    NT_REQUIRE(ld_x >= d && ld_x % 8 == 0, "permute: ld_x must be >= d and a multiple of 8");
+    NT_REQUIRE(aligned16(x) && aligned16(x_perm), "permute: x and x_perm must be 16-byte aligned");
+  }
+  RouteWorkspace ws = route_ws(const_cast<void*>(workspace), T, k);
+  hipError_t err = launch_permute(x, ld_x, topk_ids, topk_w, T, d, k, E, ws.ranks,
+                                  ws.block_counts, src_row, perm_w, combine_dest, combine_w,
+                                  x_perm, reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "permute");
+}
+
+int nt_moe_grouped_ffn_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows, const int32_t* src_row,
+                            const int32_t* seg_offsets, int32_t num_segments,
+                            int64_t total_rows, const uint16_t* w1, const uint16_t* w2,
+                            int32_t d, int32_t H, int32_t activation, uint16_t* h,
+                            uint16_t* y, nt_moe_stream_t stream) {
+  NT_REQUIRE(d > 0 && d % 64 == 0, "grouped_ffn: d must be a positive multiple of 64, got %d", d);
+  NT_REQUIRE(H > 0 && H % 64 == 0, "grouped_ffn: H must be a positive multiple of 64, got %d", H);
+  NT_REQUIRE(num_segments >= 1 && num_segments <= NT_MOE_MAX_SEGMENTS,
+             "grouped_ffn: num_segments must be in [1, %d]", NT_MOE_MAX_SEGMENTS);
+  NT_REQUIRE(total_rows >= 0 && total_rows < ((int64_t)1 << 31), "grouped_ffn: bad total_rows");
+  NT_REQUIRE(activation == NT_MOE_ACT_SWIGLU || activation == NT_MOE_ACT_RELU2,
+             "grouped_ffn: unknown activation %d", activation);
+  NT_REQUIRE(ld_a >= d && ld_a % 8 == 0, "grouped_ffn: ld_a must be >= d and a multiple of 8");
+  NT_REQUIRE(a_rows >= 1, "grouped_ffn: a_rows must be positive");
+  NT_REQUIRE(src_row || a_rows >= total_rows, "grouped_ffn: a needs total_rows rows without src_row");
+  NT_REQUIRE(a && seg_offsets && w1 && w2 && h && y, "grouped_ffn: null buffer");
+  NT_REQUIRE(aligned16(a) && aligned16(w1) && aligned16(w2) && aligned16(h) && aligned16(y),
+             "grouped_ffn: buffers must be 16-byte aligned");
+  if (total_rows == 0) return ok();
+  hipError_t err = launch_grouped_ffn_bf16(a, ld_a, a_rows, src_row, seg_offsets, num_segments,
+                                           total_rows, w1, w2, d, H, activation, h, y,
+                                           reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "grouped_ffn_bf16");
+}
+
+int nt_moe_combine_aux(const uint16_t* y, const int32_t* combine_dest, const float* combine_w,
+                       int64_t T, int32_t d, int32_t k, const uint16_t* shared_y,
+                       int64_t ld_shared, uint16_t* out, int64_t ld_out,
+                       const float* prob_partial, const float* z_partial,
+                       const int32_t* counts, int32_t E, float aux_coeff, float z_coeff,
+                       float* aux_out, nt_moe_stream_t stream) {
+  int rc = check_route_shape(T, k, E);
+  if (rc) return rc;
+  NT_REQUIRE(d > 0 && d % 8 == 0, "combine: d must be a positive multiple of 8, got %d", d);
+  NT_REQUIRE(ld_out >= d && ld_out % 8 == 0, "combine: ld_out must be >= d and a multiple of 8");
+  NT_REQUIRE(!shared_y || (ld_shared >= d && ld_shared % 8 == 0 && aligned16(shared_y)),
+             "combine: shared_y needs ld_shared >= d, a multiple of 8, 16-byte alignment");
+  if (T > 0) {
+    NT_REQUIRE(y && combine_dest && combine_w && out, "combine: null buffer");
+    NT_REQUIRE(aligned16(y) && aligned16(out), "combine: y and out must be 16-byte aligned");
+  }
+  if (aux_out) NT_REQUIRE(counts && (T == 0 || (prob_partial && z_partial)), "combine: null aux input");
+  hipError_t err = launch_combine_aux(y, combine_dest, combine_w, T, d, k, shared_y, ld_shared,
+                                      out, ld_out, prob_partial, z_partial, counts, E, aux_coeff,
+                                      z_coeff, aux_out, reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "combine_aux");
+}
+
+}  // extern "C"

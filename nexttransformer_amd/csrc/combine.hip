@@ -1,0 +1,155 @@
+// Deterministic weighted combine (unpermute) and the auxiliary losses.
+//
+// Replaces result = zeros_like(rows).index_add(0, ids, output) + shared_experts(hidden)
+// (nexttransformer/scaling/megatron_moe.py:148-150) and RoutedFFN's shared-then-index_add
+// loop (reference_blocks.py:39-44). No atomics: one wave owns one output row and adds its k
+// expert rows in ascending expert order (combine_dest is stored in that order) into fp32,
+// starting from the shared expert row when there is one, and rounds to bf16 once.
+// All k source rows are loaded before the first add so k row reads are in flight at once.
+//
+// Aux losses (MCore TopKRouter "aux_loss" type and z-loss, megatron_moe.py:44-45) from the
+// router's per-block partials, reduced in block order in double precision:
+//   lb = aux_coeff * E / (k T^2) * sum_e S_e * counts[e],  S_e = sum_t s_te
+//   z  = z_coeff * (sum_t lse_t^2) / T
+#include "common.h"
+
+namespace ntmoe {
+namespace {
+
+// One wave per output row; the row is walked in column chunks of 64 lanes x VPC 16-byte
+// vectors (VPC = 2: 1024 bf16 per chunk) so k * VPC vectors are in flight per lane.
+constexpr int VPC = 2;
+
+__global__ __launch_bounds__(256) void combine_kernel(
+    const uint16_t* __restrict__ y, const int32_t* __restrict__ combine_dest,
+    const float* __restrict__ combine_w, int64_t T, int d, int k,
+    const uint16_t* __restrict__ shared_y, int64_t ld_shared, uint16_t* __restrict__ out,
+    int64_t ld_out) {
+  const int lane = lane_id();
+  const int vecs = d >> 3;
+  const int64_t waves = (int64_t)gridDim.x * 4;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + wave_id(); t < T; t += waves) {
+    int dest = 0;
+    float w = 0.f;
+    if (lane < k) {
+      dest = combine_dest[t * k + lane];
+      w = combine_w[t * k + lane];
+      const int64_t A = T * k;  // rows of y; out-of-range rows are clamped
+      dest = dest < 0 ? 0 : (dest >= A ? (int)(A - 1) : dest);
+    }
+    for (int v0 = 0; v0 < vecs; v0 += 64 * VPC) {
+      float acc[VPC][8];
+      if (shared_y) {
+        const u32x4* srow = reinterpret_cast<const u32x4*>(shared_y + t * ld_shared);
+#pragma unroll
+        for (int q = 0; q < VPC; ++q) {
+          int v = v0 + q * 64 + lane;
+          u32x4 r = v < vecs ? srow[v] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            acc[q][2 * i] = __builtin_bit_cast(float, r[i] << 16);
+            acc[q][2 * i + 1] = __builtin_bit_cast(float, r[i] & 0xffff0000u);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < VPC; ++q)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[q][i] = 0.f;
+      }
+      u32x4 rows[NT_MOE_MAX_TOPK][VPC];
+#pragma unroll
+      for (int j = 0; j < NT_MOE_MAX_TOPK; ++j) {
+        if (j < k) {
+          const u32x4* src = reinterpret_cast<const u32x4*>(y + (int64_t)__shfl(dest, j) * d);
+#pragma unroll
+          for (int q = 0; q < VPC; ++q) {
+            int v = v0 + q * 64 + lane;
+            rows[j][q] = v < vecs ? src[v] : u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NT_MOE_MAX_TOPK; ++j) {
+        if (j < k) {
+          const float wj = __shfl(w, j);
+#pragma unroll
+          for (int q = 0; q < VPC; ++q)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              acc[q][2 * i] = __builtin_fmaf(
+                  wj, __builtin_bit_cast(float, rows[j][q][i] << 16), acc[q][2 * i]);
+              acc[q][2 * i + 1] = __builtin_fmaf(
+                  wj, __builtin_bit_cast(float, rows[j][q][i] & 0xffff0000u), acc[q][2 * i + 1]);
+            }
+        }
+      }
+      u32x4* orow = reinterpret_cast<u32x4*>(out + t * ld_out);
+#pragma unroll
+      for (int q = 0; q < VPC; ++q) {
+        int v = v0 + q * 64 + lane;
+        if (v < vecs) {
+          u32x4 r;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) r[i] = pack_bf16x2(acc[q][2 * i], acc[q][2 * i + 1]);
+          orow[v] = r;
+        }
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void aux_kernel(const float* __restrict__ prob_partial,
+                                                  const float* __restrict__ z_partial, int nblk,
+                                                  const int32_t* __restrict__ counts, int E,
+                                                  int k, int64_t T, float aux_coeff,
+                                                  float z_coeff, float* __restrict__ aux_out) {
+  __shared__ double term[NT_MOE_MAX_EXPERTS];
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    double s = 0.0;
+    for (int b = 0; b < nblk; ++b) s += (double)prob_partial[(int64_t)b * E + e];
+    term[e] = s * (double)counts[e];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double sum = 0.0;
+    for (int e = 0; e < E; ++e) sum += term[e];
+    double zs = 0.0;
+    for (int b = 0; b < nblk; ++b) zs += (double)z_partial[b];
+    double Td = (double)T;
+    double lb = T > 0 ? (double)aux_coeff * E / ((double)k * Td * Td) * sum : 0.0;
+    double z = T > 0 ? (double)z_coeff * zs / Td : 0.0;
+    aux_out[0] = (float)(lb + z);
+    aux_out[1] = (float)lb;
+    aux_out[2] = (float)z;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_combine_aux(const uint16_t* y, const int32_t* combine_dest,
+                              const float* combine_w, int64_t T, int d, int k,
+                              const uint16_t* shared_y, int64_t ld_shared, uint16_t* out,
+                              int64_t ld_out, const float* prob_partial, const float* z_partial,
+                              const int32_t* counts, int E, float aux_coeff, float z_coeff,
+                              float* aux_out, hipStream_t stream) {
+  hipError_t err = hipSuccess;
+  if (T > 0) {
+    int64_t blocks = (T + 3) / 4;
+    int64_t cap = (int64_t)num_cus() * 32;
+    if (blocks > cap) blocks = cap;
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, y,
+                       combine_dest, combine_w, T, d, k, shared_y, ld_shared, out, ld_out);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  if (aux_out) {
+    const int nblk = ceil_div(T, kRouteBlock);
+    hipLaunchKernelGGL(aux_kernel, dim3(1), dim3(256), 0, stream, prob_partial, z_partial, nblk,
+                       counts, E, k, T, aux_coeff, z_coeff, aux_out);
+    err = hipGetLastError();
+  }
+  return err;
+}
+
+}  // namespace ntmoe

@@ -1,0 +1,87 @@
+// Shared definitions for the gfx950 MoE kernels and their C-ABI shim.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "nt_moe.h"
+
+namespace ntmoe {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+constexpr int kRouteBlock = NT_MOE_ROUTE_BLOCK;  // tokens per router / histogram block
+constexpr int kRouterChunk = 128;               // features per fixed-order partial sum
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __builtin_bit_cast(float, bits16 << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (gfx950 v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+
+// (va, ia) ranks before (vb, ib): larger logit, or equal logit and lower expert index.
+__device__ __forceinline__ bool rank_before(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+// Kernel launchers (one per translation unit). They assume validated arguments and return
+// a hipError_t from the launch.
+hipError_t launch_router(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
+                         int64_t T, int d, int E, int k, int score_fn, float* logits,
+                         int32_t* topk_ids, float* topk_w, float* prob_partial,
+                         float* z_partial, float* partials, bool split, hipStream_t stream);
+hipError_t launch_topk_from_logits(const float* logits, int64_t T, int E, int k,
+                                   int score_fn, int32_t* topk_ids, float* topk_w,
+                                   float* prob_partial, float* z_partial, hipStream_t stream);
+int router_split_chunks(int64_t T, int d, int E);
+
+hipError_t launch_histogram_scan(const int32_t* topk_ids, int64_t T, int k, int E,
+                                 int32_t* counts, int32_t* offsets, int32_t* ranks,
+                                 int32_t* block_counts, hipStream_t stream);
+hipError_t launch_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
+                          const float* topk_w, int64_t T, int d, int k, int E,
+                          const int32_t* ranks, const int32_t* block_base,
+                          int32_t* src_row, float* perm_w, int32_t* combine_dest,
+                          float* combine_w, uint16_t* x_perm, hipStream_t stream);
+
+hipError_t launch_grouped_ffn_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                   const int32_t* src_row,
+                                   const int32_t* seg_offsets, int num_segments,
+                                   int64_t total_rows, const uint16_t* w1, const uint16_t* w2,
+                                   int d, int H, int activation, uint16_t* h, uint16_t* y,
+                                   hipStream_t stream);
+
+hipError_t launch_combine_aux(const uint16_t* y, const int32_t* combine_dest,
+                              const float* combine_w, int64_t T, int d, int k,
+                              const uint16_t* shared_y, int64_t ld_shared, uint16_t* out,
+                              int64_t ld_out, const float* prob_partial, const float* z_partial,
+                              const int32_t* counts, int E, float aux_coeff, float z_coeff,
+                              float* aux_out, hipStream_t stream);
+
+int num_cus();
+
+// Lets `kernel` take `bytes` of dynamic LDS (gfx950: up to 160 KB per workgroup).
+hipError_t allow_dynamic_lds(const void* kernel, size_t bytes);
+
+}  // namespace ntmoe

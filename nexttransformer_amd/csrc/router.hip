@@ -1,0 +1,426 @@
+// Router: fp32 gating GEMM in a fixed reduction order, softmax / sigmoid scoring and
+// a wavefront-shuffle top-k, with per-block auxiliary-loss partials.
+//
+// Replaces NativeRouter.gating -> F.linear(x.float(), W.float())
+// (nexttransformer/scaling/megatron_moe.py:95-99) and TopKRouter's top-k followed by softmax
+// over the selected logits (megatron_moe.py:43; reference_blocks.py:37-38).
+//
+// Fixed order (bit-exact contract shared with oracle/router_ref.c):
+//   c_j   = fma chain over features [128 j, 128 j + 128) in ascending order, from 0.0f
+//   logit = ((c_0 + c_1) + c_2) + ...   then  + bias[e]
+// Ties in top-k: equal logits rank the lower expert index first.
+//
+// Work mapping. A block of 256 threads (4 waves) owns 64 tokens; lane = token. Wave w owns a
+// window of EPW consecutive experts, so its router weights are wave-uniform and come in
+// through scalar loads (w_router_t is [d, E], E contiguous); each lane keeps EPW fp32
+// accumulators. x is staged through LDS one 128-feature chunk at a time (coalesced global
+// loads, padded rows so per-lane row reads are conflict-free).
+// When T is small the fused grid cannot fill the chip: the split variant gives every
+// (token block, chunk, expert group) its own block, writes the chunk sums c_j to a
+// workspace, and the top-k kernel adds them in ascending j -- the same order.
+//
+// Top-k: logits go to an LDS tile [64][E+1]; 4 lanes share a token, each scans every 4th
+// expert into a sorted register list, then k rounds of an xor-shuffle butterfly over the 4
+// lanes emit the global order.
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "common.h"
+
+namespace ntmoe {
+namespace {
+
+constexpr int kXStride = kRouterChunk + 8;  // bf16 per padded LDS row (272 bytes)
+constexpr int kXTileBytes = kRouteBlock * kXStride * 2;
+
+__host__ __device__ inline int lg_tile_bytes(int E) { return kRouteBlock * (E + 1) * 4; }
+__host__ __device__ inline int zt_offset(int E) {
+  int lg = lg_tile_bytes(E);
+  return lg > kXTileBytes ? lg : kXTileBytes;
+}
+inline size_t router_lds_bytes(int E) { return zt_offset(E) + kRouteBlock * sizeof(float); }
+
+// acc[e] = fma chain over the clen features of the staged chunk (row of this lane's token).
+template <int EPW>
+__device__ __forceinline__ void chunk_fma(const uint16_t* xs_row, const float* __restrict__ wt,
+                                          int E, int ws, int c0, int clen, float* acc) {
+  for (int kk = 0; kk < clen; kk += 8) {
+    u32x4 raw = *reinterpret_cast<const u32x4*>(xs_row + kk);
+    float xf[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      xf[2 * i] = __builtin_bit_cast(float, raw[i] << 16);
+      xf[2 * i + 1] = __builtin_bit_cast(float, raw[i] & 0xffff0000u);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float* wrow = wt + (size_t)(c0 + kk + i) * E + ws;
+#pragma unroll
+      for (int e = 0; e < EPW; ++e) acc[e] = __builtin_fmaf(xf[i], wrow[e], acc[e]);
+    }
+  }
+}
+
+// Stage x[t0 .. t0+63][c0 .. c0+clen) into LDS (zeros beyond T).
+__device__ __forceinline__ void stage_x(const uint16_t* __restrict__ x, int64_t ld_x, int64_t T,
+                                        int64_t t0, int c0, int clen, uint16_t* xs) {
+  const int groups = clen >> 3;  // 16-byte groups per row
+  for (int g = threadIdx.x; g < kRouteBlock * 16; g += blockDim.x) {
+    int row = g >> 4, col = g & 15;
+    if (col >= groups) continue;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    int64_t t = t0 + row;
+    if (t < T) v = *reinterpret_cast<const u32x4*>(x + t * ld_x + c0 + col * 8);
+    *reinterpret_cast<u32x4*>(xs + row * kXStride + col * 8) = v;
+  }
+}
+
+template <int KMAX>
+__device__ __forceinline__ void list_insert(float v, int e, float* lv, int* li) {
+  if (!rank_before(v, e, lv[KMAX - 1], li[KMAX - 1])) return;
+  lv[KMAX - 1] = v;
+  li[KMAX - 1] = e;
+#pragma unroll
+  for (int j = KMAX - 1; j > 0; --j) {
+    if (rank_before(lv[j], li[j], lv[j - 1], li[j - 1])) {
+      float tv = lv[j]; lv[j] = lv[j - 1]; lv[j - 1] = tv;
+      int ti = li[j]; li[j] = li[j - 1]; li[j - 1] = ti;
+    }
+  }
+}
+
+// Top-k, weights, full scores and aux partials for the 64 tokens whose logits sit in the
+// LDS tile lg[64][E+1]; overwrites lg with the full scores s_te. Called by all 256 threads.
+template <int KMAX>
+__device__ void topk_and_scores(float* lg, float* zt, int64_t t0, int64_t T, int E, int k,
+                                int score_fn, int32_t* __restrict__ topk_ids,
+                                float* __restrict__ topk_w, float* __restrict__ prob_partial,
+                                float* __restrict__ z_partial) {
+  const int ldl = E + 1;
+  const int tt = threadIdx.x >> 2;  // token within the block
+  const int sub = threadIdx.x & 3;  // which quarter of the experts this lane scans
+  const int64_t t = t0 + tt;
+  float* row = lg + tt * ldl;
+
+  float lv[KMAX];
+  int li[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) { lv[j] = -INFINITY; li[j] = 0x7fffffff; }
+  for (int e = sub; e < E; e += 4) list_insert<KMAX>(row[e], e, lv, li);
+
+  // k rounds: best head of the 4 lists (xor butterfly), the owner pops it.
+  float ov[KMAX];
+  int oi[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    float bv = lv[0];
+    int bi = li[0];
+#pragma unroll
+    for (int m = 1; m <= 2; m <<= 1) {
+      float v2 = __shfl_xor(bv, m);
+      int i2 = __shfl_xor(bi, m);
+      if (rank_before(v2, i2, bv, bi)) { bv = v2; bi = i2; }
+    }
+    ov[j] = bv;
+    oi[j] = bi;
+    if (li[0] == bi) {
+#pragma unroll
+      for (int q = 0; q < KMAX - 1; ++q) { lv[q] = lv[q + 1]; li[q] = li[q + 1]; }
+      lv[KMAX - 1] = -INFINITY;
+      li[KMAX - 1] = 0x7fffffff;
+    }
+  }
+
+  // Routing weights over the k selected: softmax, or sigmoid normalised over the selected.
+  const float top = ov[0];
+  float wsum = 0.f, wv[KMAX];
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    float s = score_fn == NT_MOE_SCORE_SOFTMAX ? expf(ov[j] - top) : 1.f / (1.f + expf(-ov[j]));
+    wv[j] = j < k ? s : 0.f;
+    wsum += wv[j];
+  }
+  const float winv = 1.f / wsum;
+  if (t < T) {
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      if (j < k && (j & 3) == sub) {
+        topk_ids[t * k + j] = oi[j];
+        topk_w[t * k + j] = wv[j] * winv;
+      }
+    }
+  }
+
+  // Full scores s_te for the load-balance loss, logsumexp for the z-loss.
+  float part = 0.f, spart = 0.f;
+  for (int e = sub; e < E; e += 4) {
+    part += expf(row[e] - top);
+    if (score_fn == NT_MOE_SCORE_SIGMOID) spart += 1.f / (1.f + expf(-row[e]));
+  }
+  part += __shfl_xor(part, 1);
+  part += __shfl_xor(part, 2);
+  spart += __shfl_xor(spart, 1);
+  spart += __shfl_xor(spart, 2);
+  const float lse = top + logf(part);
+  if (score_fn == NT_MOE_SCORE_SOFTMAX) {
+    const float inv = 1.f / part;
+    for (int e = sub; e < E; e += 4) row[e] = expf(row[e] - top) * inv;
+  } else {
+    const float inv = 1.f / spart;
+    for (int e = sub; e < E; e += 4) row[e] = inv / (1.f + expf(-row[e]));
+  }
+  if (sub == 0) zt[tt] = lse * lse;
+  __syncthreads();
+
+  // Per-block column sums in token order (deterministic).
+  const int nvalid = (int)((T - t0) < kRouteBlock ? (T - t0) : kRouteBlock);
+  const int64_t blk = t0 / kRouteBlock;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    float s = 0.f;
+    for (int r = 0; r < nvalid; ++r) s += lg[r * ldl + e];
+    prob_partial[blk * E + e] = s;
+  }
+  if (threadIdx.x == 0) {
+    float s = 0.f;
+    for (int r = 0; r < nvalid; ++r) s += zt[r];
+    z_partial[blk] = s;
+  }
+}
+
+__device__ __forceinline__ void write_logits_out(const float* lg, int64_t t0, int64_t T, int E,
+                                                 float* __restrict__ logits) {
+  for (int idx = threadIdx.x; idx < kRouteBlock * E; idx += blockDim.x) {
+    int r = idx / E, e = idx - r * E;
+    if (t0 + r < T) logits[(t0 + r) * E + e] = lg[r * (E + 1) + e];
+  }
+}
+
+// Fused: all chunks and all experts for 64 tokens, then top-k in the same block.
+template <int EPW, int KMAX>
+__global__ __launch_bounds__(256) void router_fused_kernel(
+    const uint16_t* __restrict__ x, int64_t ld_x, const float* __restrict__ wt,
+    const float* __restrict__ bias, int64_t T, int d, int E, int k, int score_fn,
+    float* __restrict__ logits, int32_t* __restrict__ topk_ids, float* __restrict__ topk_w,
+    float* __restrict__ prob_partial, float* __restrict__ z_partial) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
+  float* lg = reinterpret_cast<float*>(smem);
+  float* zt = reinterpret_cast<float*>(smem + zt_offset(E));
+  const int64_t t0 = (int64_t)blockIdx.x * kRouteBlock;
+  const int lane = lane_id();
+  const int e0 = wave_id() * EPW;
+  const int ws = e0 < E - EPW ? e0 : E - EPW;  // window start kept inside [0, E)
+
+  float total[EPW];
+#pragma unroll
+  for (int e = 0; e < EPW; ++e) total[e] = 0.f;
+  for (int c0 = 0; c0 < d; c0 += kRouterChunk) {
+    const int clen = d - c0 < kRouterChunk ? d - c0 : kRouterChunk;
+    __syncthreads();
+    stage_x(x, ld_x, T, t0, c0, clen, xs);
+    __syncthreads();
+    float acc[EPW];
+#pragma unroll
+    for (int e = 0; e < EPW; ++e) acc[e] = 0.f;
+    chunk_fma<EPW>(xs + lane * kXStride, wt, E, ws, c0, clen, acc);
+#pragma unroll
+    for (int e = 0; e < EPW; ++e) total[e] = c0 == 0 ? acc[e] : total[e] + acc[e];
+  }
+  if (bias) {
+#pragma unroll
+    for (int e = 0; e < EPW; ++e) total[e] = total[e] + bias[ws + e];
+  }
+  __syncthreads();  // the x tile is dead; lg aliases it
+#pragma unroll
+  for (int i = 0; i < EPW; ++i) {
+    int e = ws + i;
+    if (e >= e0 && e < E) lg[lane * (E + 1) + e] = total[i];
+  }
+  __syncthreads();
+  if (logits) write_logits_out(lg, t0, T, E, logits);
+  topk_and_scores<KMAX>(lg, zt, t0, T, E, k, score_fn, topk_ids, topk_w, prob_partial,
+                        z_partial);
+}
+
+// Split: one chunk of one expert group for 64 tokens -> partials[chunk][t][e].
+template <int EPW>
+__global__ __launch_bounds__(256) void router_partial_kernel(
+    const uint16_t* __restrict__ x, int64_t ld_x, const float* __restrict__ wt, int64_t T, int d,
+    int E, float* __restrict__ partials) {
+  __shared__ __align__(16) uint16_t xs[kRouteBlock * kXStride];
+  const int64_t t0 = (int64_t)blockIdx.x * kRouteBlock;
+  const int c0 = blockIdx.y * kRouterChunk;
+  const int clen = d - c0 < kRouterChunk ? d - c0 : kRouterChunk;
+  const int lane = lane_id();
+  const int e0 = (blockIdx.z * 4 + wave_id()) * EPW;
+  const int ws = e0 < E - EPW ? e0 : E - EPW;
+  stage_x(x, ld_x, T, t0, c0, clen, xs);
+  __syncthreads();
+  float acc[EPW];
+#pragma unroll
+  for (int e = 0; e < EPW; ++e) acc[e] = 0.f;
+  chunk_fma<EPW>(xs + lane * kXStride, wt, E, ws, c0, clen, acc);
+  const int64_t t = t0 + lane;
+  if (t < T) {
+    float* out = partials + ((int64_t)blockIdx.y * T + t) * E;
+#pragma unroll
+    for (int i = 0; i < EPW; ++i) {
+      int e = ws + i;
+      if (e >= e0 && e < E) out[e] = acc[i];
+    }
+  }
+}
+
+// Sum nchunk partial planes in ascending order (+ bias), then top-k. With nchunk = 1 and no
+// bias this is top-k on caller-supplied logits.
+template <int KMAX>
+__global__ __launch_bounds__(256) void router_topk_kernel(
+    const float* __restrict__ partials, int nchunk, const float* __restrict__ bias, int64_t T,
+    int E, int k, int score_fn, float* __restrict__ logits, int32_t* __restrict__ topk_ids,
+    float* __restrict__ topk_w, float* __restrict__ prob_partial, float* __restrict__ z_partial) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* lg = reinterpret_cast<float*>(smem);
+  float* zt = reinterpret_cast<float*>(smem + zt_offset(E));
+  const int64_t t0 = (int64_t)blockIdx.x * kRouteBlock;
+  for (int idx = threadIdx.x; idx < kRouteBlock * E; idx += blockDim.x) {
+    int r = idx / E, e = idx - r * E;
+    int64_t t = t0 + r;
+    float v = 0.f;
+    if (t < T) {
+      v = partials[t * E + e];
+      for (int c = 1; c < nchunk; ++c) v = v + partials[((int64_t)c * T + t) * E + e];
+      if (bias) v = v + bias[e];
+      if (logits) logits[t * E + e] = v;
+    }
+    lg[r * (E + 1) + e] = v;
+  }
+  __syncthreads();
+  topk_and_scores<KMAX>(lg, zt, t0, T, E, k, score_fn, topk_ids, topk_w, prob_partial,
+                        z_partial);
+}
+
+int experts_per_wave(int E) {
+  int need = (E + 3) / 4, epw = 1;
+  while (epw < need) epw <<= 1;
+  return epw;
+}
+
+int kmax_for(int k) { return k <= 2 ? 2 : (k <= 4 ? 4 : 8); }
+
+// NT_MOE_ROUTER_MODE=fused|split overrides the size heuristic (for tuning runs).
+int router_mode_override() {
+  static int mode = [] {
+    const char* s = getenv("NT_MOE_ROUTER_MODE");
+    if (!s) return 0;
+    if (!strcmp(s, "fused")) return 1;
+    if (!strcmp(s, "split")) return 2;
+    return 0;
+  }();
+  return mode;
+}
+
+template <int KMAX>
+hipError_t launch_topk_k(const float* partials, int nchunk, const float* bias, int64_t T, int E,
+                         int k, int score_fn, float* logits, int32_t* ids, float* w, float* pp,
+                         float* zp, hipStream_t stream) {
+  dim3 grid(ceil_div(T, kRouteBlock));
+  hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(router_topk_kernel<KMAX>),
+                                     router_lds_bytes(E));
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL((router_topk_kernel<KMAX>), grid, dim3(256), router_lds_bytes(E), stream,
+                     partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp);
+  return hipGetLastError();
+}
+
+hipError_t launch_topk_any(const float* partials, int nchunk, const float* bias, int64_t T,
+                           int E, int k, int score_fn, float* logits, int32_t* ids, float* w,
+                           float* pp, float* zp, hipStream_t stream) {
+  switch (kmax_for(k)) {
+    case 2: return launch_topk_k<2>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    case 4: return launch_topk_k<4>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    default: return launch_topk_k<8>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
+  }
+}
+
+template <int EPW, int KMAX>
+hipError_t launch_fused_k(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
+                          int64_t T, int d, int E, int k, int score_fn, float* logits,
+                          int32_t* ids, float* w, float* pp, float* zp, hipStream_t stream) {
+  dim3 grid(ceil_div(T, kRouteBlock));
+  hipError_t err = allow_dynamic_lds(
+      reinterpret_cast<const void*>(router_fused_kernel<EPW, KMAX>), router_lds_bytes(E));
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL((router_fused_kernel<EPW, KMAX>), grid, dim3(256), router_lds_bytes(E),
+                     stream, x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp);
+  return hipGetLastError();
+}
+
+template <int EPW>
+hipError_t launch_fused_e(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
+                          int64_t T, int d, int E, int k, int score_fn, float* logits,
+                          int32_t* ids, float* w, float* pp, float* zp, hipStream_t stream) {
+  switch (kmax_for(k)) {
+    case 2: return launch_fused_k<EPW, 2>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    case 4: return launch_fused_k<EPW, 4>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    default: return launch_fused_k<EPW, 8>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
+  }
+}
+
+template <int EPW>
+hipError_t launch_partial_e(const uint16_t* x, int64_t ld_x, const float* wt, int64_t T, int d,
+                            int E, float* partials, hipStream_t stream) {
+  dim3 grid(ceil_div(T, kRouteBlock), ceil_div(d, kRouterChunk), ceil_div(E, 4 * EPW));
+  hipLaunchKernelGGL((router_partial_kernel<EPW>), grid, dim3(256), 0, stream, x, ld_x, wt, T,
+                     d, E, partials);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// Chunks of the split variant when it is used for this shape, else 0 (fused).
+int router_split_chunks(int64_t T, int d, int E) {
+  (void)E;
+  int mode = router_mode_override();
+  if (mode == 1) return 0;
+  int blocks = ceil_div(T, kRouteBlock);
+  if (mode == 2 || blocks < 2 * num_cus()) return ceil_div(d, kRouterChunk);
+  return 0;
+}
+
+hipError_t launch_router(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
+                         int64_t T, int d, int E, int k, int score_fn, float* logits,
+                         int32_t* topk_ids, float* topk_w, float* prob_partial,
+                         float* z_partial, float* partials, bool split, hipStream_t stream) {
+  int epw = experts_per_wave(E);
+  if (!split) {
+    switch (epw) {
+#define NT_FUSED(N) case N: return launch_fused_e<N>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, topk_ids, topk_w, prob_partial, z_partial, stream);
+      NT_FUSED(1) NT_FUSED(2) NT_FUSED(4) NT_FUSED(8) NT_FUSED(16) NT_FUSED(32) NT_FUSED(64)
+#undef NT_FUSED
+      default: return hipErrorInvalidValue;
+    }
+  }
+  // Split: smaller expert groups give more blocks when T is small.
+  int epw_split = epw < 16 ? epw : 16;
+  hipError_t err;
+  switch (epw_split) {
+    case 1: err = launch_partial_e<1>(x, ld_x, wt, T, d, E, partials, stream); break;
+    case 2: err = launch_partial_e<2>(x, ld_x, wt, T, d, E, partials, stream); break;
+    case 4: err = launch_partial_e<4>(x, ld_x, wt, T, d, E, partials, stream); break;
+    case 8: err = launch_partial_e<8>(x, ld_x, wt, T, d, E, partials, stream); break;
+    default: err = launch_partial_e<16>(x, ld_x, wt, T, d, E, partials, stream); break;
+  }
+  if (err != hipSuccess) return err;
+  return launch_topk_any(partials, ceil_div(d, kRouterChunk), bias, T, E, k, score_fn, logits,
+                         topk_ids, topk_w, prob_partial, z_partial, stream);
+}
+
+hipError_t launch_topk_from_logits(const float* logits, int64_t T, int E, int k,
+                                   int score_fn, int32_t* topk_ids, float* topk_w,
+                                   float* prob_partial, float* z_partial, hipStream_t stream) {
+  return launch_topk_any(logits, 1, nullptr, T, E, k, score_fn, nullptr, topk_ids, topk_w,
+                         prob_partial, z_partial, stream);
+}
+
+}  // namespace ntmoe

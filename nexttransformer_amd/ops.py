@@ -1,0 +1,273 @@
+"""torch.library custom ops ("ntmoe::*") over the C ABI of libnt_moe.so.
+
+Each op checks devices, dtypes and shapes (ValueError, as the reference's config checks do,
+nexttransformer/scaling/moe_recipe.py:54-72), allocates its outputs with torch's caching
+allocator, and enqueues the HIP kernels on the current stream. Status codes from the library
+become ValueError (bad arguments) or RuntimeError (launch failures). There is no CPU path: a
+CPU tensor is a ValueError and a missing library raises NativeLibraryMissing.
+"""
+import ctypes
+from typing import Optional
+
+import torch
+from torch import Tensor
+
+from nexttransformer_amd import _native as nat
+from nexttransformer_amd._native import ptr
+
+
+def _stream(device):
+    """The current HIP stream of `device` as a raw handle."""
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require(cond, message):
+    if not cond:
+        raise ValueError(message)
+
+
+def _on_gpu(*tensors):
+    for t in tensors:
+        if t is not None:
+            _require(t.is_cuda, f"ntmoe ops run on the GPU only; got a {t.device} tensor")
+
+
+def _nblk(T):
+    return (T + nat.ROUTE_BLOCK - 1) // nat.ROUTE_BLOCK
+
+
+# ---------------------------------------------------------------------------------------------
+# router
+
+@torch.library.custom_op("ntmoe::router", mutates_args=())
+def router(x: Tensor, w_router_t: Tensor, bias: Optional[Tensor], k: int, score_fn: int,
+           want_logits: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(logits [T,E] or empty, ids [T,k] int32, weights [T,k], prob_partial, z_partial)."""
+    _on_gpu(x, w_router_t, bias)
+    _require(x.dtype == torch.bfloat16 and x.dim() == 2, "router: x must be bf16 [T, d]")
+    _require(x.stride(1) == 1, "router: x rows must be contiguous")
+    _require(w_router_t.dtype == torch.float32 and w_router_t.is_contiguous(),
+             "router: w_router_t must be contiguous fp32 [d, E]")
+    T, d = x.shape
+    _require(w_router_t.shape[0] == d, "router: w_router_t must be [d, E]")
+    E = w_router_t.shape[1]
+    if bias is not None:
+        _require(bias.dtype == torch.float32 and bias.shape == (E,) and bias.is_contiguous(),
+                 "router: bias must be contiguous fp32 [E]")
+    dev = x.device
+    logits = torch.empty((T, E) if want_logits else (0,), device=dev, dtype=torch.float32)
+    ids = torch.empty(T, k, device=dev, dtype=torch.int32)
+    w = torch.empty(T, k, device=dev, dtype=torch.float32)
+    pp = torch.empty(_nblk(T), E, device=dev, dtype=torch.float32)
+    zp = torch.empty(_nblk(T), device=dev, dtype=torch.float32)
+    lib = nat.load()
+    ws_bytes = lib.nt_moe_router_workspace_bytes(T, d, E, k)
+    ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    st = lib.nt_moe_router_fwd(ptr(x), x.stride(0), ptr(w_router_t), ptr(bias), T, d, E, k,
+                               score_fn, ptr(logits) if want_logits else None, ptr(ids), ptr(w),
+                               ptr(pp), ptr(zp), ptr(ws), ws_bytes, _stream(dev))
+    nat.check(st, "ntmoe::router")
+    return logits, ids, w, pp, zp
+
+
+@router.register_fake
+def _(x, w_router_t, bias, k, score_fn, want_logits):
+    T, E = x.shape[0], w_router_t.shape[1]
+    f = x.new_empty
+    return (f((T, E) if want_logits else (0,), dtype=torch.float32),
+            f((T, k), dtype=torch.int32), f((T, k), dtype=torch.float32),
+            f((_nblk(T), E), dtype=torch.float32), f((_nblk(T),), dtype=torch.float32))
+
+
+@torch.library.custom_op("ntmoe::topk_from_logits", mutates_args=())
+def topk_from_logits(logits: Tensor, k: int, score_fn: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Top-k / weights / aux partials from given fp32 logits [T, E]."""
+    _on_gpu(logits)
+    _require(logits.dtype == torch.float32 and logits.dim() == 2 and logits.is_contiguous(),
+             "topk_from_logits: logits must be contiguous fp32 [T, E]")
+    T, E = logits.shape
+    dev = logits.device
+    ids = torch.empty(T, k, device=dev, dtype=torch.int32)
+    w = torch.empty(T, k, device=dev, dtype=torch.float32)
+    pp = torch.empty(_nblk(T), E, device=dev, dtype=torch.float32)
+    zp = torch.empty(_nblk(T), device=dev, dtype=torch.float32)
+    st = nat.load().nt_moe_topk_from_logits(ptr(logits), T, E, k, score_fn, ptr(ids), ptr(w),
+                                            ptr(pp), ptr(zp), _stream(dev))
+    nat.check(st, "ntmoe::topk_from_logits")
+    return ids, w, pp, zp
+
+
+@topk_from_logits.register_fake
+def _(logits, k, score_fn):
+    T, E = logits.shape
+    f = logits.new_empty
+    return (f((T, k), dtype=torch.int32), f((T, k), dtype=torch.float32),
+            f((_nblk(T), E), dtype=torch.float32), f((_nblk(T),), dtype=torch.float32))
+
+
+# ---------------------------------------------------------------------------------------------
+# route plan: histogram + scan + permute
+
+@torch.library.custom_op("ntmoe::route_plan", mutates_args=())
+def route_plan(ids: Tensor, weights: Tensor, num_experts: int, x: Optional[Tensor],
+               want_x_perm: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(counts [E], offsets [E+1], src_row [A], perm_w [A], combine_dest [T,k], combine_w [T,k],
+    x_perm [A,d] or empty), A = T*k, in the order of mapping.T.nonzero()."""
+    _on_gpu(ids, weights, x)
+    _require(ids.dtype == torch.int32 and ids.dim() == 2 and ids.is_contiguous(),
+             "route_plan: ids must be contiguous int32 [T, k]")
+    _require(weights.dtype == torch.float32 and weights.shape == ids.shape and weights.is_contiguous(),
+             "route_plan: weights must be contiguous fp32 [T, k]")
+    T, k = ids.shape
+    E = num_experts
+    A = T * k
+    dev = ids.device
+    if want_x_perm:
+        _require(x is not None and x.dtype == torch.bfloat16 and x.dim() == 2 and x.shape[0] == T
+                 and x.stride(1) == 1, "route_plan: x must be bf16 [T, d] with contiguous rows")
+    d = x.shape[1] if x is not None else 0
+    counts = torch.empty(E, device=dev, dtype=torch.int32)
+    offsets = torch.empty(E + 1, device=dev, dtype=torch.int32)
+    src = torch.empty(A, device=dev, dtype=torch.int32)
+    perm_w = torch.empty(A, device=dev, dtype=torch.float32)
+    cdest = torch.empty(T, k, device=dev, dtype=torch.int32)
+    cw = torch.empty(T, k, device=dev, dtype=torch.float32)
+    x_perm = torch.empty((A, d) if want_x_perm else (0,), device=dev, dtype=torch.bfloat16)
+    lib = nat.load()
+    ws_bytes = lib.nt_moe_route_workspace_bytes(T, k, E)
+    ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    stream = _stream(dev)
+    nat.check(lib.nt_moe_histogram_scan(ptr(ids), T, k, E, ptr(counts), ptr(offsets), ptr(ws),
+                                        ws_bytes, stream), "ntmoe::route_plan histogram")
+    nat.check(lib.nt_moe_permute(ptr(x) if want_x_perm else None,
+                                 x.stride(0) if want_x_perm else 0, ptr(ids), ptr(weights), T, d,
+                                 k, E, ptr(ws), ws_bytes, ptr(src), ptr(perm_w), ptr(cdest),
+                                 ptr(cw), ptr(x_perm) if want_x_perm else None, stream),
+              "ntmoe::route_plan permute")
+    return counts, offsets, src, perm_w, cdest, cw, x_perm
+
+
+@route_plan.register_fake
+def _(ids, weights, num_experts, x, want_x_perm):
+    T, k = ids.shape
+    A = T * k
+    d = x.shape[1] if x is not None else 0
+    f = ids.new_empty
+    return (f((num_experts,), dtype=torch.int32), f((num_experts + 1,), dtype=torch.int32),
+            f((A,), dtype=torch.int32), f((A,), dtype=torch.float32), f((T, k), dtype=torch.int32),
+            f((T, k), dtype=torch.float32),
+            f((A, d) if want_x_perm else (0,), dtype=torch.bfloat16))
+
+
+# ---------------------------------------------------------------------------------------------
+# grouped expert FFN
+
+@torch.library.custom_op("ntmoe::grouped_ffn", mutates_args=())
+def grouped_ffn(a: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor, w1: Tensor,
+                w2: Tensor, activation: int, total_rows: int) -> tuple[Tensor, Tensor]:
+    """(h [rows, H], y [rows, d]) for ragged segments; rows read a[src_row[r]] if given."""
+    _on_gpu(a, src_row, seg_offsets, w1, w2)
+    _require(a.dtype == torch.bfloat16 and a.dim() == 2 and a.stride(1) == 1,
+             "grouped_ffn: a must be bf16 [*, d] with contiguous rows")
+    _require(w1.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16 and w1.dim() == 3
+             and w2.dim() == 3 and w1.is_contiguous() and w2.is_contiguous(),
+             "grouped_ffn: w1 [S, F, d] and w2 [S, d, H] must be contiguous bf16")
+    S, _, d = w1.shape
+    H = w2.shape[2]
+    F = 2 * H if activation == nat.ACT_SWIGLU else H
+    _require(w1.shape == (S, F, d) and w2.shape == (S, d, H) and a.shape[1] == d,
+             f"grouped_ffn: expected w1 [S,{F},{d}], w2 [S,{d},{H}], a [*, {d}]")
+    _require(seg_offsets.dtype == torch.int32 and seg_offsets.shape == (S + 1,)
+             and seg_offsets.is_contiguous(), "grouped_ffn: seg_offsets must be int32 [S+1]")
+    if src_row is not None:
+        _require(src_row.dtype == torch.int32 and src_row.is_contiguous(),
+                 "grouped_ffn: src_row must be contiguous int32")
+    dev = a.device
+    h = torch.empty(total_rows, H, device=dev, dtype=torch.bfloat16)
+    y = torch.empty(total_rows, d, device=dev, dtype=torch.bfloat16)
+    st = nat.load().nt_moe_grouped_ffn_bf16(ptr(a), a.stride(0), a.shape[0], ptr(src_row),
+                                            ptr(seg_offsets),
+                                            S, total_rows, ptr(w1), ptr(w2), d, H, activation,
+                                            ptr(h), ptr(y), _stream(dev))
+    nat.check(st, "ntmoe::grouped_ffn")
+    return h, y
+
+
+@grouped_ffn.register_fake
+def _(a, src_row, seg_offsets, w1, w2, activation, total_rows):
+    H, d = w2.shape[2], w1.shape[2]
+    return (a.new_empty((total_rows, H)), a.new_empty((total_rows, d)))
+
+
+# ---------------------------------------------------------------------------------------------
+# combine + aux
+
+@torch.library.custom_op("ntmoe::combine_aux", mutates_args=())
+def combine_aux(y: Tensor, combine_dest: Tensor, combine_w: Tensor, shared_y: Optional[Tensor],
+                prob_partial: Tensor, z_partial: Tensor, counts: Tensor, aux_coeff: float,
+                z_coeff: float) -> tuple[Tensor, Tensor]:
+    """(out [T, d] bf16, aux fp32 [3] = {lb + z, lb, z})."""
+    _on_gpu(y, combine_dest, combine_w, shared_y, prob_partial, z_partial, counts)
+    _require(y.dtype == torch.bfloat16 and y.dim() == 2 and y.is_contiguous(),
+             "combine_aux: y must be contiguous bf16 [A, d]")
+    T, k = combine_dest.shape
+    d = y.shape[1]
+    E = counts.shape[0]
+    _require(combine_dest.dtype == torch.int32 and combine_dest.is_contiguous()
+             and combine_w.dtype == torch.float32 and combine_w.shape == (T, k)
+             and combine_w.is_contiguous(), "combine_aux: bad combine_dest / combine_w")
+    _require(counts.dtype == torch.int32 and prob_partial.shape == (_nblk(T), E)
+             and z_partial.shape == (_nblk(T),), "combine_aux: bad aux partials")
+    if shared_y is not None:
+        _require(shared_y.dtype == torch.bfloat16 and shared_y.shape == (T, d)
+                 and shared_y.stride(1) == 1, "combine_aux: shared_y must be bf16 [T, d]")
+    dev = y.device
+    out = torch.empty(T, d, device=dev, dtype=torch.bfloat16)
+    aux = torch.empty(3, device=dev, dtype=torch.float32)
+    st = nat.load().nt_moe_combine_aux(
+        ptr(y), ptr(combine_dest), ptr(combine_w), T, d, k, ptr(shared_y),
+        shared_y.stride(0) if shared_y is not None else 0, ptr(out), out.stride(0),
+        ptr(prob_partial), ptr(z_partial), ptr(counts), E, float(aux_coeff), float(z_coeff),
+        ptr(aux), _stream(dev))
+    nat.check(st, "ntmoe::combine_aux")
+    return out, aux
+
+
+@combine_aux.register_fake
+def _(y, combine_dest, combine_w, shared_y, prob_partial, z_partial, counts, aux_coeff, z_coeff):
+    T = combine_dest.shape[0]
+    return y.new_empty((T, y.shape[1])), y.new_empty((3,), dtype=torch.float32)
+
+
+# ---------------------------------------------------------------------------------------------
+# the whole layer
+
+def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
+                activation=nat.ACT_SWIGLU, aux_coeff=0.01, z_coeff=0.001, logit_bias=None,
+                shared_w1=None, shared_w2=None, want_logits=False, permute_rows=False):
+    """The MoE layer forward on the GPU: router -> route plan -> grouped FFN -> combine + aux.
+
+    x bf16 [T, d]; w_router_t fp32 [d, E]; w1 bf16 [E, F, d]; w2 bf16 [E, d, H]; optional
+    shared expert shared_w1 [1, Fs, d], shared_w2 [1, d, Hs]. Returns (out [T, d] bf16,
+    aux fp32 [3], state) where state holds the routing tensors. With permute_rows the token rows
+    are moved into expert order by the permute kernel first (x_perm), otherwise the grouped
+    FFN gathers them directly.
+    """
+    T = x.shape[0]
+    E = w_router_t.shape[1]
+    logits, ids, w, pp, zp = router(x, w_router_t, logit_bias, top_k, score_fn, want_logits)
+    counts, offsets, src, perm_w, cdest, cw, x_perm = route_plan(ids, w, E, x if permute_rows else None,
+                                                                 permute_rows)
+    A = T * top_k
+    if permute_rows:
+        _, y = grouped_ffn(x_perm, None, offsets, w1, w2, activation, A)
+    else:
+        _, y = grouped_ffn(x, src, offsets, w1, w2, activation, A)
+    shared_y = None
+    if shared_w1 is not None:
+        seg = torch.tensor([0, T], device=x.device, dtype=torch.int32)
+        _, shared_y = grouped_ffn(x, None, seg, shared_w1, shared_w2, activation, T)
+    out, aux = combine_aux(y, cdest, cw, shared_y, pp, zp, counts, aux_coeff, z_coeff)
+    state = dict(logits=logits, ids=ids, weights=w, counts=counts, offsets=offsets, src_row=src,
+                 perm_w=perm_w, combine_dest=cdest, combine_w=cw)
+    return out, aux, state
