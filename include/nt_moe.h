@@ -51,10 +51,15 @@ extern "C" {
 #define NT_MOE_ACT_SWIGLU 0 /* fc1 rows [0,H) are the gate, [H,2H) the value: silu(g) * u */
 #define NT_MOE_ACT_RELU2 1  /* fc1 has H rows: relu(g)^2 (megatron_moe.py:23-24) */
 
+/* epilogue values of nt_moe_grouped_gemm_bf16. */
+#define NT_MOE_EPI_SWIGLU 0 /* w has 2 n_out rows: c = silu(a.w[j]) * a.w[n_out + j] */
+#define NT_MOE_EPI_RELU2 1  /* c = relu(a.w[j])^2 */
+#define NT_MOE_EPI_NONE 2   /* c = a.w[j] */
+
 /* Largest supported sizes. */
 #define NT_MOE_MAX_EXPERTS 256
 #define NT_MOE_MAX_TOPK 8
-#define NT_MOE_MAX_SEGMENTS 1024
+#define NT_MOE_MAX_SEGMENTS 512
 /* Tokens per router / histogram block: aux partial buffers have ceil(T / 64) rows. */
 #define NT_MOE_ROUTE_BLOCK 64
 
@@ -143,13 +148,32 @@ int nt_moe_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
  *   h            bf16 [total_rows, H] (intermediate, caller-owned)
  *   y            bf16 [total_rows, d]
  *   total_rows   upper bound of seg_offsets[num_segments] used to size the launch
- * Requirements: d % 64 == 0, H % 64 == 0, 16-byte aligned buffers.
+ *   workspace    nt_moe_grouped_gemm_workspace_bytes() bytes of device memory (tile claim
+ *                counters, reset by the call itself); calls that share one workspace must be
+ *                ordered on one stream
+ * Requirements: d % 64 == 0, H % 64 == 0, 16-byte aligned buffers, a_rows * ld_a * 2 and one
+ * segment's weights each within 4 GiB.
  */
+size_t nt_moe_grouped_gemm_workspace_bytes(void);
 int nt_moe_grouped_ffn_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows, const int32_t* src_row,
                             const int32_t* seg_offsets, int32_t num_segments,
                             int64_t total_rows, const uint16_t* w1, const uint16_t* w2,
                             int32_t d, int32_t H, int32_t activation, uint16_t* h,
-                            uint16_t* y, nt_moe_stream_t stream);
+                            uint16_t* y, void* workspace, size_t workspace_bytes,
+                            nt_moe_stream_t stream);
+
+/*
+ * One grouped GEMM launch over ragged segments (the building block of nt_moe_grouped_ffn_bf16):
+ *   c[r, j] = epilogue(a_r . w_s[j, :])  for r in segment s, j in [0, n_out)
+ *   w  bf16 [num_segments, 2 n_out (SWIGLU) or n_out, K];  c bf16 [total_rows, n_out]
+ * Requirements: K % 64 == 0, n_out % 4 == 0 (n_out % 64 == 0 for SWIGLU), 16-byte alignment;
+ * workspace as for nt_moe_grouped_ffn_bf16.
+ */
+int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                             const int32_t* src_row, const int32_t* seg_offsets,
+                             int32_t num_segments, int64_t total_rows, const uint16_t* w,
+                             int32_t K, int32_t n_out, int32_t epilogue, uint16_t* c,
+                             void* workspace, size_t workspace_bytes, nt_moe_stream_t stream);
 
 /*
  * Deterministic weighted combine plus the load-balance and z auxiliary losses.

@@ -16,7 +16,8 @@ ABI_VERSION = 1
 
 SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
 ACT_SWIGLU, ACT_RELU2 = 0, 1
-MAX_EXPERTS, MAX_TOPK, MAX_SEGMENTS, ROUTE_BLOCK = 256, 8, 1024, 64
+EPI_SWIGLU, EPI_RELU2, EPI_NONE = 0, 1, 2
+MAX_EXPERTS, MAX_TOPK, MAX_SEGMENTS, ROUTE_BLOCK = 256, 8, 512, 64
 
 _p, _i64, _i32, _f32, _sz = (ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float,
                              ctypes.c_size_t)
@@ -33,8 +34,11 @@ SIGNATURES = {
     "nt_moe_histogram_scan": (_i32, [_p, _i64, _i32, _i32, _p, _p, _p, _sz, _p]),
     "nt_moe_permute": (_i32, [_p, _i64, _p, _p, _i64, _i32, _i32, _i32, _p, _sz, _p, _p, _p, _p,
                               _p, _p]),
+    "nt_moe_grouped_gemm_workspace_bytes": (_sz, []),
     "nt_moe_grouped_ffn_bf16": (_i32, [_p, _i64, _i64, _p, _p, _i32, _i64, _p, _p, _i32, _i32,
-                                       _i32, _p, _p, _p]),
+                                       _i32, _p, _p, _p, _sz, _p]),
+    "nt_moe_grouped_gemm_bf16": (_i32, [_p, _i64, _i64, _p, _p, _i32, _i64, _p, _i32, _i32, _i32,
+                                        _p, _p, _sz, _p]),
     "nt_moe_combine_aux": (_i32, [_p, _p, _p, _i64, _i32, _i32, _p, _i64, _p, _i64, _p, _p, _p,
                                   _i32, _f32, _f32, _p, _p]),
 }

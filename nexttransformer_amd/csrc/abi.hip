@@ -74,6 +74,16 @@ int check_route_shape(int64_t T, int k, int E) {
   return NT_MOE_OK;
 }
 
+// The grouped GEMM addresses its operands with 32-bit byte offsets per lane.
+int check_gemm_extent(int64_t a_rows, int64_t ld_a, int64_t w_rows_per_segment, int64_t K) {
+  NT_REQUIRE(a_rows * ld_a * 2 <= ((int64_t)1 << 32),
+             "grouped GEMM: a spans %lld bytes, more than the 4 GiB the loader addresses",
+             (long long)(a_rows * ld_a * 2));
+  NT_REQUIRE(w_rows_per_segment * K * 2 <= ((int64_t)1 << 32),
+             "grouped GEMM: one segment's weights exceed 4 GiB");
+  return NT_MOE_OK;
+}
+
 }  // namespace
 
 int num_cus() {
@@ -198,11 +208,14 @@ int nt_moe_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
   return launched(err, "permute");
 }
 
+size_t nt_moe_grouped_gemm_workspace_bytes(void) { return kGemmWorkspaceBytes; }
+
 int nt_moe_grouped_ffn_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows, const int32_t* src_row,
                             const int32_t* seg_offsets, int32_t num_segments,
                             int64_t total_rows, const uint16_t* w1, const uint16_t* w2,
                             int32_t d, int32_t H, int32_t activation, uint16_t* h,
-                            uint16_t* y, nt_moe_stream_t stream) {
+                            uint16_t* y, void* workspace, size_t workspace_bytes,
+                            nt_moe_stream_t stream) {
   NT_REQUIRE(d > 0 && d % 64 == 0, "grouped_ffn: d must be a positive multiple of 64, got %d", d);
   NT_REQUIRE(H > 0 && H % 64 == 0, "grouped_ffn: H must be a positive multiple of 64, got %d", H);
   NT_REQUIRE(num_segments >= 1 && num_segments <= NT_MOE_MAX_SEGMENTS,
@@ -216,11 +229,52 @@ int nt_moe_grouped_ffn_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows, con
   NT_REQUIRE(a && seg_offsets && w1 && w2 && h && y, "grouped_ffn: null buffer");
   NT_REQUIRE(aligned16(a) && aligned16(w1) && aligned16(w2) && aligned16(h) && aligned16(y),
              "grouped_ffn: buffers must be 16-byte aligned");
+  int rc = check_gemm_extent(a_rows, ld_a, (int64_t)2 * H, d);
+  if (rc) return rc;
+  rc = check_gemm_extent(total_rows, H, d, H);
+  if (rc) return rc;
+  if (!workspace || workspace_bytes < kGemmWorkspaceBytes)
+    return fail(NT_MOE_ENOSPC, "grouped_ffn: workspace %zu < %zu bytes", workspace_bytes,
+                kGemmWorkspaceBytes);
   if (total_rows == 0) return ok();
   hipError_t err = launch_grouped_ffn_bf16(a, ld_a, a_rows, src_row, seg_offsets, num_segments,
                                            total_rows, w1, w2, d, H, activation, h, y,
+                                           reinterpret_cast<int*>(workspace),
                                            reinterpret_cast<hipStream_t>(stream));
   return launched(err, "grouped_ffn_bf16");
+}
+
+int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                             const int32_t* src_row, const int32_t* seg_offsets,
+                             int32_t num_segments, int64_t total_rows, const uint16_t* w,
+                             int32_t K, int32_t n_out, int32_t epilogue, uint16_t* c,
+                             void* workspace, size_t workspace_bytes, nt_moe_stream_t stream) {
+  NT_REQUIRE(K > 0 && K % 64 == 0, "grouped_gemm: K must be a positive multiple of 64, got %d", K);
+  NT_REQUIRE(epilogue == NT_MOE_EPI_SWIGLU || epilogue == NT_MOE_EPI_RELU2 ||
+                 epilogue == NT_MOE_EPI_NONE, "grouped_gemm: unknown epilogue %d", epilogue);
+  NT_REQUIRE(n_out > 0 && n_out % (epilogue == NT_MOE_EPI_SWIGLU ? 64 : 4) == 0,
+             "grouped_gemm: n_out must be a positive multiple of %d, got %d",
+             epilogue == NT_MOE_EPI_SWIGLU ? 64 : 4, n_out);
+  NT_REQUIRE(num_segments >= 1 && num_segments <= NT_MOE_MAX_SEGMENTS,
+             "grouped_gemm: num_segments must be in [1, %d]", NT_MOE_MAX_SEGMENTS);
+  NT_REQUIRE(total_rows >= 0 && total_rows < ((int64_t)1 << 31), "grouped_gemm: bad total_rows");
+  NT_REQUIRE(ld_a >= K && ld_a % 8 == 0, "grouped_gemm: ld_a must be >= K and a multiple of 8");
+  NT_REQUIRE(a_rows >= 1, "grouped_gemm: a_rows must be positive");
+  NT_REQUIRE(src_row || a_rows >= total_rows, "grouped_gemm: a needs total_rows rows without src_row");
+  NT_REQUIRE(a && seg_offsets && w && c, "grouped_gemm: null buffer");
+  NT_REQUIRE(aligned16(a) && aligned16(w) && aligned16(c), "grouped_gemm: buffers must be 16-byte aligned");
+  int rc = check_gemm_extent(a_rows, ld_a,
+                             epilogue == NT_MOE_EPI_SWIGLU ? (int64_t)2 * n_out : n_out, K);
+  if (rc) return rc;
+  if (!workspace || workspace_bytes < kGemmWorkspaceBytes)
+    return fail(NT_MOE_ENOSPC, "grouped_gemm: workspace %zu < %zu bytes", workspace_bytes,
+                kGemmWorkspaceBytes);
+  if (total_rows == 0) return ok();
+  hipError_t err = launch_grouped_gemm_bf16(a, ld_a, a_rows, src_row, seg_offsets, num_segments,
+                                            total_rows, w, K, n_out, epilogue, c,
+                                            reinterpret_cast<int*>(workspace),
+                                            reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "grouped_gemm_bf16");
 }
 
 int nt_moe_combine_aux(const uint16_t* y, const int32_t* combine_dest, const float* combine_w,

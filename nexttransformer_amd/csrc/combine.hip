@@ -99,29 +99,52 @@ __global__ __launch_bounds__(256) void combine_kernel(
   }
 }
 
-__global__ __launch_bounds__(256) void aux_kernel(const float* __restrict__ prob_partial,
-                                                  const float* __restrict__ z_partial, int nblk,
-                                                  const int32_t* __restrict__ counts, int E,
-                                                  int k, int64_t T, float aux_coeff,
-                                                  float z_coeff, float* __restrict__ aux_out) {
-  __shared__ double term[NT_MOE_MAX_EXPERTS];
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    double s = 0.0;
-    for (int b = 0; b < nblk; ++b) s += (double)prob_partial[(int64_t)b * E + e];
-    term[e] = s * (double)counts[e];
+// One workgroup of 1024 threads. Thread (e, p), p < P = 1024 / E (a power of two), sums
+// block partials b = p, p + P, ... of expert e; a fixed-shape tree then combines the P values
+// and the E experts, so the result does not depend on scheduling.
+constexpr int kAuxThreads = 1024;
+
+__global__ __launch_bounds__(kAuxThreads) void aux_kernel(
+    const float* __restrict__ prob_partial, const float* __restrict__ z_partial, int nblk,
+    const int32_t* __restrict__ counts, int E, int P, int k, int64_t T, float aux_coeff,
+    float z_coeff, float* __restrict__ aux_out) {
+  __shared__ double red[kAuxThreads];
+  __shared__ double zred[kAuxThreads];
+  const int tid = threadIdx.x;
+  const int e = tid / P, p = tid - (tid / P) * P;
+  double s = 0.0;
+  if (e < E) {
+#pragma unroll 8
+    for (int b = p; b < nblk; b += P) s += (double)prob_partial[(int64_t)b * E + e];
   }
+  double z = 0.0;
+#pragma unroll 8
+  for (int b = tid; b < nblk; b += kAuxThreads) z += (double)z_partial[b];
+  red[tid] = s;
+  zred[tid] = z;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    double sum = 0.0;
-    for (int e = 0; e < E; ++e) sum += term[e];
-    double zs = 0.0;
-    for (int b = 0; b < nblk; ++b) zs += (double)z_partial[b];
+  for (int w = P >> 1; w > 0; w >>= 1) {  // tree over p inside each expert's group
+    if (e < E && p < w) red[tid] += red[tid + w];
+    __syncthreads();
+  }
+  if (e < E && p == 0) red[tid] *= (double)counts[e];  // S_e * count_e at red[e * P]
+  __syncthreads();
+  // Sum the E products (stride P) and the z partials with fixed trees.
+  for (int w = kAuxThreads >> 1; w > 0; w >>= 1) {
+    if (tid < w) {
+      zred[tid] += zred[tid + w];
+      int a = tid, bidx = tid + w;
+      if (bidx < E) red[a * P] += red[bidx * P];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
     double Td = (double)T;
-    double lb = T > 0 ? (double)aux_coeff * E / ((double)k * Td * Td) * sum : 0.0;
-    double z = T > 0 ? (double)z_coeff * zs / Td : 0.0;
-    aux_out[0] = (float)(lb + z);
+    double lb = T > 0 ? (double)aux_coeff * E / ((double)k * Td * Td) * red[0] : 0.0;
+    double zz = T > 0 ? (double)z_coeff * zred[0] / Td : 0.0;
+    aux_out[0] = (float)(lb + zz);
     aux_out[1] = (float)lb;
-    aux_out[2] = (float)z;
+    aux_out[2] = (float)zz;
   }
 }
 
@@ -145,8 +168,10 @@ hipError_t launch_combine_aux(const uint16_t* y, const int32_t* combine_dest,
   }
   if (aux_out) {
     const int nblk = ceil_div(T, kRouteBlock);
-    hipLaunchKernelGGL(aux_kernel, dim3(1), dim3(256), 0, stream, prob_partial, z_partial, nblk,
-                       counts, E, k, T, aux_coeff, z_coeff, aux_out);
+    int P = 1;
+    while (P * 2 * E <= kAuxThreads) P *= 2;
+    hipLaunchKernelGGL(aux_kernel, dim3(1), dim3(kAuxThreads), 0, stream, prob_partial, z_partial,
+                       nblk, counts, E, P, k, T, aux_coeff, z_coeff, aux_out);
     err = hipGetLastError();
   }
   return err;

@@ -13,6 +13,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kWave = 64;
@@ -70,7 +71,13 @@ hipError_t launch_grouped_ffn_bf16(const uint16_t* a, int64_t ld_a, int64_t a_ro
                                    const int32_t* seg_offsets, int num_segments,
                                    int64_t total_rows, const uint16_t* w1, const uint16_t* w2,
                                    int d, int H, int activation, uint16_t* h, uint16_t* y,
-                                   hipStream_t stream);
+                                   int* counters, hipStream_t stream);
+
+hipError_t launch_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                    const int32_t* src_row, const int32_t* seg_offsets,
+                                    int num_segments, int64_t total_rows, const uint16_t* w,
+                                    int K, int n_out, int epilogue, uint16_t* c, int* counters,
+                                    hipStream_t stream);
 
 hipError_t launch_combine_aux(const uint16_t* y, const int32_t* combine_dest,
                               const float* combine_w, int64_t T, int d, int k,
@@ -80,6 +87,9 @@ hipError_t launch_combine_aux(const uint16_t* y, const int32_t* combine_dest,
                               float* aux_out, hipStream_t stream);
 
 int num_cus();
+
+// Workspace of the grouped GEMM entry points: per-XCD tile claim counters.
+constexpr size_t kGemmWorkspaceBytes = 256;
 
 // Lets `kernel` take `bytes` of dynamic LDS (gfx950: up to 160 KB per workgroup).
 hipError_t allow_dynamic_lds(const void* kernel, size_t bytes);

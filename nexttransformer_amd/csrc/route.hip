@@ -62,41 +62,60 @@ __global__ __launch_bounds__(256) void histogram_kernel(const int32_t* __restric
   }
 }
 
-// One workgroup: counts, offsets and block_base[b][e] = offsets[e] + sum_{b' < b} counts_b'[e].
-// P = 1024 / E threads cooperate on each expert's column of block counts.
+// Inclusive scan of v over groups of `width` consecutive lanes (width a power of two <= 64).
+__device__ __forceinline__ int group_inclusive_scan(int v, int width) {
+  const int lane = lane_id();
+  for (int o = 1; o < width; o <<= 1) {
+    int u = __shfl_up(v, o, width);
+    if ((lane & (width - 1)) >= o) v += u;
+  }
+  return v;
+}
+
+// One workgroup of 1024 threads: counts, offsets and
+//   block_base[b][e] = offsets[e] + sum_{b' < b} block_counts[b'][e]   (written in place).
+// P = min(64, 1024 / E) threads (a power of two, inside one wave) own expert e's column, each a
+// contiguous run of blocks; shuffle scans combine runs and then experts.
 __global__ __launch_bounds__(1024) void scan_kernel(int32_t* __restrict__ block_counts, int nblk,
-                                                    int E, int32_t* __restrict__ counts,
+                                                    int E, int P, int32_t* __restrict__ counts,
                                                     int32_t* __restrict__ offsets) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int P = blockDim.x / E;
-  int32_t* part = reinterpret_cast<int32_t*>(smem);  // [E][P]
-  int32_t* off = part + E * P;                       // [E+1]
-  const int e = threadIdx.x / P, p = threadIdx.x - (threadIdx.x / P) * P;
+  __shared__ int32_t cnt[NT_MOE_MAX_EXPERTS];
+  __shared__ int32_t off[NT_MOE_MAX_EXPERTS + 1];
+  const int tid = threadIdx.x;
+  const int e = tid / P, p = tid - (tid / P) * P;
   const bool active = e < E;
   const int per = (nblk + P - 1) / P;
-  const int b0 = p * per, b1 = (b0 + per < nblk) ? b0 + per : nblk;
+  const int b0 = p * per < nblk ? p * per : nblk;
+  const int b1 = b0 + per < nblk ? b0 + per : nblk;
   int local = 0;
-  if (active)
+  if (active) {
+#pragma unroll 4
     for (int b = b0; b < b1; ++b) local += block_counts[(int64_t)b * E + e];
-  if (active) part[e * P + p] = local;
+  }
+  const int incl = group_inclusive_scan(local, P);
+  if (active && p == P - 1) cnt[e] = incl;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int q = 0; q < E; ++q) {
-      int c = 0;
-      for (int r = 0; r < P; ++r) c += part[q * P + r];
-      off[q] = run;
-      counts[q] = c;
-      offsets[q] = run;
-      run += c;
+  // Exclusive scan over experts by wave 0, 64 experts per pass.
+  if (tid < 64) {
+    int carry = 0;
+    for (int base = 0; base < E; base += 64) {
+      int v = base + tid < E ? cnt[base + tid] : 0;
+      int inc = group_inclusive_scan(v, 64);
+      if (base + tid < E) {
+        off[base + tid] = carry + inc - v;
+        counts[base + tid] = v;
+        offsets[base + tid] = carry + inc - v;
+      }
+      carry += __shfl(inc, 63);
     }
-    off[E] = run;
-    offsets[E] = run;
+    if (tid == 0) {
+      off[E] = carry;
+      offsets[E] = carry;
+    }
   }
   __syncthreads();
   if (active) {
-    int run = off[e];
-    for (int r = 0; r < p; ++r) run += part[e * P + r];
+    int run = off[e] + incl - local;
     for (int b = b0; b < b1; ++b) {
       int c = block_counts[(int64_t)b * E + e];
       block_counts[(int64_t)b * E + e] = run;  // becomes block_base in place
@@ -173,10 +192,10 @@ hipError_t launch_histogram_scan(const int32_t* topk_ids, int64_t T, int k, int 
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
-  const int P = 1024 / E;
-  size_t lds = (size_t)(E * P + E + 1) * sizeof(int32_t);
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), lds, stream, block_counts, nblk, E, counts,
-                     offsets);
+  int P = 1;
+  while (P < 64 && P * 2 * E <= 1024) P *= 2;
+  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, stream, block_counts, nblk, E, P,
+                     counts, offsets);
   return hipGetLastError();
 }
 

@@ -185,10 +185,12 @@ def grouped_ffn(a: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor, w1: T
     dev = a.device
     h = torch.empty(total_rows, H, device=dev, dtype=torch.bfloat16)
     y = torch.empty(total_rows, d, device=dev, dtype=torch.bfloat16)
-    st = nat.load().nt_moe_grouped_ffn_bf16(ptr(a), a.stride(0), a.shape[0], ptr(src_row),
-                                            ptr(seg_offsets),
-                                            S, total_rows, ptr(w1), ptr(w2), d, H, activation,
-                                            ptr(h), ptr(y), _stream(dev))
+    lib = nat.load()
+    ws_bytes = lib.nt_moe_grouped_gemm_workspace_bytes()
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    st = lib.nt_moe_grouped_ffn_bf16(ptr(a), a.stride(0), a.shape[0], ptr(src_row),
+                                     ptr(seg_offsets), S, total_rows, ptr(w1), ptr(w2), d, H,
+                                     activation, ptr(h), ptr(y), ptr(ws), ws_bytes, _stream(dev))
     nat.check(st, "ntmoe::grouped_ffn")
     return h, y
 
@@ -197,6 +199,40 @@ def grouped_ffn(a: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor, w1: T
 def _(a, src_row, seg_offsets, w1, w2, activation, total_rows):
     H, d = w2.shape[2], w1.shape[2]
     return (a.new_empty((total_rows, H)), a.new_empty((total_rows, d)))
+
+
+@torch.library.custom_op("ntmoe::grouped_gemm", mutates_args=())
+def grouped_gemm(a: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor, w: Tensor,
+                 epilogue: int, total_rows: int) -> Tensor:
+    """One grouped GEMM launch: c [rows, n_out] = epilogue(a_r . w_s^T) per ragged segment."""
+    _on_gpu(a, src_row, seg_offsets, w)
+    _require(a.dtype == torch.bfloat16 and a.dim() == 2 and a.stride(1) == 1,
+             "grouped_gemm: a must be bf16 [*, K] with contiguous rows")
+    _require(w.dtype == torch.bfloat16 and w.dim() == 3 and w.is_contiguous(),
+             "grouped_gemm: w must be contiguous bf16 [S, rows, K]")
+    S, rows, K = w.shape
+    n_out = rows // 2 if epilogue == nat.EPI_SWIGLU else rows
+    _require(a.shape[1] == K, "grouped_gemm: a and w disagree on K")
+    _require(seg_offsets.dtype == torch.int32 and seg_offsets.shape == (S + 1,)
+             and seg_offsets.is_contiguous(), "grouped_gemm: seg_offsets must be int32 [S+1]")
+    if src_row is not None:
+        _require(src_row.dtype == torch.int32 and src_row.is_contiguous(),
+                 "grouped_gemm: src_row must be contiguous int32")
+    c = torch.empty(total_rows, n_out, device=a.device, dtype=torch.bfloat16)
+    lib = nat.load()
+    ws_bytes = lib.nt_moe_grouped_gemm_workspace_bytes()
+    ws = torch.empty(ws_bytes, device=a.device, dtype=torch.uint8)
+    st = lib.nt_moe_grouped_gemm_bf16(ptr(a), a.stride(0), a.shape[0], ptr(src_row),
+                                      ptr(seg_offsets), S, total_rows, ptr(w), K, n_out,
+                                      epilogue, ptr(c), ptr(ws), ws_bytes, _stream(a.device))
+    nat.check(st, "ntmoe::grouped_gemm")
+    return c
+
+
+@grouped_gemm.register_fake
+def _(a, src_row, seg_offsets, w, epilogue, total_rows):
+    rows = w.shape[1]
+    return a.new_empty((total_rows, rows // 2 if epilogue == nat.EPI_SWIGLU else rows))
 
 
 # ---------------------------------------------------------------------------------------------
@@ -244,30 +280,43 @@ def _(y, combine_dest, combine_w, shared_y, prob_partial, z_partial, counts, aux
 
 def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
                 activation=nat.ACT_SWIGLU, aux_coeff=0.01, z_coeff=0.001, logit_bias=None,
-                shared_w1=None, shared_w2=None, want_logits=False, permute_rows=False):
-    """The MoE layer forward on the GPU: router -> route plan -> grouped FFN -> combine + aux.
+                shared_w1=None, shared_w2=None, want_logits=False, permute_rows=False,
+                mark=None):
+    """The MoE layer forward on the GPU: router -> route plan -> grouped GEMMs -> combine + aux.
 
-    x bf16 [T, d]; w_router_t fp32 [d, E]; w1 bf16 [E, F, d]; w2 bf16 [E, d, H]; optional
-    shared expert shared_w1 [1, Fs, d], shared_w2 [1, d, Hs]. Returns (out [T, d] bf16,
-    aux fp32 [3], state) where state holds the routing tensors. With permute_rows the token rows
-    are moved into expert order by the permute kernel first (x_perm), otherwise the grouped
-    FFN gathers them directly.
+    x bf16 [T, d]; w_router_t fp32 [d, E]; w1 bf16 [E, F, d] (F = 2H for SwiGLU, H for ReLU^2);
+    w2 bf16 [E, d, H]; optional shared expert shared_w1 [1, Fs, d], shared_w2 [1, d, Hs].
+    Returns (out [T, d] bf16, aux fp32 [3] = {lb + z, lb, z}, state with the routing tensors).
+    With permute_rows the token rows are first moved into expert order by the permute kernel
+    (x_perm); by default the up-projection GEMM gathers them itself.
+    `mark(name)`, when given, is called after each stage is enqueued (used to place timing
+    events on the stream).
     """
     T = x.shape[0]
     E = w_router_t.shape[1]
-    logits, ids, w, pp, zp = router(x, w_router_t, logit_bias, top_k, score_fn, want_logits)
-    counts, offsets, src, perm_w, cdest, cw, x_perm = route_plan(ids, w, E, x if permute_rows else None,
-                                                                 permute_rows)
     A = T * top_k
+    mark = mark or (lambda name: None)
+    logits, ids, w, pp, zp = router(x, w_router_t, logit_bias, top_k, score_fn, want_logits)
+    mark("router")
+    counts, offsets, src, perm_w, cdest, cw, x_perm = route_plan(
+        ids, w, E, x if permute_rows else None, permute_rows)
+    mark("route_plan")
+    up_epi = nat.EPI_SWIGLU if activation == nat.ACT_SWIGLU else nat.EPI_RELU2
     if permute_rows:
-        _, y = grouped_ffn(x_perm, None, offsets, w1, w2, activation, A)
+        h = grouped_gemm(x_perm, None, offsets, w1, up_epi, A)
     else:
-        _, y = grouped_ffn(x, src, offsets, w1, w2, activation, A)
+        h = grouped_gemm(x, src, offsets, w1, up_epi, A)
+    mark("gemm_up")
+    y = grouped_gemm(h, None, offsets, w2, nat.EPI_NONE, A)
+    mark("gemm_down")
     shared_y = None
     if shared_w1 is not None:
         seg = torch.tensor([0, T], device=x.device, dtype=torch.int32)
-        _, shared_y = grouped_ffn(x, None, seg, shared_w1, shared_w2, activation, T)
+        hs = grouped_gemm(x, None, seg, shared_w1, up_epi, T)
+        shared_y = grouped_gemm(hs, None, seg, shared_w2, nat.EPI_NONE, T)
+        mark("shared")
     out, aux = combine_aux(y, cdest, cw, shared_y, pp, zp, counts, aux_coeff, z_coeff)
+    mark("combine")
     state = dict(logits=logits, ids=ids, weights=w, counts=counts, offsets=offsets, src_row=src,
                  perm_w=perm_w, combine_dest=cdest, combine_w=cw)
     return out, aux, state
