@@ -283,13 +283,24 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   float* lg = reinterpret_cast<float*>(smem);
   float* zt = reinterpret_cast<float*>(smem + zt_offset(E));
   const int64_t t0 = (int64_t)blockIdx.x * kRouteBlock;
+  // Chunk planes are summed in ascending order; loads go out 8 planes at a time so the sum is
+  // not a chain of dependent memory round trips.
+  const int64_t plane = T * E;
   for (int idx = threadIdx.x; idx < kRouteBlock * E; idx += blockDim.x) {
     int r = idx / E, e = idx - r * E;
     int64_t t = t0 + r;
     float v = 0.f;
     if (t < T) {
-      v = partials[t * E + e];
-      for (int c = 1; c < nchunk; ++c) v = v + partials[((int64_t)c * T + t) * E + e];
+      const float* p = partials + t * E + e;
+      v = p[0];
+      for (int c0 = 1; c0 < nchunk; c0 += 8) {
+        float part[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) part[j] = c0 + j < nchunk ? p[(int64_t)(c0 + j) * plane] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (c0 + j < nchunk) v = v + part[j];
+      }
       if (bias) v = v + bias[e];
       if (logits) logits[t * E + e] = v;
     }
