@@ -45,7 +45,30 @@ def parse():
     p.add_argument("--permute-rows", action="store_true",
                    help="move token rows with the permute kernel instead of gathering in the GEMM")
     p.add_argument("--cpu-budget-s", type=float, default=20.0)
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only run a plain 1 GiB device-to-device copy (known HBM bytes), used to "
+                        "scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     return p.parse_args()
+
+
+def calibrate_copy(reps=20, nbytes=1 << 30):
+    """A plain copy of known size: reads and writes `nbytes` per launch."""
+    import torch
+    src = torch.empty(nbytes // 2, device="cuda", dtype=torch.bfloat16).normal_()
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes,
+                      "avg_launch_ms": round(ms, 5),
+                      "GB_per_s": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
 
 
 def gpu_inputs(case):
@@ -110,6 +133,10 @@ def main():
         log("bench.py: this build is single-GPU only (one MI355X, no collectives); "
             f"--gpus {args.gpus} / WORLD_SIZE {world} is not supported.")
         sys.exit(2)
+
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
 
     import torch
     from nexttransformer_amd import ops

@@ -1,0 +1,274 @@
+"""The MoE layer module over the HIP kernels: a drop-in for the reference's MoE engine.
+
+Reference contract (nexttransformer/scaling/megatron_moe.py):
+  * constructor (recipe, layer_number, pg_collection)                         :124-135
+  * submodules router.weight [E, d]; experts.local_experts.{i}.linear_fc1/2;
+    shared_experts.linear_fc1/2 (fp32 masters, bias-free)                      :58-78, 128-134
+  * initialisation keyed by global expert id, fork_rng-style private seeds     :105-120, :27-29
+  * last_load = per-expert token counts                                        :143, 149
+  * MegatronFFN(recipe, layer_number, *, pg_collection, cpu_math) wraps the
+    engine and returns only the output for a [B, S, d] hidden                  :153-182
+The engine's forward here returns (out, aux_loss) rather than MCore's (out, bias=None): the
+aux loss (load balance + z-loss, closed forms of megatron_moe.py:44-45) is a value, and it is
+also kept as the tensor attribute `last_aux` that the plugin shell sums into the training loss
+(nexttransformer/models/plugins.py:24-25, lm.py:386-388).
+
+Compute: x is cast to bf16 (the reference's MasterLinear runs matmuls in the activation dtype,
+megatron_moe.py:74-75); the router GEMM runs in fp32 on the bf16 values; expert GEMMs run on
+bf16 copies of the fp32 masters, repacked into [E, rows, cols] stacks only when a master changes
+(tracked by the tensors' version counters, which in-place optimizer updates bump).
+
+The HIP path is forward-only: a call that would need gradients raises RuntimeError instead of
+returning a result without a graph. There is no CPU path.
+"""
+import math
+
+import torch
+from torch import nn
+
+from nexttransformer_amd import _native as nat
+from nexttransformer_amd import ops
+from nexttransformer_amd.moe_recipe import MoERecipe
+
+SEED_LAYER_STRIDE = 100003  # megatron_moe.py:113-120: seed + 100003 * layer_number + index
+_SCORE = {"softmax": nat.SCORE_SOFTMAX, "sigmoid": nat.SCORE_SIGMOID}
+_ACT = {"swiglu": nat.ACT_SWIGLU, "relu2": nat.ACT_RELU2}
+
+
+def input_init_(weight, generator=None):
+    """U(-b, b), b = 0.4 * sqrt(3 / fan_in) (megatron_moe.py:27-29)."""
+    bound = 0.4 * math.sqrt(3 / weight.shape[-1])
+    return nn.init.uniform_(weight, -bound, bound, generator=generator)
+
+
+def _round64(n):
+    return (n + 63) // 64 * 64
+
+
+def _seeded(seed):
+    return torch.Generator(device="cpu").manual_seed(seed)
+
+
+class Router(nn.Module):
+    """The gating matrix: router.weight [E, d], fp32 (router dtype fp32, megatron_moe.py:42)."""
+
+    def __init__(self, experts, width, device):
+        super().__init__()
+        self.weight = nn.Parameter(torch.empty(experts, width, device=device, dtype=torch.float32))
+
+
+class ExpertMLP(nn.Module):
+    """One expert: linear_fc1 [rows, d], linear_fc2 [d, hidden], bias-free fp32 masters.
+
+    rows = 2 * hidden for SwiGLU (rows [0, hidden) gate, [hidden, 2 hidden) value), hidden for
+    the reference's ReLU^2 expert (megatron_moe.py:23-24, 51).
+    """
+
+    def __init__(self, width, hidden, gated, device):
+        super().__init__()
+        rows = 2 * hidden if gated else hidden
+        self.linear_fc1 = nn.utils.skip_init(nn.Linear, width, rows, bias=False, device=device)
+        self.linear_fc2 = nn.utils.skip_init(nn.Linear, hidden, width, bias=False, device=device)
+
+
+class LocalExperts(nn.Module):
+    """experts.local_experts.{i}: every routed expert (one GPU, so local ids are global ids)."""
+
+    def __init__(self, count, width, hidden, gated, device):
+        super().__init__()
+        self.local_experts = nn.ModuleList(
+            ExpertMLP(width, hidden, gated, device) for _ in range(count))
+
+
+def _ep_size(pg_collection):
+    ep = getattr(pg_collection, "ep", None)
+    if ep is None:
+        return 1
+    size = ep.size() if callable(getattr(ep, "size", None)) else getattr(ep, "size", 1)
+    return int(size)
+
+
+class MoELayer(nn.Module):
+    """MoE layer forward on one MI355X: router -> route plan -> grouped GEMMs -> combine + aux.
+
+    forward(hidden [..., d]) -> (out [..., d] in hidden's dtype, aux_loss fp32 scalar).
+    """
+
+    def __init__(self, recipe: MoERecipe, layer_number: int, pg_collection=None, *, device=None):
+        super().__init__()
+        if not isinstance(recipe, MoERecipe):
+            raise ValueError("recipe must be a MoERecipe")
+        if layer_number < 1:
+            raise ValueError("layer_number counts from one")
+        if _ep_size(pg_collection) != 1:
+            raise ValueError("this build runs the MoE layer on one GPU; expert parallelism "
+                             "(pg_collection.ep size > 1) is not supported")
+        if recipe.routed_experts > nat.MAX_EXPERTS or recipe.top_k > nat.MAX_TOPK:
+            raise ValueError(f"the HIP router supports at most {nat.MAX_EXPERTS} experts and "
+                             f"top-{nat.MAX_TOPK}")
+        if recipe.expert_dtype != "bf16":
+            raise ValueError(f"expert_dtype {recipe.expert_dtype!r} has no grouped GEMM in this "
+                             "build (bf16 only)")
+        if device is None:
+            device = (torch.device("cuda", torch.cuda.current_device())
+                      if torch.cuda.is_available() else torch.device("cpu"))
+        self.recipe = recipe
+        self.layer_number = layer_number
+        gated = recipe.activation == "swiglu"
+        self.router = Router(recipe.routed_experts, recipe.width, device)
+        self.experts = LocalExperts(recipe.routed_experts, recipe.width, recipe.expert_width,
+                                    gated, device)
+        self.shared_experts = (ExpertMLP(recipe.width, recipe.shared_expert_width, gated, device)
+                               if recipe.shared_experts else None)
+        self.last_load = None
+        self.last_aux = None
+        self.last_aux_parts = None
+        self._pack_key = None
+        self._packed = None
+        self.reset_parameters()
+
+    # -- initialisation --------------------------------------------------------------------
+
+    @torch.no_grad()
+    def reset_parameters(self):
+        """Initialise as megatron_moe.py:105-120 does on its CPU path: every expert draws from
+        its own CPU generator seeded seed + 100003 * layer + global expert id; the shared expert
+        uses id E and the router id E + 1. fc1 ~ U(+-0.4 sqrt(3/d)), fc2 = 0, router ~ N(0, std).
+        Values are drawn on the CPU and copied, so they are identical on every device."""
+        r = self.recipe
+        base = r.seed + SEED_LAYER_STRIDE * self.layer_number
+
+        def init_expert(expert, seed):
+            fc1 = torch.empty(expert.linear_fc1.weight.shape, dtype=torch.float32, device="cpu")
+            input_init_(fc1, _seeded(seed))
+            expert.linear_fc1.weight.copy_(fc1)
+            expert.linear_fc2.weight.zero_()
+
+        for i, expert in enumerate(self.experts.local_experts):
+            init_expert(expert, base + i)
+        if self.shared_experts is not None:
+            init_expert(self.shared_experts, base + r.routed_experts)
+        w = torch.empty(self.router.weight.shape, dtype=torch.float32, device="cpu")
+        nn.init.normal_(w, std=r.router_init_std, generator=_seeded(base + r.routed_experts + 1))
+        self.router.weight.copy_(w)
+        self._pack_key = None
+
+    # -- packed bf16 weights ---------------------------------------------------------------
+
+    def _masters(self):
+        ps = [self.router.weight]
+        for e in self.experts.local_experts:
+            ps += [e.linear_fc1.weight, e.linear_fc2.weight]
+        if self.shared_experts is not None:
+            ps += [self.shared_experts.linear_fc1.weight, self.shared_experts.linear_fc2.weight]
+        return ps
+
+    @torch.no_grad()
+    def packed_weights(self):
+        """Device weights the kernels read, rebuilt only when a master tensor changed:
+        router_t fp32 [dp, E]; w1 bf16 [E, rows, dp]; w2 bf16 [E, dp, Hp]; shared_w1/2 [1, ...].
+
+        The grouped GEMM tiles K and the SwiGLU halves in multiples of 64, so d and the expert
+        widths are zero-padded up to dp, Hp (multiples of 64) when they are not already: zero
+        input features add exact zeros to every dot product, and a zero hidden unit has
+        act(0) = 0 under both SwiGLU and ReLU^2, so the padded layer computes the same values.
+        """
+        masters = self._masters()
+        key = tuple((p.data_ptr(), p._version) for p in masters)
+        if key != self._pack_key:
+            r = self.recipe
+            dp = _round64(r.width)
+            gated = r.activation == "swiglu"
+
+            def stack(experts, hidden):
+                hp = _round64(hidden)
+                if hp == hidden and dp == r.width:
+                    return (torch.stack([e.linear_fc1.weight.detach() for e in experts])
+                            .to(torch.bfloat16),
+                            torch.stack([e.linear_fc2.weight.detach() for e in experts])
+                            .to(torch.bfloat16))
+                n = len(experts)
+                dev = experts[0].linear_fc1.weight.device
+                w1 = torch.zeros(n, (2 if gated else 1) * hp, dp, device=dev, dtype=torch.bfloat16)
+                w2 = torch.zeros(n, dp, hp, device=dev, dtype=torch.bfloat16)
+                for i, e in enumerate(experts):
+                    fc1 = e.linear_fc1.weight.detach()
+                    if gated:
+                        w1[i, :hidden, :r.width] = fc1[:hidden]
+                        w1[i, hp:hp + hidden, :r.width] = fc1[hidden:]
+                    else:
+                        w1[i, :hidden, :r.width] = fc1
+                    w2[i, :r.width, :hidden] = e.linear_fc2.weight.detach()
+                return w1, w2
+
+            router_t = torch.zeros(dp, r.routed_experts, device=self.router.weight.device,
+                                   dtype=torch.float32)
+            router_t[:r.width] = self.router.weight.detach().t()
+            w1, w2 = stack(list(self.experts.local_experts), r.expert_width)
+            packed = dict(router_t=router_t, w1=w1, w2=w2, shared_w1=None, shared_w2=None)
+            if self.shared_experts is not None:
+                packed["shared_w1"], packed["shared_w2"] = stack([self.shared_experts],
+                                                                 r.shared_expert_width)
+            self._packed = packed
+            self._pack_key = key
+        return self._packed
+
+    # -- forward ---------------------------------------------------------------------------
+
+    def forward(self, hidden):
+        r = self.recipe
+        if hidden.shape[-1] != r.width:
+            raise ValueError(f"hidden width {hidden.shape[-1]} != recipe width {r.width}")
+        if not hidden.is_cuda:
+            raise ValueError("the MoE layer runs on the GPU only (no CPU path)")
+        if torch.is_grad_enabled() and (hidden.requires_grad or
+                                        any(p.requires_grad for p in self.parameters())):
+            raise RuntimeError("the HIP MoE layer is forward-only: call it under torch.no_grad() "
+                               "or torch.inference_mode()")
+        if self.router.weight.device != hidden.device:
+            raise ValueError(f"parameters are on {self.router.weight.device}, hidden on "
+                             f"{hidden.device}")
+        w = self.packed_weights()
+        x = hidden.reshape(-1, r.width)
+        dp = w["router_t"].shape[0]
+        if dp != r.width:
+            xp = torch.zeros(x.shape[0], dp, device=x.device, dtype=torch.bfloat16)
+            xp[:, :r.width] = x
+            x = xp
+        elif x.dtype != torch.bfloat16 or x.stride(-1) != 1:
+            x = x.to(torch.bfloat16).contiguous()
+        out, aux, state = ops.moe_forward(
+            x, w["router_t"], w["w1"], w["w2"], top_k=r.top_k,
+            score_fn=_SCORE[r.score_function], activation=_ACT[r.activation],
+            aux_coeff=r.aux_loss_coeff, z_coeff=r.z_loss_coeff,
+            shared_w1=w["shared_w1"], shared_w2=w["shared_w2"])
+        if dp != r.width:
+            out = out[:, :r.width]
+        self.last_load = state["counts"].to(torch.int64)
+        self.last_aux_parts = aux
+        self.last_aux = aux[0]
+        out = out.reshape(hidden.shape).to(hidden.dtype)
+        return out, self.last_aux
+
+
+class MoEFFN(nn.Module):
+    """The block-level wrapper (megatron_moe.py:153-182): forward(hidden [B, S, d]) -> [B, S, d].
+
+    The engine's per-row computation and its aux loss (sums over all tokens) do not depend on the
+    token order, so no [B, S] <-> [S, B] transpose is needed around it.
+    """
+
+    def __init__(self, recipe, layer_number, *, pg_collection=None, cpu_math=False, device=None):
+        super().__init__()
+        if cpu_math:
+            raise ValueError("this build has no CPU math path: the MoE layer runs on the GPU")
+        self.engine = MoELayer(recipe, layer_number, pg_collection, device=device)
+        self.last_aux = None
+
+    def forward(self, hidden):
+        out, aux = self.engine(hidden)
+        self.last_aux = aux
+        return out
+
+
+MegatronFFN = MoEFFN

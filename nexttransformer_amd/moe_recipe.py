@@ -1,6 +1,7 @@
 """MoE recipe: the reference's MoERecipe config keys plus the keys this MI355X build adds.
 
-Mirrors nexttransformer/scaling/moe_recipe.py:26-72 (field names, defaults, validation and
+Mirrors nexttransformer/scaling/moe_recipe.py:26-154 (field names, defaults, validation,
+counts/estimate/manifest, load_t3_recipe and
 ValueError behaviour). Added keys, all explicit so no reference recipe changes meaning:
   score_function         "softmax" (the reference's router, megatron_moe.py:43) or "sigmoid"
                          (top-k on logits, sigmoid scores normalised over the selected)
@@ -13,14 +14,23 @@ ValueError behaviour). Added keys, all explicit so no reference recipe changes m
   allow_any_expert_width the reference requires expert_width == width // 4
                          (moe_recipe.py:63-64); True relaxes exactly that check
 """
-from dataclasses import dataclass, replace
+from dataclasses import asdict, dataclass, replace
+import json
 import math
+from pathlib import Path
 
 EXPERT_FAMILIES = ("moe", "looped", "kda-dsa")
 FULL_ATTENTION = ("moe", "looped")
 SCORE_FUNCTIONS = ("softmax", "sigmoid")
 ACTIVATIONS = ("relu2", "swiglu")
 EXPERT_DTYPES = ("bf16", "fp8")
+# The feed-forward keys the T3 expert families share (moe_recipe.py:14-17); a manifest whose
+# expert families disagree with them is rejected by load_t3_recipe.
+SHARED_FFN_RECIPE = dict(firstLayerDense=True, ffn="ReLU²", routedExperts=256,
+                         selectedExperts=8, sharedExperts=1, expertWidthDivisor=4)
+ATTENTION_NOTE = {"moe": "native full causal MHA; no VE",
+                  "looped": "native full causal MHA, shared core executed twice; no VE",
+                  "kda-dsa": "three KDA mixers then one DSA mixer; no VE"}
 
 
 @dataclass(frozen=True)
@@ -113,6 +123,46 @@ class MoERecipe:
                 + (self.layers - 1) * (self.top_k * self.expert_params() + shared)
                 + (self.layers - 1) * d * e)
 
+    def describes_capacity(self):
+        """Whether the parameter counts describe the family: a flat stack of MHA layers."""
+        return self.family in FULL_ATTENTION and self.unique_layers == self.layers
+
+    def counts(self):
+        """Parameter counts (moe_recipe.py:93-106): attention 4Ld^2, a dense first FFN 8d^2,
+        (L-1) MoE layers of E routed + shared experts and a d x E router, embeddings and head
+        padded to 64 rows, and the backbone's 2L + 26 scalars."""
+        if not self.describes_capacity():
+            raise ValueError(f"{self.family} capacity needs its own accounting")
+        d, e = self.width, self.routed_experts
+        shared = self.shared_experts * self.expert_params(self.shared_expert_width)
+        total = (4 * self.layers * d * d + 8 * d * d
+                 + (self.layers - 1) * (e * self.expert_params() + shared)
+                 + (self.layers - 1) * d * e)
+        small = 2 * self.layers + 26
+        io = 2 * d * math.ceil(self.vocab_size / 64) * 64
+        return dict(block_total=total, block_active=self.block_active(), embedding_and_head=io,
+                    native_small_parameters=small, model_total=total + io + small)
+
+    def estimate(self):
+        """Main-term training cost (moe_recipe.py:108-118): 6 x active parameters + attention
+        12 s d L + head 6 d V FLOP per token, and the updates / tokens the budget buys."""
+        if self.family not in FULL_ATTENTION:
+            return dict(flops_per_token_main_term=None, estimated_updates=None,
+                        estimated_tokens=None, cost_proof_complete=False)
+        d, s = self.width, self.sequence_len
+        flops = 6 * self.block_active() + 12 * s * d * self.layers + 6 * d * self.vocab_size
+        updates = round(self.training_flops / (flops * self.global_batch_tokens))
+        return dict(flops_per_token_main_term=flops, estimated_updates=updates,
+                    estimated_tokens=updates * self.global_batch_tokens, cost_proof_complete=False)
+
+    def manifest(self):
+        counts = self.counts() if self.describes_capacity() else None
+        act = {"relu2": "ReLU squared", "swiglu": "SwiGLU"}[self.activation]
+        return dict(protocol="nextt-scale-2k-v1", recipe=asdict(self), counts=counts,
+                    estimate=self.estimate(), attention=ATTENTION_NOTE[self.family],
+                    ffn=f"first dense 4d; then routed top-k plus {self.shared_experts} shared; {act}",
+                    gpu_validated=False, formal_training_ready=False)
+
     def moe_layer_params(self):
         """Parameters of one MoE layer as built by nexttransformer_amd.moe.MoELayer."""
         shared = self.shared_experts * self.expert_params(self.shared_expert_width)
@@ -126,3 +176,30 @@ class MoERecipe:
                        routed_experts=routed_experts, top_k=top_k, expert_width=8,
                        shared_expert_width=8, global_batch_tokens=32,
                        cell_id=self.cell_id + "-cpu-debug")
+
+
+def load_t3_recipe(cell_id="moe-T3-L20", path=None):
+    """The recipe of a T3 expert cell from a scaling manifest (moe_recipe.py:136-154).
+
+    `path` is the manifest JSON (the reference keeps it at configs/scaling/t3.json); this
+    package ships none, so it is required.
+    """
+    if path is None:
+        raise ValueError("load_t3_recipe needs the path of a T3 scaling manifest")
+    data = json.loads(Path(path).read_text())
+    cell = next((c for c in data["cells"]
+                 if c["id"] == cell_id and c["family"] in EXPERT_FAMILIES), None)
+    if cell is None:
+        raise ValueError(f"unknown T3 expert cell: {cell_id}")
+    rule = next(f["recipe"] for f in data["families"] if f["id"] == cell["family"])
+    if ({k: v for k, v in rule.items() if k in SHARED_FFN_RECIPE} != SHARED_FFN_RECIPE
+            or data["valueEmbeddings"] or data["protocol"] != "nextt-scale-2k-v1"):
+        raise ValueError("the shared T3 expert recipe changed; review the adapter before using it")
+    loops = rule.get("loops", 1)
+    unique = (cell["preLayers"] + cell["coreLayers"] + cell["postLayers"] if loops > 1
+              else cell["layers"])
+    return MoERecipe(layers=cell["layers"], width=cell["width"], heads=cell["heads"],
+                     vocab_size=data["vocabSize"], sequence_len=data["sequenceLength"],
+                     seed=data["seed"], global_batch_tokens=data["globalBatchTokens"],
+                     training_flops=data["trainingFlops"], expert_width=cell["expertWidth"],
+                     cell_id=cell_id, family=cell["family"], unique_layers=unique, loops=loops)

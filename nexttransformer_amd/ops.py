@@ -296,6 +296,16 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
     E = w_router_t.shape[1]
     A = T * top_k
     mark = mark or (lambda name: None)
+    if T == 0:
+        dev = x.device
+        i32, f32 = torch.int32, torch.float32
+        empty = lambda *shape, dtype=i32: torch.empty(shape, device=dev, dtype=dtype)
+        state = dict(logits=empty(0, E, dtype=f32), ids=empty(0, top_k),
+                     weights=empty(0, top_k, dtype=f32), counts=torch.zeros(E, device=dev, dtype=i32),
+                     offsets=torch.zeros(E + 1, device=dev, dtype=i32), src_row=empty(0),
+                     perm_w=empty(0, dtype=f32), combine_dest=empty(0, top_k),
+                     combine_w=empty(0, top_k, dtype=f32))
+        return x.new_empty(0, x.shape[1]), torch.zeros(3, device=dev, dtype=f32), state
     logits, ids, w, pp, zp = router(x, w_router_t, logit_bias, top_k, score_fn, want_logits)
     mark("router")
     counts, offsets, src, perm_w, cdest, cw, x_perm = route_plan(
