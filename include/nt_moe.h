@@ -148,9 +148,9 @@ int nt_moe_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
  *   h            bf16 [total_rows, H] (intermediate, caller-owned)
  *   y            bf16 [total_rows, d]
  *   total_rows   upper bound of seg_offsets[num_segments] used to size the launch
- *   workspace    nt_moe_grouped_gemm_workspace_bytes() bytes of device memory (tile claim
- *                counters, reset by the call itself); calls that share one workspace must be
- *                ordered on one stream
+ *   workspace    nt_moe_grouped_gemm_workspace_bytes() bytes of device memory, reserved for
+ *                the tile scheduler: required, but the static per-XCD schedule of this
+ *                version neither reads nor writes it
  * Requirements: d % 64 == 0, H % 64 == 0, 16-byte aligned buffers, a_rows * ld_a * 2 and one
  * segment's weights each within 4 GiB.
  */
