@@ -3,15 +3,19 @@
     python bench.py [--steps K] [--warmup W] [--config 2] [--no-cpu-baseline]
 
 A step is one full MoE layer forward (router -> histogram/scan -> permute plan -> grouped
-SwiGLU GEMMs -> combine + aux loss) over one batch of synthetic input already resident in HBM.
-Default workload: config 2 of BASELINE.json (T=16384 = 8 x 2048, d=1024, 32 experts, top-4
-softmax, SwiGLU H=512, bf16, dropless). Prints ONE JSON line.
+expert GEMMs -> combine + aux loss) over one batch of synthetic input already resident in HBM.
+Default workload: config 2 (T=16384 = 8 x 2048, d=1024, 32 experts, top-4 softmax, SwiGLU H=512,
+bf16, dropless). Configs 1-4 run the bf16 path; config 5 (T=64, d=4096, 128 experts, top-8,
+H=1536) runs the fp8 path (e4m3 weights with 128 x 128 block scales, activations quantised per
+row on the fly). Prints ONE JSON line.
 
 roofline: the dominant kernel is the grouped up-projection GEMM (gate/value GEMM with the fused
-SwiGLU epilogue, 2/3 of the layer's FLOP). Its algorithmic FLOP per launch = 2 * (T k) * d * 2H;
-its average launch duration is measured with HIP events recorded on the launch stream around
-every launch inside the timed region. `traffic` (HBM bytes per launch) comes from the rocprofv3
-FETCH_SIZE / WRITE_SIZE summary committed in profiles/traffic.json, when present.
+SwiGLU epilogue, 2/3 of the layer's FLOP). bf16 configs: bound "mfma", algorithmic FLOP per
+launch = 2 * (T k) * d * 2H. Config 5: bound "hbm", algorithmic bytes per launch = the e4m3
+weights and scales of the experts that received tokens + the quantised token rows once + h
+written. The average launch duration is measured with HIP events recorded on the launch stream
+around every launch inside the timed region. `traffic` (HBM bytes per launch) comes from the
+rocprofv3 FETCH_SIZE / WRITE_SIZE summary in profiles/traffic.json, when present.
 
 cpu_baseline: the CPU oracle (a restatement of the reference's eager per-expert PyTorch loop,
 fp32) timed on this host's cores on the same workload, on rank 0 only.
@@ -40,7 +44,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=50)
-    p.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4])
+    p.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--permute-rows", action="store_true",
                    help="move token rows with the permute kernel instead of gathering in the GEMM")
@@ -71,16 +75,24 @@ def calibrate_copy(reps=20, nbytes=1 << 30):
                       "GB_per_s": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
 
 
-def gpu_inputs(case):
+def gpu_inputs(case, fp8):
     import torch
+    from nexttransformer_amd import ops
     from tests.moe_cases import make_inputs
     cpu = make_inputs(case)
     dev = torch.device("cuda")
-    bf = lambda t: None if t is None else t.to(torch.bfloat16).to(dev)
-    return cpu, dict(x=cpu["x"].to(dev), wt=cpu["router"].t().contiguous().to(dev),
-                     w1=bf(cpu["w1"]), w2=bf(cpu["w2"]), sw1=bf(cpu["shared_w1"]),
-                     sw2=bf(cpu["shared_w2"]),
-                     bias=None if cpu["bias"] is None else cpu["bias"].to(dev))
+    g = dict(x=cpu["x"].to(dev), wt=cpu["router"].t().contiguous().to(dev),
+             bias=None if cpu["bias"] is None else cpu["bias"].to(dev))
+    for name in ("w1", "w2", "shared_w1", "shared_w2"):
+        g[name], g[name + "_scale"] = None, None
+        if cpu[name] is None:
+            continue
+        if fp8:
+            g[name], g[name + "_scale"] = ops.quantize_fp8_blockwise(cpu[name].to(dev))
+        else:
+            g[name] = cpu[name].to(torch.bfloat16).to(dev)
+    torch.cuda.synchronize()
+    return cpu, g
 
 
 def layer_flops(case):
@@ -110,20 +122,36 @@ def cpu_baseline(case, cpu, budget_s):
                           bias=cpu["bias"])
     x = cpu["x"]
 
-    def run(tokens):
+    def run():
         t0 = time.perf_counter()
-        orc.moe_forward(x[:tokens], weights, case.k, score_fn=case.score_fn,
-                        activation=case.activation, router="reference")
+        orc.moe_forward(x, weights, case.k, score_fn=case.score_fn, activation=case.activation,
+                        router="reference")
         return time.perf_counter() - t0
 
-    first = run(case.T)  # warm-up, also sizes the sample
+    first = run()  # warm-up, also sizes the sample
     reps = max(1, min(5, int(budget_s / max(first, 1e-3))))
-    times = sorted(run(case.T) for _ in range(reps))
+    times = sorted(run() for _ in range(reps))
     med = times[len(times) // 2]
     return dict(value=case.T / med, unit="tokens/s", cores=threads, kind="port",
                 sample=f"full workload ({case.T} tokens), oracle eager per-expert fp32 loop with "
                        f"the reference's F.linear router, median of {reps} after 1 warm-up",
                 ms_per_step=med * 1e3)
+
+
+def describe(case, cfg, permute_rows, fp8):
+    act = "SwiGLU" if case.activation == 0 else "ReLU2"
+    score = "softmax" if case.score_fn == 0 else "sigmoid (normalised over top-k)"
+    text = (f"MoE layer forward, config {cfg}: T={case.T}, d={case.d}, E={case.E}, "
+            f"top-{case.k} {score}, {act} H={case.H}")
+    if case.shared_H:
+        text += f", shared expert H={case.shared_H}"
+    if case.zipf_bias:
+        text += f", Zipf({case.zipf_bias}) logit bias"
+    if fp8:
+        text += ", fp8 e4m3 experts (128x128 block scales, per-row activation scales)"
+    return {"workload": text + ", dropless", "tokens": case.T, "d_model": case.d,
+            "experts": case.E, "top_k": case.k, "expert_hidden": case.H,
+            "shared_hidden": case.shared_H, "rows_gathered_in_gemm": not permute_rows}
 
 
 def main():
@@ -143,22 +171,29 @@ def main():
     from tests.moe_cases import CONFIGS
 
     case = CONFIGS[args.config]
+    fp8 = args.config == 5
     log(f"[bench] config {args.config}: {case}")
-    cpu, g = gpu_inputs(case)
-    torch.cuda.synchronize()
+    cpu, g = gpu_inputs(case, fp8)
 
     def forward(mark=None):
         return ops.moe_forward(g["x"], g["wt"], g["w1"], g["w2"], top_k=case.k,
                                score_fn=case.score_fn, activation=case.activation,
-                               logit_bias=g["bias"], shared_w1=g["sw1"], shared_w2=g["sw2"],
+                               logit_bias=g["bias"], shared_w1=g["shared_w1"],
+                               shared_w2=g["shared_w2"], w1_scale=g["w1_scale"],
+                               w2_scale=g["w2_scale"], shared_w1_scale=g["shared_w1_scale"],
+                               shared_w2_scale=g["shared_w2_scale"],
                                permute_rows=args.permute_rows, mark=mark)
 
-    for _ in range(args.warmup):
-        forward()
+    state = None
+    for _ in range(max(1, args.warmup)):
+        _, _, state = forward()
     torch.cuda.synchronize()
-    log(f"[bench] warm-up done ({args.warmup} steps)")
+    counts = state["counts"].cpu()
+    load_ratio = counts.max().item() / counts.float().mean().item()
+    log(f"[bench] warm-up done ({args.warmup} steps); expert load max/mean {load_ratio:.2f}")
 
     # Timed region: K full forwards; HIP events bracket every up-projection GEMM launch.
+    before_up = "quantize" if fp8 else "route_plan"
     stream = torch.cuda.current_stream()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(args.steps)]
@@ -166,7 +201,7 @@ def main():
     t0 = time.perf_counter()
     for i in range(args.steps):
         def mark(name, i=i):
-            if name == "route_plan":
+            if name == before_up:
                 ev[i][0].record(stream)
             elif name == "gemm_up":
                 ev[i][1].record(stream)
@@ -178,9 +213,8 @@ def main():
     log(f"[bench] timed {args.steps} steps: {ms:.4f} ms/step, gemm_up {up_ms:.4f} ms")
 
     # Per-stage breakdown (separate instrumented pass, outside the timed region).
-    names = ["router", "route_plan", "gemm_up", "gemm_down", "shared", "combine"]
     reps = 10
-    stage = {n: 0.0 for n in names}
+    stage = {}
     for _ in range(reps):
         evs = [("start", torch.cuda.Event(enable_timing=True))]
         evs[0][1].record(stream)
@@ -192,14 +226,30 @@ def main():
         forward(mark)
         torch.cuda.synchronize()
         for (_, a), (n, b) in zip(evs, evs[1:]):
-            stage[n] += a.elapsed_time(b) / reps
-    stage = {n: round(v, 5) for n, v in stage.items() if v > 0}
+            stage[n] = stage.get(n, 0.0) + a.elapsed_time(b) / reps
+    stage = {n: round(v, 5) for n, v in stage.items()}
 
     A = case.T * case.k
     F = 2 * case.H if case.activation == 0 else case.H
-    up_flop = 2.0 * A * case.d * F
-    achieved = up_flop / (up_ms * 1e-3) / 1e12
-    traffic = load_traffic(f"config{args.config}")
+    if fp8:
+        touched = int((counts > 0).sum())
+        up_bytes = (touched * F * case.d + touched * (F // 128) * (case.d // 128) * 4
+                    + case.T * case.d + case.T * 4 + A * case.H * 2)
+        achieved = up_bytes / (up_ms * 1e-3) / 1e9
+        roofline = {"kernel": "fp8_grouped_gemm_kernel (up-projection, e4m3 weight streaming)",
+                    "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                    "traffic": load_traffic(f"config{args.config}"),
+                    "bytes_per_launch": up_bytes, "experts_touched": touched,
+                    "avg_launch_ms": round(up_ms, 5)}
+    else:
+        up_flop = 2.0 * A * case.d * F
+        achieved = up_flop / (up_ms * 1e-3) / 1e12
+        roofline = {"kernel": "grouped_gemm_kernel (up-projection + SwiGLU epilogue)",
+                    "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                    "traffic": load_traffic(f"config{args.config}"),
+                    "flop_per_launch": up_flop, "avg_launch_ms": round(up_ms, 5)}
     result = {
         "metric": METRIC,
         "value": round(case.T / (ms * 1e-3), 1),
@@ -211,30 +261,12 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "fp8-e4m3 (fp32 accumulate)" if fp8 else "bf16",
         "data": "synthetic: hidden ~N(0,1), router/expert weights ~N(0,0.02) random init, seed 0",
-        "config": {
-            "workload": f"MoE layer forward, config {args.config}: T={case.T}, d={case.d}, "
-                        f"E={case.E}, top-{case.k} {'softmax' if case.score_fn == 0 else 'sigmoid'}, "
-                        f"{'SwiGLU' if case.activation == 0 else 'ReLU2'} H={case.H}"
-                        + (f", shared H={case.shared_H}" if case.shared_H else "")
-                        + (f", Zipf({case.zipf_bias}) logit bias" if case.zipf_bias else "")
-                        + ", dropless",
-            "tokens": case.T, "d_model": case.d, "experts": case.E, "top_k": case.k,
-            "expert_hidden": case.H, "rows_gathered_in_gemm": not args.permute_rows,
-        },
-        "roofline": {
-            "kernel": "grouped_gemm_kernel (up-projection + SwiGLU epilogue)",
-            "bound": "mfma",
-            "achieved": round(achieved, 2),
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": traffic,
-            "flop_per_launch": up_flop,
-            "avg_launch_ms": round(up_ms, 5),
-        },
+        "config": describe(case, args.config, args.permute_rows, fp8),
+        "roofline": roofline,
         "layer_tflops": round(layer_flops(case) / (ms * 1e-3) / 1e12, 2),
+        "expert_load_max_over_mean": round(load_ratio, 3),
         "stages_ms": stage,
     }
     if not args.no_cpu_baseline:

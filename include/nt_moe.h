@@ -176,6 +176,49 @@ int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                              void* workspace, size_t workspace_bytes, nt_moe_stream_t stream);
 
 /*
+ * FP8 path (OCP E4M3FN, the format of gfx950's matrix cores). The reference has no fp8
+ * experts -- its MasterLinear runs bf16/fp32 matmuls (megatron_moe.py:58-78) -- so these entry
+ * points are the fp8 variant of the same expert computation (megatron_moe.py:145) for the
+ * memory-bound small-batch regime, scored against the fp32 computation on dequantised values.
+ *
+ * Row-wise quantisation of activations: per row, s = amax(|row|) / 448 (1 for an all-zero
+ * row), q = e4m3(v / s) rounded to nearest even.
+ *   x      bf16 [rows, ld_x], d used columns (d % 8 == 0, ld_x % 8 == 0)
+ *   q      e4m3 [rows, ld_q] (ld_q >= d, ld_q % 8 == 0);  scale fp32 [rows]
+ */
+int nt_moe_quantize_fp8_rowwise(const uint16_t* x, int64_t ld_x, int64_t rows, int32_t d,
+                                uint8_t* q, int64_t ld_q, float* scale, nt_moe_stream_t stream);
+
+/*
+ * Block-wise quantisation of weights: every 128 x 128 block of each [rows, cols] matrix gets
+ * s = amax(|block|) / 448 (1 for an all-zero block) and q = e4m3(v / s).
+ *   w      fp32 [num_matrices, rows, cols] (rows % 128 == 0, cols % 128 == 0)
+ *   q      e4m3 [num_matrices, rows, cols];  scale fp32 [num_matrices, rows/128, cols/128]
+ */
+int nt_moe_quantize_fp8_blockwise(const float* w, int64_t num_matrices, int32_t rows,
+                                  int32_t cols, uint8_t* q, float* scale, nt_moe_stream_t stream);
+
+/*
+ * Grouped GEMM on e4m3 operands with fp32 scales, over ragged segments:
+ *   c[r, j] = epilogue( a_scale[i] * sum_kb w_scale[s, row/128, kb] *
+ *                       sum_{k in [128 kb, 128 kb + 128)} a[i, k] * w[s, row, k] )
+ * with i = src_row[r] when given (gather fused into the load, clamped to [0, a_rows)), else r;
+ * `row` is j for NONE/RELU2, and j (gate) and n_out + j (value) for SWIGLU.
+ *   a        e4m3 [a_rows, ld_a] (ld_a % 32 == 0), a_scale fp32 [a_rows]
+ *   w        e4m3 [num_segments, R, K], R = 2 n_out (SWIGLU) or n_out, R % 128 == 0
+ *   w_scale  fp32 [num_segments, R/128, K/128]
+ *   c        bf16 [total_rows, n_out]
+ * Requirements: K % 128 == 0; n_out % 64 == 0 (SWIGLU) or n_out % 128 == 0; 32-byte aligned
+ * a and w; 8-byte aligned c. The kernel streams each segment's weights once per 32 rows of the
+ * segment: it is the right tool when segments are short (decode, small batches).
+ */
+int nt_moe_grouped_gemm_fp8(const uint8_t* a, int64_t ld_a, int64_t a_rows, const float* a_scale,
+                            const int32_t* src_row, const int32_t* seg_offsets,
+                            int32_t num_segments, int64_t total_rows, const uint8_t* w,
+                            const float* w_scale, int32_t K, int32_t n_out, int32_t epilogue,
+                            uint16_t* c, nt_moe_stream_t stream);
+
+/*
  * Deterministic weighted combine plus the load-balance and z auxiliary losses.
  *   out[t] = sum over j in ascending expert order of combine_w[t,j] * y[combine_dest[t,j]]
  *            (+ shared_y[t] when given), accumulated in fp32, rounded once to bf16.

@@ -39,6 +39,10 @@ SIGNATURES = {
                                        _i32, _p, _p, _p, _sz, _p]),
     "nt_moe_grouped_gemm_bf16": (_i32, [_p, _i64, _i64, _p, _p, _i32, _i64, _p, _i32, _i32, _i32,
                                         _p, _p, _sz, _p]),
+    "nt_moe_quantize_fp8_rowwise": (_i32, [_p, _i64, _i64, _i32, _p, _i64, _p, _p]),
+    "nt_moe_quantize_fp8_blockwise": (_i32, [_p, _i64, _i32, _i32, _p, _p, _p]),
+    "nt_moe_grouped_gemm_fp8": (_i32, [_p, _i64, _i64, _p, _p, _p, _i32, _i64, _p, _p, _i32, _i32,
+                                       _i32, _p, _p]),
     "nt_moe_combine_aux": (_i32, [_p, _p, _p, _i64, _i32, _i32, _p, _i64, _p, _i64, _p, _p, _p,
                                   _i32, _f32, _f32, _p, _p]),
 }

@@ -38,6 +38,7 @@ int launched(hipError_t err, const char* what) {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned_to(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
 
 size_t align256(size_t n) { return (n + 255) & ~size_t(255); }
 
@@ -275,6 +276,63 @@ int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                                             reinterpret_cast<int*>(workspace),
                                             reinterpret_cast<hipStream_t>(stream));
   return launched(err, "grouped_gemm_bf16");
+}
+
+int nt_moe_quantize_fp8_rowwise(const uint16_t* x, int64_t ld_x, int64_t rows, int32_t d,
+                                uint8_t* q, int64_t ld_q, float* scale, nt_moe_stream_t stream) {
+  NT_REQUIRE(rows >= 0 && rows < ((int64_t)1 << 31), "quantize_fp8_rowwise: bad row count");
+  NT_REQUIRE(d > 0 && d % 8 == 0, "quantize_fp8_rowwise: d must be a positive multiple of 8, got %d", d);
+  NT_REQUIRE(ld_x >= d && ld_x % 8 == 0 && ld_q >= d && ld_q % 8 == 0,
+             "quantize_fp8_rowwise: ld_x and ld_q must be >= d and multiples of 8");
+  if (rows == 0) return ok();
+  NT_REQUIRE(x && q && scale, "quantize_fp8_rowwise: null buffer");
+  NT_REQUIRE(aligned16(x) && aligned_to(q, 8), "quantize_fp8_rowwise: x must be 16-byte and q 8-byte aligned");
+  hipError_t err = launch_quantize_fp8_rowwise(x, ld_x, rows, d, q, ld_q, scale,
+                                               reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "quantize_fp8_rowwise");
+}
+
+int nt_moe_quantize_fp8_blockwise(const float* w, int64_t num_matrices, int32_t rows,
+                                  int32_t cols, uint8_t* q, float* scale, nt_moe_stream_t stream) {
+  NT_REQUIRE(num_matrices >= 0, "quantize_fp8_blockwise: negative matrix count");
+  NT_REQUIRE(rows > 0 && rows % 128 == 0 && cols > 0 && cols % 128 == 0,
+             "quantize_fp8_blockwise: rows and cols must be positive multiples of 128, got %d x %d",
+             rows, cols);
+  NT_REQUIRE(num_matrices * (rows / 128) * (cols / 128) < ((int64_t)1 << 31),
+             "quantize_fp8_blockwise: too many blocks");
+  if (num_matrices == 0) return ok();
+  NT_REQUIRE(w && q && scale, "quantize_fp8_blockwise: null buffer");
+  NT_REQUIRE(aligned16(w) && aligned_to(q, 4), "quantize_fp8_blockwise: w must be 16-byte and q 4-byte aligned");
+  hipError_t err = launch_quantize_fp8_blockwise(w, num_matrices, rows, cols, q, scale,
+                                                 reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "quantize_fp8_blockwise");
+}
+
+int nt_moe_grouped_gemm_fp8(const uint8_t* a, int64_t ld_a, int64_t a_rows, const float* a_scale,
+                            const int32_t* src_row, const int32_t* seg_offsets,
+                            int32_t num_segments, int64_t total_rows, const uint8_t* w,
+                            const float* w_scale, int32_t K, int32_t n_out, int32_t epilogue,
+                            uint16_t* c, nt_moe_stream_t stream) {
+  NT_REQUIRE(K > 0 && K % 128 == 0, "grouped_gemm_fp8: K must be a positive multiple of 128, got %d", K);
+  NT_REQUIRE(epilogue == NT_MOE_EPI_SWIGLU || epilogue == NT_MOE_EPI_RELU2 ||
+                 epilogue == NT_MOE_EPI_NONE, "grouped_gemm_fp8: unknown epilogue %d", epilogue);
+  NT_REQUIRE(n_out > 0 && n_out % (epilogue == NT_MOE_EPI_SWIGLU ? 64 : 128) == 0,
+             "grouped_gemm_fp8: n_out must be a positive multiple of %d, got %d",
+             epilogue == NT_MOE_EPI_SWIGLU ? 64 : 128, n_out);
+  NT_REQUIRE(num_segments >= 1 && num_segments <= NT_MOE_MAX_SEGMENTS,
+             "grouped_gemm_fp8: num_segments must be in [1, %d]", NT_MOE_MAX_SEGMENTS);
+  NT_REQUIRE(total_rows >= 0 && total_rows < ((int64_t)1 << 31), "grouped_gemm_fp8: bad total_rows");
+  NT_REQUIRE(ld_a >= K && ld_a % 32 == 0, "grouped_gemm_fp8: ld_a must be >= K and a multiple of 32");
+  NT_REQUIRE(a_rows >= 1, "grouped_gemm_fp8: a_rows must be positive");
+  NT_REQUIRE(src_row || a_rows >= total_rows, "grouped_gemm_fp8: a needs total_rows rows without src_row");
+  NT_REQUIRE(a && a_scale && seg_offsets && w && w_scale && c, "grouped_gemm_fp8: null buffer");
+  NT_REQUIRE(aligned_to(a, 32) && aligned_to(w, 32) && aligned_to(c, 8),
+             "grouped_gemm_fp8: a and w must be 32-byte aligned, c 8-byte aligned");
+  if (total_rows == 0) return ok();
+  hipError_t err = launch_grouped_gemm_fp8(a, ld_a, a_rows, a_scale, src_row, seg_offsets,
+                                           num_segments, total_rows, w, w_scale, K, n_out,
+                                           epilogue, c, reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "grouped_gemm_fp8");
 }
 
 int nt_moe_combine_aux(const uint16_t* y, const int32_t* combine_dest, const float* combine_w,

@@ -86,6 +86,17 @@ hipError_t launch_combine_aux(const uint16_t* y, const int32_t* combine_dest,
                               const int32_t* counts, int E, float aux_coeff, float z_coeff,
                               float* aux_out, hipStream_t stream);
 
+hipError_t launch_quantize_fp8_rowwise(const uint16_t* x, int64_t ld_x, int64_t rows, int d,
+                                       uint8_t* q, int64_t ld_q, float* scale, hipStream_t stream);
+hipError_t launch_quantize_fp8_blockwise(const float* w, int64_t S, int R, int C, uint8_t* q,
+                                         float* scale, hipStream_t stream);
+hipError_t launch_grouped_gemm_fp8(const uint8_t* a, int64_t ld_a, int64_t a_rows,
+                                   const float* a_scale, const int32_t* src_row,
+                                   const int32_t* seg_offsets, int num_segments,
+                                   int64_t total_rows, const uint8_t* w, const float* w_scale,
+                                   int K, int n_out, int epilogue, uint16_t* c,
+                                   hipStream_t stream);
+
 int num_cus();
 
 // Workspace of the grouped GEMM entry points: per-XCD tile claim counters.

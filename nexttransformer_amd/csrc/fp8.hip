@@ -1,0 +1,288 @@
+// FP8 (OCP E4M3FN) path of the MoE layer on gfx950: quantisation kernels and a block-scaled
+// grouped expert GEMM for the small-batch, weight-streaming regime.
+//
+// Numerics (the fp8 variant of SequentialMLP's expert loop, megatron_moe.py:145, with weights
+// stored as e4m3 and one fp32 scale per 128 x 128 block, activations quantised per row):
+//   row scale      s = amax(|row|) / 448 (1 for an all-zero row); q = e4m3_rne(v / s)
+//   block scale    the same per 128 x 128 block of a weight matrix
+//   GEMM           c[r, j] = epi( a_scale[row(r)] * sum_kb w_scale[s, j/128, kb] *
+//                                  sum_{k in block kb} e4m3(a[row(r), k]) * e4m3(w[s, j, k]) )
+// The inner 128-wide block sums run on v_mfma_scale_f32_32x32x64_f8f6f4 (both formats e4m3,
+// E8M0 scales fixed at 2^0) into a zeroed fp32 fragment, which is then scaled and added to the
+// fp32 accumulator: the block scales are arbitrary fp32 values, not powers of two, so they are
+// applied outside the matrix core.
+//
+// GEMM shape. The regime this kernel is for (a few rows per expert, e.g. T = 64 tokens over
+// 128 experts) is bound by streaming the weights from HBM once, so the kernel streams: a
+// workgroup owns one (segment, column tile) pair, each of its 4 waves a 32-row slice of the
+// weight matrix, and every weight byte is loaded exactly once per 32 rows of the segment. The
+// segment's activation rows (gathered through src_row) are the MFMA's B operand, read from L2.
+// A lane holds 32 consecutive K bytes of its weight row for a 64-wide K step (bytes
+// [32 * (lane / 32), +32)); the activation operand uses the same byte mapping, so whatever
+// order the matrix core assigns those bytes to, both operands agree and the dot product is
+// exact up to fp32 accumulation order. The next 128-wide K block is loaded while the current
+// one is multiplied.
+// SwiGLU tiles pair 16 gate rows with the 16 value rows of the same output columns in one MFMA
+// (A rows 0-15 gate, 16-31 value), so both land in the same lane of the accumulator layout
+// (row i of a 32 x 32 fragment sits in lane (i / 4) % 2 * 32 + column, element (i / 8) * 4 + i % 4).
+#include <math.h>
+
+#include "common.h"
+
+namespace ntmoe {
+namespace {
+
+constexpr float kE4m3Max = 448.0f;
+constexpr int kScaleBlock = 128;
+constexpr int kScaleOne = 127;  // E8M0 encoding of 2^0
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+// Four fp32 values -> four e4m3 bytes (round to nearest even), little-endian in one word.
+__device__ __forceinline__ uint32_t to_e4m3x4(float a, float b, float c, float d) {
+  int packed = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  packed = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, packed, true);
+  return (uint32_t)packed;
+}
+
+__device__ __forceinline__ float row_scale(float amax) {
+  return amax > 0.f ? amax / kE4m3Max : 1.f;
+}
+
+// One wave per row: amax over the row, then q = e4m3(v / s). d % 8 == 0.
+__global__ __launch_bounds__(256) void quantize_rowwise_kernel(
+    const uint16_t* __restrict__ x, int64_t ld_x, int64_t rows, int d, uint8_t* __restrict__ q,
+    int64_t ld_q, float* __restrict__ scale) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
+  if (row >= rows) return;
+  const int lane = lane_id();
+  const uint16_t* xr = x + row * ld_x;
+  float amax = 0.f;
+  for (int c = lane * 8; c < d; c += 512) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      amax = fmaxf(amax, fabsf(bf16_bits_to_f32(v[i] & 0xffffu)));
+      amax = fmaxf(amax, fabsf(bf16_bits_to_f32(v[i] >> 16)));
+    }
+  }
+  const float s = row_scale(wave_max(amax));
+  uint8_t* qr = q + row * ld_q;
+  for (int c = lane * 8; c < d; c += 512) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + c);
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = bf16_bits_to_f32(v[i] & 0xffffu) / s;
+      f[2 * i + 1] = bf16_bits_to_f32(v[i] >> 16) / s;
+    }
+    u32x2 out;
+    out[0] = to_e4m3x4(f[0], f[1], f[2], f[3]);
+    out[1] = to_e4m3x4(f[4], f[5], f[6], f[7]);
+    *reinterpret_cast<u32x2*>(qr + c) = out;
+  }
+  if (lane == 0) scale[row] = s;
+}
+
+// One 256-thread workgroup per 128 x 128 block of w [S, R, C] (fp32 masters).
+__global__ __launch_bounds__(256) void quantize_blockwise_kernel(
+    const float* __restrict__ w, int R, int C, uint8_t* __restrict__ q, float* __restrict__ scale) {
+  __shared__ float part[4];
+  const int cb_count = C / kScaleBlock, rb_count = R / kScaleBlock;
+  const int64_t blk = blockIdx.x;
+  const int cb = (int)(blk % cb_count);
+  const int rb = (int)((blk / cb_count) % rb_count);
+  const int64_t s = blk / ((int64_t)cb_count * rb_count);
+  const int t = threadIdx.x;
+  const int col = cb * kScaleBlock + (t & 31) * 4;  // 32 threads x 4 columns per row
+  const int64_t base = (s * R + (int64_t)rb * kScaleBlock) * C + col;
+  float amax = 0.f;
+  for (int r = t >> 5; r < kScaleBlock; r += 8) {
+    const floatx4 v = *reinterpret_cast<const floatx4*>(w + base + (int64_t)r * C);
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+  }
+  amax = wave_max(amax);
+  if (lane_id() == 0) part[wave_id()] = amax;
+  __syncthreads();
+  const float sc = row_scale(fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3])));
+  for (int r = t >> 5; r < kScaleBlock; r += 8) {
+    const floatx4 v = *reinterpret_cast<const floatx4*>(w + base + (int64_t)r * C);
+    *reinterpret_cast<uint32_t*>(q + base + (int64_t)r * C) =
+        to_e4m3x4(v[0] / sc, v[1] / sc, v[2] / sc, v[3] / sc);
+  }
+  if (t == 0) scale[blk] = sc;
+}
+
+template <int EPI>
+struct Fp8Tile {
+  // output columns per wave / per workgroup
+  static constexpr int kColsPerWave = EPI == NT_MOE_EPI_SWIGLU ? 16 : 32;
+  static constexpr int kColsPerBlock = 4 * kColsPerWave;
+};
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g * u * __builtin_amdgcn_rcpf(1.f + __expf(-g));
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void fp8_grouped_gemm_kernel(
+    const uint8_t* __restrict__ a, int64_t ld_a, int64_t a_rows, const float* __restrict__ a_scale,
+    const int32_t* __restrict__ src_row, const int32_t* __restrict__ seg_offsets,
+    int64_t total_rows, const uint8_t* __restrict__ w, const float* __restrict__ w_scale, int K,
+    int n_out, int n_tiles, uint16_t* __restrict__ c) {
+  using Tile = Fp8Tile<EPI>;
+  const int seg = blockIdx.x / n_tiles;
+  const int tile = blockIdx.x - seg * n_tiles;
+  int64_t lo = seg_offsets[seg], hi = seg_offsets[seg + 1];
+  lo = lo < 0 ? 0 : (lo > total_rows ? total_rows : lo);
+  hi = hi < lo ? lo : (hi > total_rows ? total_rows : hi);
+  if (hi <= lo) return;
+  const int wave = wave_id(), lane = lane_id();
+  const int li = lane & 31, half = lane >> 5;
+  const int col0 = tile * Tile::kColsPerBlock + wave * Tile::kColsPerWave;
+  if (col0 >= n_out) return;  // no barriers below: a wave past the last column just leaves
+
+  const int w_rows = EPI == NT_MOE_EPI_SWIGLU ? 2 * n_out : n_out;
+  const int scale_rows = (w_rows + kScaleBlock - 1) / kScaleBlock;
+  const int kblocks = K / kScaleBlock;
+  int wrow;
+  if (EPI == NT_MOE_EPI_SWIGLU)
+    wrow = li < 16 ? col0 + li : n_out + col0 + (li - 16);
+  else
+    wrow = col0 + li;
+  const bool wvalid = EPI == NT_MOE_EPI_SWIGLU ? (col0 + (li & 15) < n_out) : (wrow < n_out);
+  const uint8_t* wp = w + ((int64_t)seg * w_rows + (wvalid ? wrow : col0)) * K + half * 32;
+  // scale rows of the gate (or only) half and of the value half
+  const float* ws_lo = w_scale + ((int64_t)seg * scale_rows + col0 / kScaleBlock) * kblocks;
+  const float* ws_hi =
+      EPI == NT_MOE_EPI_SWIGLU
+          ? w_scale + ((int64_t)seg * scale_rows + (n_out + col0) / kScaleBlock) * kblocks
+          : ws_lo;
+
+  for (int64_t t0 = lo; t0 < hi; t0 += 32) {
+    const int64_t tok = t0 + li;
+    const bool tvalid = tok < hi;
+    int64_t arow = tok;
+    if (src_row) arow = tvalid ? (int64_t)src_row[tok] : 0;
+    arow = arow < 0 ? 0 : (arow >= a_rows ? a_rows - 1 : arow);
+    const uint8_t* ap = a + arow * ld_a + half * 32;
+
+    const i32x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+    i32x8 wa0 = *reinterpret_cast<const i32x8*>(wp);
+    i32x8 wa1 = *reinterpret_cast<const i32x8*>(wp + 64);
+    i32x8 xb0 = tvalid ? *reinterpret_cast<const i32x8*>(ap) : zero8;
+    i32x8 xb1 = tvalid ? *reinterpret_cast<const i32x8*>(ap + 64) : zero8;
+    floatx16 acc = {};
+    for (int kb = 0; kb < kblocks; ++kb) {
+      i32x8 nwa0 = wa0, nwa1 = wa1, nxb0 = xb0, nxb1 = xb1;
+      if (kb + 1 < kblocks) {
+        const int64_t off = (int64_t)(kb + 1) * kScaleBlock;
+        nwa0 = *reinterpret_cast<const i32x8*>(wp + off);
+        nwa1 = *reinterpret_cast<const i32x8*>(wp + off + 64);
+        nxb0 = tvalid ? *reinterpret_cast<const i32x8*>(ap + off) : zero8;
+        nxb1 = tvalid ? *reinterpret_cast<const i32x8*>(ap + off + 64) : zero8;
+      }
+      floatx16 part = {};
+      part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wa0, xb0, part, 0, 0, 0, kScaleOne, 0,
+                                                             kScaleOne);
+      part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wa1, xb1, part, 0, 0, 0, kScaleOne, 0,
+                                                             kScaleOne);
+      const float s_lo = ws_lo[kb], s_hi = ws_hi[kb];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] = fmaf(part[i], i < 8 ? s_lo : s_hi, acc[i]);
+      wa0 = nwa0;
+      wa1 = nwa1;
+      xb0 = nxb0;
+      xb1 = nxb1;
+    }
+    if (!tvalid) continue;
+    const float as = a_scale[arow];
+    uint16_t* crow = c + tok * n_out;
+    if (EPI == NT_MOE_EPI_SWIGLU) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int col = col0 + 8 * g + 4 * half;
+        if (col >= n_out) continue;
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = silu_mul(as * acc[4 * g + r], as * acc[4 * (g + 2) + r]);
+        u32x2 v;
+        v[0] = pack_bf16x2(o[0], o[1]);
+        v[1] = pack_bf16x2(o[2], o[3]);
+        *reinterpret_cast<u32x2*>(crow + col) = v;
+      }
+    } else {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int col = col0 + 8 * g + 4 * half;
+        if (col >= n_out) continue;
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = as * acc[4 * g + r];
+          if (EPI == NT_MOE_EPI_RELU2) v = v > 0.f ? v * v : 0.f;
+          o[r] = v;
+        }
+        u32x2 v;
+        v[0] = pack_bf16x2(o[0], o[1]);
+        v[1] = pack_bf16x2(o[2], o[3]);
+        *reinterpret_cast<u32x2*>(crow + col) = v;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_quantize_fp8_rowwise(const uint16_t* x, int64_t ld_x, int64_t rows, int d,
+                                       uint8_t* q, int64_t ld_q, float* scale, hipStream_t stream) {
+  if (rows == 0) return hipSuccess;
+  quantize_rowwise_kernel<<<dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream>>>(
+      x, ld_x, rows, d, q, ld_q, scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_fp8_blockwise(const float* w, int64_t S, int R, int C, uint8_t* q,
+                                         float* scale, hipStream_t stream) {
+  const int64_t blocks = S * (R / kScaleBlock) * (C / kScaleBlock);
+  if (blocks == 0) return hipSuccess;
+  quantize_blockwise_kernel<<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(w, R, C, q, scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_grouped_gemm_fp8(const uint8_t* a, int64_t ld_a, int64_t a_rows,
+                                   const float* a_scale, const int32_t* src_row,
+                                   const int32_t* seg_offsets, int num_segments,
+                                   int64_t total_rows, const uint8_t* w, const float* w_scale,
+                                   int K, int n_out, int epilogue, uint16_t* c,
+                                   hipStream_t stream) {
+  const int per_block = epilogue == NT_MOE_EPI_SWIGLU ? Fp8Tile<NT_MOE_EPI_SWIGLU>::kColsPerBlock
+                                                      : Fp8Tile<NT_MOE_EPI_NONE>::kColsPerBlock;
+  const int n_tiles = ceil_div(n_out, per_block);
+  const dim3 grid((unsigned)((int64_t)num_segments * n_tiles)), block(256);
+  if (total_rows == 0) return hipSuccess;
+  switch (epilogue) {
+    case NT_MOE_EPI_SWIGLU:
+      fp8_grouped_gemm_kernel<NT_MOE_EPI_SWIGLU><<<grid, block, 0, stream>>>(
+          a, ld_a, a_rows, a_scale, src_row, seg_offsets, total_rows, w, w_scale, K, n_out,
+          n_tiles, c);
+      break;
+    case NT_MOE_EPI_RELU2:
+      fp8_grouped_gemm_kernel<NT_MOE_EPI_RELU2><<<grid, block, 0, stream>>>(
+          a, ld_a, a_rows, a_scale, src_row, seg_offsets, total_rows, w, w_scale, K, n_out,
+          n_tiles, c);
+      break;
+    default:
+      fp8_grouped_gemm_kernel<NT_MOE_EPI_NONE><<<grid, block, 0, stream>>>(
+          a, ld_a, a_rows, a_scale, src_row, seg_offsets, total_rows, w, w_scale, K, n_out,
+          n_tiles, c);
+      break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace ntmoe

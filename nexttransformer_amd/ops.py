@@ -236,6 +236,91 @@ def _(a, src_row, seg_offsets, w, epilogue, total_rows):
 
 
 # ---------------------------------------------------------------------------------------------
+# fp8 (OCP e4m3fn bytes held in uint8 tensors)
+
+@torch.library.custom_op("ntmoe::quantize_fp8_rowwise", mutates_args=())
+def quantize_fp8_rowwise(x: Tensor) -> tuple[Tensor, Tensor]:
+    """(q uint8 [rows, d] e4m3 codes, scale fp32 [rows]) with s = amax / 448 per row."""
+    _on_gpu(x)
+    _require(x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1,
+             "quantize_fp8_rowwise: x must be bf16 [rows, d] with contiguous rows")
+    rows, d = x.shape
+    # rows of q stay 32-byte aligned for the fp8 GEMM's 32-byte operand loads
+    _require(d % 32 == 0, "quantize_fp8_rowwise: d must be a multiple of 32")
+    q = torch.empty(rows, d, device=x.device, dtype=torch.uint8)
+    scale = torch.empty(rows, device=x.device, dtype=torch.float32)
+    st = nat.load().nt_moe_quantize_fp8_rowwise(ptr(x), x.stride(0), rows, d, ptr(q), d,
+                                                ptr(scale), _stream(x.device))
+    nat.check(st, "ntmoe::quantize_fp8_rowwise")
+    return q, scale
+
+
+@quantize_fp8_rowwise.register_fake
+def _(x):
+    rows, d = x.shape
+    return (x.new_empty((rows, d), dtype=torch.uint8), x.new_empty((rows,), dtype=torch.float32))
+
+
+@torch.library.custom_op("ntmoe::quantize_fp8_blockwise", mutates_args=())
+def quantize_fp8_blockwise(w: Tensor) -> tuple[Tensor, Tensor]:
+    """(q uint8 [S, R, C] e4m3 codes, scale fp32 [S, R/128, C/128]) of fp32 w [S, R, C]."""
+    _on_gpu(w)
+    _require(w.dtype == torch.float32 and w.dim() == 3 and w.is_contiguous(),
+             "quantize_fp8_blockwise: w must be contiguous fp32 [S, R, C]")
+    S, R, C = w.shape
+    q = torch.empty(S, R, C, device=w.device, dtype=torch.uint8)
+    scale = torch.empty(S, R // 128, C // 128, device=w.device, dtype=torch.float32)
+    st = nat.load().nt_moe_quantize_fp8_blockwise(ptr(w), S, R, C, ptr(q), ptr(scale),
+                                                  _stream(w.device))
+    nat.check(st, "ntmoe::quantize_fp8_blockwise")
+    return q, scale
+
+
+@quantize_fp8_blockwise.register_fake
+def _(w):
+    S, R, C = w.shape
+    return (w.new_empty((S, R, C), dtype=torch.uint8),
+            w.new_empty((S, R // 128, C // 128), dtype=torch.float32))
+
+
+@torch.library.custom_op("ntmoe::grouped_gemm_fp8", mutates_args=())
+def grouped_gemm_fp8(a: Tensor, a_scale: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor,
+                     w: Tensor, w_scale: Tensor, epilogue: int, total_rows: int) -> Tensor:
+    """c bf16 [rows, n_out] = epilogue(a_scale . sum_kb w_scale . (a_q . w_q^T)_kb) per segment."""
+    _on_gpu(a, a_scale, src_row, seg_offsets, w, w_scale)
+    _require(a.dtype == torch.uint8 and a.dim() == 2 and a.stride(1) == 1,
+             "grouped_gemm_fp8: a must be uint8 (e4m3) [*, K] with contiguous rows")
+    _require(w.dtype == torch.uint8 and w.dim() == 3 and w.is_contiguous(),
+             "grouped_gemm_fp8: w must be contiguous uint8 (e4m3) [S, R, K]")
+    S, R, K = w.shape
+    n_out = R // 2 if epilogue == nat.EPI_SWIGLU else R
+    _require(a.shape[1] == K, "grouped_gemm_fp8: a and w disagree on K")
+    _require(a_scale.dtype == torch.float32 and a_scale.shape == (a.shape[0],)
+             and a_scale.is_contiguous(), "grouped_gemm_fp8: a_scale must be fp32 [a_rows]")
+    _require(w_scale.dtype == torch.float32 and w_scale.shape == (S, R // 128, K // 128)
+             and w_scale.is_contiguous(), "grouped_gemm_fp8: w_scale must be fp32 [S, R/128, K/128]")
+    _require(seg_offsets.dtype == torch.int32 and seg_offsets.shape == (S + 1,)
+             and seg_offsets.is_contiguous(), "grouped_gemm_fp8: seg_offsets must be int32 [S+1]")
+    if src_row is not None:
+        _require(src_row.dtype == torch.int32 and src_row.is_contiguous(),
+                 "grouped_gemm_fp8: src_row must be contiguous int32")
+    c = torch.empty(total_rows, n_out, device=a.device, dtype=torch.bfloat16)
+    st = nat.load().nt_moe_grouped_gemm_fp8(ptr(a), a.stride(0), a.shape[0], ptr(a_scale),
+                                            ptr(src_row), ptr(seg_offsets), S, total_rows, ptr(w),
+                                            ptr(w_scale), K, n_out, epilogue, ptr(c),
+                                            _stream(a.device))
+    nat.check(st, "ntmoe::grouped_gemm_fp8")
+    return c
+
+
+@grouped_gemm_fp8.register_fake
+def _(a, a_scale, src_row, seg_offsets, w, w_scale, epilogue, total_rows):
+    R = w.shape[1]
+    return a.new_empty((total_rows, R // 2 if epilogue == nat.EPI_SWIGLU else R),
+                       dtype=torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------------------------
 # combine + aux
 
 @torch.library.custom_op("ntmoe::combine_aux", mutates_args=())
@@ -281,6 +366,7 @@ def _(y, combine_dest, combine_w, shared_y, prob_partial, z_partial, counts, aux
 def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
                 activation=nat.ACT_SWIGLU, aux_coeff=0.01, z_coeff=0.001, logit_bias=None,
                 shared_w1=None, shared_w2=None, want_logits=False, permute_rows=False,
+                w1_scale=None, w2_scale=None, shared_w1_scale=None, shared_w2_scale=None,
                 mark=None):
     """The MoE layer forward on the GPU: router -> route plan -> grouped GEMMs -> combine + aux.
 
@@ -289,6 +375,9 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
     Returns (out [T, d] bf16, aux fp32 [3] = {lb + z, lb, z}, state with the routing tensors).
     With permute_rows the token rows are first moved into expert order by the permute kernel
     (x_perm); by default the up-projection GEMM gathers them itself.
+    fp8 experts: pass w1/w2 (and the shared expert's) as uint8 e4m3 codes with their 128 x 128
+    block scales (w*_scale, from quantize_fp8_blockwise); the token rows and the intermediate
+    h are then quantised per row and both projections run on the fp8 grouped GEMM.
     `mark(name)`, when given, is called after each stage is enqueued (used to place timing
     events on the stream).
     """
@@ -312,6 +401,30 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
         ids, w, E, x if permute_rows else None, permute_rows)
     mark("route_plan")
     up_epi = nat.EPI_SWIGLU if activation == nat.ACT_SWIGLU else nat.EPI_RELU2
+    if w1.dtype == torch.uint8:
+        _require(w1_scale is not None and w2_scale is not None,
+                 "moe_forward: fp8 weights need w1_scale and w2_scale")
+        xq, xs = quantize_fp8_rowwise(x)
+        mark("quantize")
+        h = grouped_gemm_fp8(xq, xs, src, offsets, w1, w1_scale, up_epi, A)
+        mark("gemm_up")
+        hq, hs = quantize_fp8_rowwise(h)
+        y = grouped_gemm_fp8(hq, hs, None, offsets, w2, w2_scale, nat.EPI_NONE, A)
+        mark("gemm_down")
+        shared_y = None
+        if shared_w1 is not None:
+            seg = torch.tensor([0, T], device=x.device, dtype=torch.int32)
+            hs_ = grouped_gemm_fp8(xq, xs, None, seg, shared_w1, shared_w1_scale, up_epi, T)
+            hsq, hss = quantize_fp8_rowwise(hs_)
+            shared_y = grouped_gemm_fp8(hsq, hss, None, seg, shared_w2, shared_w2_scale,
+                                        nat.EPI_NONE, T)
+            mark("shared")
+        out, aux = combine_aux(y, cdest, cw, shared_y, pp, zp, counts, aux_coeff, z_coeff)
+        mark("combine")
+        state = dict(logits=logits, ids=ids, weights=w, counts=counts, offsets=offsets,
+                     src_row=src, perm_w=perm_w, combine_dest=cdest, combine_w=cw, x_q=xq,
+                     x_scale=xs)
+        return out, aux, state
     if permute_rows:
         h = grouped_gemm(x_perm, None, offsets, w1, up_epi, A)
     else:

@@ -231,6 +231,50 @@ def dequantize_blockwise(q, scale, block=128):
     return (v * scale[..., :, None, :, None]).reshape(*lead, R, C)
 
 
+def dequantize_rowwise(q, scale):
+    return e4m3_decode(q) * scale.float()[:, None]
+
+
+def moe_forward_fp8(x, router, w1q, w1s, w2q, w2s, k, *, score_fn=SOFTMAX, activation=SWIGLU,
+                    aux_coeff=0.01, z_coeff=0.001, bias=None, tokens=None):
+    """The fp8 layer on the CPU, the fp32 dequantised reference of the fp8 path.
+
+    Routing as moe_forward (fp32 router on the bf16 hidden states). Each token row is quantised
+    per row to e4m3 (quantize_rowwise) and dequantised; expert weights are the dequantised
+    128 x 128-block e4m3 weights; fc1 and the activation run in fp32, h is rounded to bf16 (the
+    dtype the GPU path stores it in), quantised per row, dequantised, and fc2 runs in fp32;
+    outputs are weighted after fc2 and accumulated in ascending expert order.
+    The weight tensors may live on any device; only the experts in use are copied to the CPU.
+    With `tokens`, out holds only those tokens' rows (each token's output depends on its own
+    row and routing alone).
+    """
+    x = x.detach().cpu()
+    logits = router_logits_fixed(x, router, bias)
+    E = router.shape[0]
+    ids, topw = topk(logits, k, score_fn)
+    counts, offsets, src, dest = route_plan(ids, E)
+    xq, xs = quantize_rowwise(x.float())
+    sel = torch.arange(x.shape[0]) if tokens is None else torch.as_tensor(tokens, dtype=torch.long)
+    rows = dequantize_rowwise(xq[sel], xs[sel])
+    out = torch.zeros(len(sel), x.shape[1], dtype=torch.float32)
+    ids64 = ids.long()[sel]
+    topw_sel = topw[sel]
+    H = w2q.shape[2]
+    for e in range(E):
+        token, slot = torch.where(ids64 == e)
+        if not token.numel():
+            continue
+        w1 = dequantize_blockwise(w1q[e].cpu(), w1s[e].cpu())
+        w2 = dequantize_blockwise(w2q[e].cpu(), w2s[e].cpu())
+        h = act(rows[token] @ w1.t(), activation, H).to(torch.bfloat16).float()
+        hq, hs = quantize_rowwise(h)
+        y = dequantize_rowwise(hq, hs) @ w2.t()
+        out.index_add_(0, token, y * topw_sel[token, slot, None])
+    lb, z = aux_losses(logits, counts, k, aux_coeff, z_coeff, score_fn)
+    return dict(out=out, aux=lb + z, lb=lb, z=z, logits=logits, ids=ids, weights=topw,
+                counts=counts, offsets=offsets, src_row=src, dest=dest, x_q=xq, x_scale=xs)
+
+
 def tflops(T, d, E, k, H, shared_H=0):
     """Algorithmic FLOP of one forward: router 2TdE + routed 6TkdH + shared 6TdHs."""
     return 2 * T * d * E + 6 * T * k * d * H + 6 * T * d * shared_H
