@@ -176,6 +176,28 @@ int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                              void* workspace, size_t workspace_bytes, nt_moe_stream_t stream);
 
 /*
+ * Packed-weight variant of the grouped GEMM. nt_moe_pack_expert_weights_bf16 rearranges
+ * w [num_segments, rows, K] once (same bytes, fragment order: 32-row x 64-K blocks in which
+ * each lane's 16-byte operand chunk is contiguous with its neighbours'); the packed GEMM then
+ * streams each wave's weights straight into registers and stages only the token rows in LDS.
+ * `epilogue` must be the one the packed weights will be used with (for SWIGLU the gate and value
+ * rows of the same output columns are packed together). No counterpart in the reference beyond
+ * the expert loop it replaces (megatron_moe.py:145).
+ *   pack:  w bf16 [num_segments, rows, K] -> packed bf16 [num_segments, rows, K] (same size)
+ *          rows % 32 == 0 (rows = 2 n_out for SWIGLU), K % 64 == 0
+ *   gemm:  as nt_moe_grouped_gemm_bf16 with w = packed weights; K % 128 == 0 and K >= 256;
+ *          n_out % 16 == 0 (SWIGLU) or % 32; total_rows * n_out * 2 < 2^31.
+ */
+int nt_moe_pack_expert_weights_bf16(const uint16_t* w, int64_t num_segments, int32_t rows,
+                                    int32_t K, int32_t epilogue, uint16_t* packed,
+                                    nt_moe_stream_t stream);
+int nt_moe_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                    const int32_t* src_row, const int32_t* seg_offsets,
+                                    int32_t num_segments, int64_t total_rows,
+                                    const uint16_t* w_packed, int32_t K, int32_t n_out,
+                                    int32_t epilogue, uint16_t* c, nt_moe_stream_t stream);
+
+/*
  * FP8 path (OCP E4M3FN, the format of gfx950's matrix cores). The reference has no fp8
  * experts -- its MasterLinear runs bf16/fp32 matmuls (megatron_moe.py:58-78) -- so these entry
  * points are the fp8 variant of the same expert computation (megatron_moe.py:145) for the

@@ -267,6 +267,8 @@ int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
   int rc = check_gemm_extent(a_rows, ld_a,
                              epilogue == NT_MOE_EPI_SWIGLU ? (int64_t)2 * n_out : n_out, K);
   if (rc) return rc;
+  NT_REQUIRE(total_rows * n_out * 2 < ((int64_t)1 << 31),
+             "grouped_gemm: the output must stay below 2 GiB");
   if (!workspace || workspace_bytes < kGemmWorkspaceBytes)
     return fail(NT_MOE_ENOSPC, "grouped_gemm: workspace %zu < %zu bytes", workspace_bytes,
                 kGemmWorkspaceBytes);
@@ -276,6 +278,57 @@ int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                                             reinterpret_cast<int*>(workspace),
                                             reinterpret_cast<hipStream_t>(stream));
   return launched(err, "grouped_gemm_bf16");
+}
+
+int nt_moe_pack_expert_weights_bf16(const uint16_t* w, int64_t num_segments, int32_t rows,
+                                    int32_t K, int32_t epilogue, uint16_t* packed,
+                                    nt_moe_stream_t stream) {
+  NT_REQUIRE(epilogue == NT_MOE_EPI_SWIGLU || epilogue == NT_MOE_EPI_RELU2 ||
+                 epilogue == NT_MOE_EPI_NONE, "pack_expert_weights: unknown epilogue %d", epilogue);
+  NT_REQUIRE(num_segments >= 0 && rows > 0 && rows % 32 == 0 && K > 0 && K % 64 == 0,
+             "pack_expert_weights: rows must be a multiple of 32 and K of 64, got %d x %d", rows, K);
+  NT_REQUIRE(epilogue != NT_MOE_EPI_SWIGLU || rows % 64 == 0,
+             "pack_expert_weights: SwiGLU rows (2 n_out) must be a multiple of 64");
+  if (num_segments == 0) return ok();
+  NT_REQUIRE(w && packed && aligned16(w) && aligned16(packed),
+             "pack_expert_weights: null or unaligned buffer");
+  hipError_t err = launch_pack_weights_bf16(w, num_segments, rows, K, epilogue, packed,
+                                            reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "pack_expert_weights_bf16");
+}
+
+int nt_moe_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                    const int32_t* src_row, const int32_t* seg_offsets,
+                                    int32_t num_segments, int64_t total_rows,
+                                    const uint16_t* w_packed, int32_t K, int32_t n_out,
+                                    int32_t epilogue, uint16_t* c, nt_moe_stream_t stream) {
+  NT_REQUIRE(K >= packed_gemm_min_k() && K % 128 == 0,
+             "grouped_gemm_packed: K must be a multiple of 128 and >= %d, got %d",
+             packed_gemm_min_k(), K);
+  NT_REQUIRE(epilogue == NT_MOE_EPI_SWIGLU || epilogue == NT_MOE_EPI_RELU2 ||
+                 epilogue == NT_MOE_EPI_NONE, "grouped_gemm_packed: unknown epilogue %d", epilogue);
+  NT_REQUIRE(n_out > 0 && n_out % (epilogue == NT_MOE_EPI_SWIGLU ? 16 : 32) == 0,
+             "grouped_gemm_packed: n_out must be a positive multiple of %d, got %d",
+             epilogue == NT_MOE_EPI_SWIGLU ? 16 : 32, n_out);
+  NT_REQUIRE(num_segments >= 1 && num_segments <= NT_MOE_MAX_SEGMENTS,
+             "grouped_gemm_packed: num_segments must be in [1, %d]", NT_MOE_MAX_SEGMENTS);
+  NT_REQUIRE(total_rows >= 0 && total_rows * n_out * 2 < ((int64_t)1 << 31),
+             "grouped_gemm_packed: the output must stay below 2 GiB");
+  NT_REQUIRE(ld_a >= K && ld_a % 8 == 0, "grouped_gemm_packed: ld_a must be >= K and a multiple of 8");
+  NT_REQUIRE(a_rows >= 1, "grouped_gemm_packed: a_rows must be positive");
+  NT_REQUIRE(src_row || a_rows >= total_rows,
+             "grouped_gemm_packed: a needs total_rows rows without src_row");
+  NT_REQUIRE(a && seg_offsets && w_packed && c, "grouped_gemm_packed: null buffer");
+  NT_REQUIRE(aligned16(a) && aligned16(w_packed) && aligned_to(c, 8),
+             "grouped_gemm_packed: a and w_packed must be 16-byte aligned, c 8-byte aligned");
+  int rc = check_gemm_extent(a_rows, ld_a, 0, 0);
+  if (rc) return rc;
+  if (total_rows == 0) return ok();
+  hipError_t err = launch_grouped_gemm_bf16_packed(a, ld_a, a_rows, src_row, seg_offsets,
+                                                   num_segments, total_rows, w_packed, K, n_out,
+                                                   epilogue, c,
+                                                   reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "grouped_gemm_bf16_packed");
 }
 
 int nt_moe_quantize_fp8_rowwise(const uint16_t* x, int64_t ld_x, int64_t rows, int32_t d,

@@ -97,6 +97,15 @@ hipError_t launch_grouped_gemm_fp8(const uint8_t* a, int64_t ld_a, int64_t a_row
                                    int K, int n_out, int epilogue, uint16_t* c,
                                    hipStream_t stream);
 
+hipError_t launch_pack_weights_bf16(const uint16_t* w, int64_t S, int R, int K, int epilogue,
+                                    uint16_t* packed, hipStream_t stream);
+hipError_t launch_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                           const int32_t* src_row, const int32_t* seg_offsets,
+                                           int num_segments, int64_t total_rows,
+                                           const uint16_t* wp, int K, int n_out, int epilogue,
+                                           uint16_t* c, hipStream_t stream);
+int packed_gemm_min_k();
+
 int num_cus();
 
 // Workspace of the grouped GEMM entry points: per-XCD tile claim counters.

@@ -1,0 +1,444 @@
+// Grouped expert GEMM on bf16 MFMA with the expert weights pre-packed in fragment order.
+//
+// Same computation as grouped_gemm.hip (SequentialMLP's per-expert fc1/fc2, megatron_moe.py:145,
+// over MasterLinear, :58-78, with the SwiGLU / ReLU^2 epilogue fused):
+//   c[r, j] = epilogue(a_src(r) . w_s[j, :])   for every row r of segment s.
+// What changes is how the two operands reach the matrix cores:
+//   * token rows (A, gathered through src_row for the up projection) are shared by all 8 waves
+//     of a workgroup, so they go through LDS, in a ring of 4 stages that the loads fill three
+//     K steps ahead (direct-to-LDS loads, XOR-swizzled so fragment reads are conflict-free);
+//   * expert weights are not shared between waves (wave w owns weight rows [32 w, 32 w + 32) of
+//     the 256-row tile), so they skip LDS: each wave streams its own 4 KB per K step into
+//     registers, one K step ahead. The weights are packed once (pack kernel below) so that the
+//     16-byte fragment chunk of lane l for K slice q sits at offset (q * 64 + l) * 16 of a 4 KB
+//     block: every weight load instruction reads 1 KB of consecutive bytes.
+// K order. Inside a 64-wide K step, lane half h of both operands holds K elements
+// [32 h + 8 q, +8) for MFMA slice q (instead of [16 q + 8 h, +8)): the same permutation on both
+// operands, so each product still pairs equal K indices and the 4 slices cover the step.
+// Tile: 256 tokens x 256 weight rows x 64 K, 8 waves in a 1 x 8 layout; a wave computes 8
+// 32 x 32 accumulators (its 32 weight rows against the 256 tokens). For SwiGLU a wave's 32
+// rows are 16 gate rows and the 16 value rows of the same output columns (packed together), so
+// gate and value of an output land in the same lane (elements 4 g + r and 4 (g + 2) + r).
+// Scheduling: persistent workgroups walk an XCD-contiguous share of the (segment, m, n) tile
+// list, as the unpacked kernel does. The load pipeline runs across tile boundaries; the gather
+// indices of the next tile go into an LDS table four K steps before they are needed, so the
+// in-order completion of vector memory operations already guarantees them when they are read.
+// Waits count outstanding vector memory operations (loads and stores retire in order on this
+// GPU family): the issue order per K step g is B(g + 1) (weights, registers), then A(g + 3)
+// (token rows, LDS), then at the end of a tile the epilogue's fixed number of stores.
+#include <math.h>
+#include <type_traits>
+
+#include "common.h"
+
+namespace ntmoe {
+namespace {
+
+typedef __attribute__((address_space(1))) void gvoid;
+typedef __attribute__((address_space(3))) void lvoid;
+
+constexpr int kBufferWord3 = 0x00020000;
+
+constexpr int kBM = 256;           // tokens per tile
+constexpr int kBK = 64;            // K per step
+constexpr int kSA = 4;             // LDS stages of token rows
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kRB = kBK * 2;       // bytes per staged token row
+constexpr int kCH = kRB / 16;      // 16-byte chunks per row (8)
+constexpr int kWIN = 256 / kRB;    // rows per 256-byte bank window (2)
+constexpr int kRPI = 64 / kCH;     // rows per load instruction (8)
+constexpr int kAQ = kBM / kRPI / kWaves;  // A load instructions per wave per stage (4)
+constexpr int kStage = kBM * kRB;  // 32 KB
+constexpr int kBlockElems = 32 * kBK;  // packed weight block (32 rows x 64 K) = 2048 bf16
+constexpr int kMinK = 4 * kBK;     // the gather table needs four K steps of lead
+
+template <int EPI>
+struct Ep {
+  static constexpr int kGroups = EPI == NT_MOE_EPI_SWIGLU ? 2 : 4;  // 4-column stores per tile
+  static constexpr int kStores = 8 * kGroups;                       // per wave per tile
+};
+
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row / kWIN) % kCH); }
+
+// Workgroup barrier without a memory fence (a fence would wait for every outstanding load). The
+// LDS reads of the previous K step are complete first (their results are already consumed), so
+// the slot they read may be refilled once every wave is past the barrier.
+__device__ __forceinline__ void barrier_nofence() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+struct Tile {
+  int s, nt, m0, seg_end;
+};
+
+template <int EPI, bool GATHER>
+__global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
+    const uint16_t* __restrict__ A, int64_t ld_a, const int32_t* __restrict__ src_row,
+    const int32_t* __restrict__ seg_offsets, int S, int total_rows, int64_t a_rows,
+    const uint16_t* __restrict__ Wp, int K, int n_out, uint16_t* __restrict__ Cout) {
+  constexpr int ST = Ep<EPI>::kStores;
+  extern __shared__ __align__(16) unsigned char smem[];
+  int* src_tab = reinterpret_cast<int*>(smem + kSA * kStage);  // [2][kBM]
+  int* src_dummy = src_tab + 2 * kBM;                           // [kWaves][64] sink
+  int* tile_prefix = src_dummy + kWaves * 64;                   // [S+1]
+  int* seg_lo = tile_prefix + (S + 1);                          // [S+1]
+
+  const int lane = lane_id(), wave = wave_id();
+  const int NB = (EPI == NT_MOE_EPI_SWIGLU ? 2 * n_out : n_out) / 32;  // packed 32-row blocks
+  const int n_tiles = (NB + kWaves - 1) / kWaves;
+  const int nk = K / kBK;
+  __builtin_assume(nk >= kMinK / kBK && nk % 2 == 0);  // the launcher guarantees both
+
+  // Segment table and tile prefix (as in the unpacked kernel): clamped, non-decreasing.
+  for (int i = threadIdx.x; i <= S; i += blockDim.x) {
+    int o = seg_offsets[i];
+    seg_lo[i] = o < 0 ? 0 : (o > total_rows ? total_rows : o);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    int run_max = 0, run_tiles = 0;
+    for (int base = 0; base <= S; base += 64) {
+      const int i = base + lane;
+      int o = i <= S ? seg_lo[i] : total_rows;
+      for (int w = 1; w < 64; w <<= 1) {
+        int u = __shfl_up(o, w);
+        if (lane >= w) o = o > u ? o : u;
+      }
+      o = o > run_max ? o : run_max;
+      int prev = __shfl_up(o, 1);
+      if (lane == 0) prev = run_max;
+      int t = i >= 1 && i <= S ? ((o - prev + kBM - 1) / kBM) * n_tiles : 0;
+      for (int w = 1; w < 64; w <<= 1) {
+        int u = __shfl_up(t, w);
+        if (lane >= w) t += u;
+      }
+      if (i <= S) {
+        seg_lo[i] = o;
+        tile_prefix[i] = run_tiles + t;
+      }
+      run_max = __shfl(o, 63);
+      run_tiles += __shfl(t, 63);
+    }
+  }
+  __syncthreads();
+
+  const int total = __builtin_amdgcn_readfirstlane(tile_prefix[S]);
+  const int xcd = blockIdx.x % 8, local = blockIdx.x / 8, per_xcd = gridDim.x / 8;
+  const int t_begin = (int)((int64_t)total * xcd / 8);
+  const int t_end = (int)((int64_t)total * (xcd + 1) / 8);
+  const int first = t_begin + local;
+  if (first >= t_end) return;
+  const int n_my = (t_end - first + per_xcd - 1) / per_xcd;  // tiles of this workgroup
+  const int total_steps = n_my * nk;
+
+  auto locate = [&](int idx, Tile& t) {  // idx-th tile of this workgroup
+    const int tl = first + idx * per_xcd;
+    int lo = 0, hi = S;
+    while (hi - lo > 1) {
+      int mid = (lo + hi) >> 1;
+      if (tile_prefix[mid] <= tl) lo = mid; else hi = mid;
+    }
+    t.s = __builtin_amdgcn_readfirstlane(lo);
+    const int lt = tl - __builtin_amdgcn_readfirstlane(tile_prefix[t.s]);
+    const int mt = lt / n_tiles;
+    t.nt = lt - mt * n_tiles;
+    t.seg_end = __builtin_amdgcn_readfirstlane(seg_lo[t.s + 1]);
+    t.m0 = __builtin_amdgcn_readfirstlane(seg_lo[t.s]) + mt * kBM;
+  };
+  // Gather indices of tile t into table slot `slot`: waves 0-3 load 64 rows each, straight to
+  // LDS; rows past the segment end repeat its last row (their results are dropped).
+  const char* abase = reinterpret_cast<const char*>(A);
+  // Byte offsets of this lane's four A chunks (one per load instruction) for tile t.
+  const int lrow = lane / kCH, lphys = lane % kCH;
+  auto a_offsets = [&](const Tile& t, int slot, uint32_t (&aoff)[kAQ]) {
+#pragma unroll
+    for (int q = 0; q < kAQ; ++q) {
+      const int row = (wave * kAQ + q) * kRPI + lrow;
+      int64_t r;
+      if (GATHER) r = src_tab[slot * kBM + row];
+      else r = t.m0 + row < t.seg_end ? t.m0 + row : t.seg_end - 1;
+      r = r < 0 ? 0 : (r >= a_rows ? a_rows - 1 : r);
+      aoff[q] = (uint32_t)(r * ld_a * 2) + swz(row, lphys) * 16;
+    }
+  };
+  // This wave's packed weight blocks for tile t (clamped in a partial N tile).
+  auto w_base = [&](const Tile& t) {
+    int nb = t.nt * kWaves + wave;
+    nb = nb < NB ? nb : NB - 1;
+    return Wp + ((int64_t)t.s * NB + nb) * (int64_t)nk * kBlockElems + lane * 8;
+  };
+  // Weight loads are issued from inline assembly: the compiler then neither counts them nor
+  // inserts its own (conservative, loop-merged) waits for their registers; the explicit wait
+  // before their use names the registers, so no use can be scheduled above it.
+  auto load_b = [&](const uint16_t* blk, u32x4 (&b)[4]) {
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(b[0]) : "v"(blk) : "memory");
+    asm volatile("global_load_dwordx4 %0, %1, off offset:1024" : "=v"(b[1]) : "v"(blk) : "memory");
+    asm volatile("global_load_dwordx4 %0, %1, off offset:2048" : "=v"(b[2]) : "v"(blk) : "memory");
+    asm volatile("global_load_dwordx4 %0, %1, off offset:3072" : "=v"(b[3]) : "v"(blk) : "memory");
+  };
+
+  // ---- producer: one A stage (+ one gather-index load) per K step, three steps ahead ---------
+  // Every K step issues the same vector memory operations -- 4 weight loads, 4 token-row loads,
+  // and with GATHER one gather-index load -- whether or not they are needed (past the end they
+  // re-read valid addresses into slots nobody reads), so the wait counts are the same in every
+  // step.
+  Tile pt, pnext;
+  int p_idx = 0, p_kt = 0, p_slot = 0, produced = 0;
+  uint32_t aoff[kAQ];
+  const int src_lead_kt = nk - 4;  // K step of a tile at which the next tile's indices go out
+
+  locate(0, pt);
+  if (GATHER && wave < 4) {  // the first tile's gather indices, before anything else
+    const int r = wave * 64 + lane;
+    const int gr = pt.m0 + r < pt.seg_end ? pt.m0 + r : pt.seg_end - 1;
+    __builtin_amdgcn_global_load_lds((gvoid*)(src_row + gr), (lvoid*)(src_tab + wave * 64), 4,
+                                     0, 0);
+  }
+  vm_wait<0>();
+  barrier_nofence();
+  a_offsets(pt, 0, aoff);
+
+  auto produce = [&]() {
+    const bool live = produced < total_steps;
+    if (live && p_kt == nk) {  // next tile: its gather indices went out four steps ago
+      pt = pnext;
+      ++p_idx;
+      p_kt = 0;
+      p_slot ^= 1;
+      a_offsets(pt, p_slot, aoff);
+    }
+    const int kt_load = live ? p_kt : nk - 1;
+    unsigned char* sb = smem + (produced % kSA) * kStage;
+#pragma unroll
+    for (int q = 0; q < kAQ; ++q)
+      __builtin_amdgcn_global_load_lds((gvoid*)(abase + kt_load * kRB + aoff[q]),
+                                       (lvoid*)(sb + (wave * kAQ + q) * 1024), 16, 0, 0);
+    const bool locate_next = live && p_kt == src_lead_kt && p_idx + 1 < n_my;
+    if (locate_next) locate(p_idx + 1, pnext);
+    if (GATHER) {
+      const bool real = locate_next && wave < 4;
+      const int r = (wave & 3) * 64 + lane;
+      const int gr = real ? (pnext.m0 + r < pnext.seg_end ? pnext.m0 + r : pnext.seg_end - 1) : 0;
+      int* dst = real ? src_tab + (p_slot ^ 1) * kBM + wave * 64 : src_dummy + wave * 64;
+      __builtin_amdgcn_global_load_lds((gvoid*)(src_row + gr), (lvoid*)dst, 4, 0, 0);
+    }
+    if (live) ++p_kt;
+    ++produced;
+  };
+
+  // Fragment read offsets inside a stage: token row 32 j + (lane & 31), K chunk 4 h + q.
+  int frag_off[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    frag_off[q] = (lane & 31) * kRB + (swz(lane & 31, 4 * (lane >> 5) + q) << 4);
+
+  const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      Cout, 0, (int)((int64_t)total_rows * n_out * 2), kBufferWord3);
+
+  // ---- consumer ---------------------------------------------------------------------------
+  Tile ct = pt;
+  const uint16_t* wb = w_base(ct);
+  u32x4 b0[4], b1[4];
+  // Prologue: A(0), A(1), B(0), A(2); then B(0) (and with it A(0), A(1)) must land.
+  produce();
+  asm volatile("" ::: "memory");
+  produce();
+  asm volatile("" ::: "memory");
+  load_b(wb, b0);
+  asm volatile("" ::: "memory");
+  produce();
+  asm volatile("s_waitcnt vmcnt(%4)"
+               : "+v"(b0[0]), "+v"(b0[1]), "+v"(b0[2]), "+v"(b0[3])
+               : "n"(kAQ + (GATHER ? 1 : 0))
+               : "memory");
+
+  // Operations issued after B(g+1) within step g: A(g+3) and, with GATHER, one index load.
+  constexpr int kAfterB = kAQ + (GATHER ? 1 : 0);
+  int g = 0;          // global K step of this workgroup
+  for (int ti = 0; ti < n_my; ++ti) {
+    if (ti > 0) locate(ti, ct);
+    const int live_m = ct.seg_end - ct.m0;  // token rows of this tile that exist (uniform)
+    floatx16 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = floatx16{};
+    const uint16_t* wb_next = wb;
+
+    // One K step: barrier, issue B(g+1), A(g+3) (+ gather indices), compute, then wait until
+    // B(g+1) is in its registers. That wait (vmcnt = the loads issued after B(g+1)) also
+    // completes A(g+1), A(g+2) and any epilogue stores, so at the next step's barrier every
+    // wave's part of A(g+1) has landed. Keeping the wait that names B's registers at the end of
+    // the step means no loop-carried copy of those registers can happen before they are valid.
+    auto step = [&](auto check, int kt, u32x4 (&bc)[4], u32x4 (&bn)[4]) {
+      constexpr bool CHECK = decltype(check)::value;
+      barrier_nofence();
+      const uint16_t* bsrc = wb + (int64_t)kt * kBlockElems;  // past the end: a re-read
+      if (kt + 1 < nk) {
+        bsrc = wb + (int64_t)(kt + 1) * kBlockElems;
+      } else if (ti + 1 < n_my) {
+        Tile nx;
+        locate(ti + 1, nx);
+        wb_next = w_base(nx);
+        bsrc = wb_next;
+      }
+      load_b(bsrc, bn);
+      asm volatile("" ::: "memory");
+      produce();
+      asm volatile("" ::: "memory");
+      const unsigned char* st = smem + (g % kSA) * kStage;
+      // 32 MFMAs (slice q, token block j) with the token fragments read four ahead.
+      auto frag = [&](int n) {
+        return *reinterpret_cast<const bf16x8*>(st + (n % 8) * 32 * kRB + frag_off[n / 8]);
+      };
+      bf16x8 fr[4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+        if (!CHECK || (n % 8) * 32 < live_m) fr[n] = frag(n);
+#pragma unroll
+      for (int n = 0; n < 32; ++n) {
+        const int q = n / 8, j = n % 8;
+        if (!CHECK || j * 32 < live_m)
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8, bc[q]), fr[n % 4], acc[j], 0, 0, 0);
+        if (n + 4 < 32 && (!CHECK || ((n + 4) % 8) * 32 < live_m)) fr[n % 4] = frag(n + 4);
+      }
+      asm volatile("s_waitcnt vmcnt(%4)"
+                   : "+v"(bn[0]), "+v"(bn[1]), "+v"(bn[2]), "+v"(bn[3])
+                   : "n"(kAfterB)
+                   : "memory");
+      ++g;
+    };
+    auto k_loop = [&](auto check) {
+      for (int kt = 0; kt < nk; kt += 2) {
+        step(check, kt, b0, b1);
+        step(check, kt + 1, b1, b0);
+      }
+    };
+    if (live_m >= kBM) k_loop(std::integral_constant<bool, false>());
+    else k_loop(std::integral_constant<bool, true>());
+
+    // Epilogue: a fixed store count per wave; rows past the segment or columns past n_out get
+    // an out-of-range offset and are dropped by the buffer range check.
+    const int nb = ct.nt * kWaves + wave;
+    const int hbit = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int m = ct.m0 + j * 32 + (lane & 31);
+      const bool row_ok = m < ct.seg_end;
+#pragma unroll
+      for (int g4 = 0; g4 < Ep<EPI>::kGroups; ++g4) {
+        int col;
+        float v[4];
+        if (EPI == NT_MOE_EPI_SWIGLU) {
+          col = nb * 16 + 8 * g4 + 4 * hbit;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float a = acc[j][4 * g4 + r], u = acc[j][4 * (g4 + 2) + r];
+            v[r] = a * u * __builtin_amdgcn_rcpf(1.f + __expf(-a));
+          }
+        } else {
+          col = nb * 32 + 8 * g4 + 4 * hbit;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float a = acc[j][4 * g4 + r];
+            v[r] = EPI == NT_MOE_EPI_RELU2 ? (a > 0.f ? a * a : 0.f) : a;
+          }
+        }
+        const uint32_t lo = pack_bf16x2(v[0], v[1]), hi = pack_bf16x2(v[2], v[3]);
+        const uint32_t voff = (row_ok && nb < NB && col < n_out)
+                                  ? (uint32_t)(((int64_t)m * n_out + col) * 2)
+                                  : 0x80000000u;
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, out_rsrc, voff, 0, 0);
+      }
+    }
+    wb = wb_next;
+  }
+  vm_wait<0>();  // the trailing re-reads land in LDS before the workgroup's LDS is released
+}
+
+// Packs w [S, R, K] (bf16) into 32-row x 64-K blocks of fragment order: block (s, nb, kb) holds,
+// at 16-byte chunk q * 64 + l, row i = l % 32 of the block and K elements
+// kb * 64 + 32 (l / 32) + 8 q .. + 8. Row i of block nb is w row 32 nb + i, or for SwiGLU
+// (R = 2 n_out) gate row 16 nb + i (i < 16) and value row n_out + 16 nb + i - 16.
+__global__ __launch_bounds__(256) void pack_weights_kernel(const uint16_t* __restrict__ w,
+                                                            int64_t chunks, int R, int K,
+                                                            int n_out, int swiglu,
+                                                            uint16_t* __restrict__ out) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= chunks) return;
+  const int KB = K / kBK, NB = R / 32;
+  const int l = (int)(c % 64), q = (int)((c / 64) % 4);
+  const int kb = (int)((c / 256) % KB);
+  const int64_t rest = c / (256 * (int64_t)KB);
+  const int nb = (int)(rest % NB);
+  const int64_t s = rest / NB;
+  const int i = l % 32;
+  const int row = swiglu ? (i < 16 ? 16 * nb + i : n_out + 16 * nb + (i - 16)) : 32 * nb + i;
+  const int k0 = kb * kBK + 32 * (l / 32) + 8 * q;
+  *reinterpret_cast<u32x4*>(out + c * 8) =
+      *reinterpret_cast<const u32x4*>(w + (s * R + row) * (int64_t)K + k0);
+}
+
+template <int EPI, bool GATHER>
+hipError_t launch_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows, const int32_t* src_row,
+                         const int32_t* seg_offsets, int S, int64_t total_rows,
+                         const uint16_t* wp, int K, int n_out, uint16_t* c, hipStream_t stream) {
+  const int NB = (EPI == NT_MOE_EPI_SWIGLU ? 2 * n_out : n_out) / 32;
+  const int64_t n_tiles = (NB + kWaves - 1) / kWaves;
+  const int64_t upper = ((total_rows + kBM - 1) / kBM + S) * n_tiles;
+  int64_t grid = num_cus();
+  if (upper < grid) grid = upper;
+  grid = ((grid + 7) / 8) * 8;
+  const size_t lds = (size_t)kSA * kStage + (2 * kBM + kWaves * 64) * sizeof(int) +
+                     (size_t)(2 * S + 2) * sizeof(int);
+  auto kern = grouped_gemm_packed_kernel<EPI, GATHER>;
+  hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), lds, stream, a, ld_a, src_row,
+                     seg_offsets, S, (int)total_rows, a_rows, wp, K, n_out, c);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int packed_gemm_min_k() { return kMinK; }
+
+hipError_t launch_pack_weights_bf16(const uint16_t* w, int64_t S, int R, int K, int epilogue,
+                                    uint16_t* packed, hipStream_t stream) {
+  const int n_out = epilogue == NT_MOE_EPI_SWIGLU ? R / 2 : R;
+  const int64_t chunks = S * (int64_t)R * K / 8;
+  if (chunks == 0) return hipSuccess;
+  pack_weights_kernel<<<dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream>>>(
+      w, chunks, R, K, n_out, epilogue == NT_MOE_EPI_SWIGLU ? 1 : 0, packed);
+  return hipGetLastError();
+}
+
+hipError_t launch_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                           const int32_t* src_row, const int32_t* seg_offsets,
+                                           int num_segments, int64_t total_rows,
+                                           const uint16_t* wp, int K, int n_out, int epilogue,
+                                           uint16_t* c, hipStream_t stream) {
+  if (total_rows == 0) return hipSuccess;
+#define NT_P(EPI)                                                                          \
+  return src_row ? launch_packed<EPI, true>(a, ld_a, a_rows, src_row, seg_offsets,         \
+                                            num_segments, total_rows, wp, K, n_out, c,      \
+                                            stream)                                         \
+                 : launch_packed<EPI, false>(a, ld_a, a_rows, src_row, seg_offsets,        \
+                                             num_segments, total_rows, wp, K, n_out, c,     \
+                                             stream)
+  switch (epilogue) {
+    case NT_MOE_EPI_SWIGLU: NT_P(NT_MOE_EPI_SWIGLU);
+    case NT_MOE_EPI_RELU2: NT_P(NT_MOE_EPI_RELU2);
+    default: NT_P(NT_MOE_EPI_NONE);
+  }
+#undef NT_P
+}
+
+}  // namespace ntmoe

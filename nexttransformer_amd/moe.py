@@ -15,8 +15,10 @@ also kept as the tensor attribute `last_aux` that the plugin shell sums into the
 
 Compute: x is cast to bf16 (the reference's MasterLinear runs matmuls in the activation dtype,
 megatron_moe.py:74-75); the router GEMM runs in fp32 on the bf16 values; expert GEMMs run on
-bf16 copies of the fp32 masters, repacked into [E, rows, cols] stacks only when a master changes
-(tracked by the tensors' version counters, which in-place optimizer updates bump).
+bf16 copies of the fp32 masters (or, with expert_dtype "fp8", on e4m3 copies with 128 x 128
+block scales and per-row quantised activations), repacked into [E, rows, cols] stacks only when
+a master changes (tracked by the tensors' version counters, which in-place optimizer updates
+bump).
 
 The HIP path is forward-only: a call that would need gradients raises RuntimeError instead of
 returning a result without a graph. There is no CPU path.
@@ -41,8 +43,8 @@ def input_init_(weight, generator=None):
     return nn.init.uniform_(weight, -bound, bound, generator=generator)
 
 
-def _round64(n):
-    return (n + 63) // 64 * 64
+def _round_up(n, m):
+    return (n + m - 1) // m * m
 
 
 def _seeded(seed):
@@ -106,9 +108,6 @@ class MoELayer(nn.Module):
         if recipe.routed_experts > nat.MAX_EXPERTS or recipe.top_k > nat.MAX_TOPK:
             raise ValueError(f"the HIP router supports at most {nat.MAX_EXPERTS} experts and "
                              f"top-{nat.MAX_TOPK}")
-        if recipe.expert_dtype != "bf16":
-            raise ValueError(f"expert_dtype {recipe.expert_dtype!r} has no grouped GEMM in this "
-                             "build (bf16 only)")
         if device is None:
             device = (torch.device("cuda", torch.cuda.current_device())
                       if torch.cuda.is_available() else torch.device("cpu"))
@@ -166,49 +165,60 @@ class MoELayer(nn.Module):
     @torch.no_grad()
     def packed_weights(self):
         """Device weights the kernels read, rebuilt only when a master tensor changed:
-        router_t fp32 [dp, E]; w1 bf16 [E, rows, dp]; w2 bf16 [E, dp, Hp]; shared_w1/2 [1, ...].
+        router_t fp32 [dp, E]; w1 [E, rows, dp]; w2 [E, dp, Hp]; shared_w1/2 [1, ...];
+        bf16, or for expert_dtype "fp8" e4m3 codes (uint8) with their 128 x 128 block scales
+        (w1_scale, w2_scale, shared_w1_scale, shared_w2_scale).
 
-        The grouped GEMM tiles K and the SwiGLU halves in multiples of 64, so d and the expert
-        widths are zero-padded up to dp, Hp (multiples of 64) when they are not already: zero
-        input features add exact zeros to every dot product, and a zero hidden unit has
-        act(0) = 0 under both SwiGLU and ReLU^2, so the padded layer computes the same values.
+        The bf16 GEMM tiles K and the SwiGLU halves in multiples of 64, the fp8 GEMM's scale
+        blocks are 128 wide, so d and the expert widths are zero-padded up to dp, Hp when they
+        are not already multiples: zero input features add exact zeros to every dot product, and
+        a zero hidden unit has act(0) = 0 under both SwiGLU and ReLU^2, so the padded layer
+        computes the same values (an all-zero fp8 block gets scale 1 and codes 0).
         """
         masters = self._masters()
         key = tuple((p.data_ptr(), p._version) for p in masters)
         if key != self._pack_key:
             r = self.recipe
-            dp = _round64(r.width)
+            fp8 = r.expert_dtype == "fp8"
+            align = 128 if fp8 else 64
+            dp = _round_up(r.width, align)
             gated = r.activation == "swiglu"
+            dtype = torch.float32 if fp8 else torch.bfloat16
 
             def stack(experts, hidden):
-                hp = _round64(hidden)
+                hp = _round_up(hidden, align)
                 if hp == hidden and dp == r.width:
-                    return (torch.stack([e.linear_fc1.weight.detach() for e in experts])
-                            .to(torch.bfloat16),
-                            torch.stack([e.linear_fc2.weight.detach() for e in experts])
-                            .to(torch.bfloat16))
-                n = len(experts)
-                dev = experts[0].linear_fc1.weight.device
-                w1 = torch.zeros(n, (2 if gated else 1) * hp, dp, device=dev, dtype=torch.bfloat16)
-                w2 = torch.zeros(n, dp, hp, device=dev, dtype=torch.bfloat16)
-                for i, e in enumerate(experts):
-                    fc1 = e.linear_fc1.weight.detach()
-                    if gated:
-                        w1[i, :hidden, :r.width] = fc1[:hidden]
-                        w1[i, hp:hp + hidden, :r.width] = fc1[hidden:]
-                    else:
-                        w1[i, :hidden, :r.width] = fc1
-                    w2[i, :r.width, :hidden] = e.linear_fc2.weight.detach()
-                return w1, w2
+                    w1 = torch.stack([e.linear_fc1.weight.detach() for e in experts]).to(dtype)
+                    w2 = torch.stack([e.linear_fc2.weight.detach() for e in experts]).to(dtype)
+                else:
+                    n = len(experts)
+                    dev = experts[0].linear_fc1.weight.device
+                    w1 = torch.zeros(n, (2 if gated else 1) * hp, dp, device=dev, dtype=dtype)
+                    w2 = torch.zeros(n, dp, hp, device=dev, dtype=dtype)
+                    for i, e in enumerate(experts):
+                        fc1 = e.linear_fc1.weight.detach()
+                        if gated:
+                            w1[i, :hidden, :r.width] = fc1[:hidden]
+                            w1[i, hp:hp + hidden, :r.width] = fc1[hidden:]
+                        else:
+                            w1[i, :hidden, :r.width] = fc1
+                        w2[i, :r.width, :hidden] = e.linear_fc2.weight.detach()
+                if not fp8:
+                    return w1, None, w2, None
+                w1q, w1s = ops.quantize_fp8_blockwise(w1.contiguous())
+                w2q, w2s = ops.quantize_fp8_blockwise(w2.contiguous())
+                return w1q, w1s, w2q, w2s
 
             router_t = torch.zeros(dp, r.routed_experts, device=self.router.weight.device,
                                    dtype=torch.float32)
             router_t[:r.width] = self.router.weight.detach().t()
-            w1, w2 = stack(list(self.experts.local_experts), r.expert_width)
-            packed = dict(router_t=router_t, w1=w1, w2=w2, shared_w1=None, shared_w2=None)
+            packed = dict(router_t=router_t, shared_w1=None, shared_w2=None,
+                          shared_w1_scale=None, shared_w2_scale=None)
+            (packed["w1"], packed["w1_scale"], packed["w2"],
+             packed["w2_scale"]) = stack(list(self.experts.local_experts), r.expert_width)
             if self.shared_experts is not None:
-                packed["shared_w1"], packed["shared_w2"] = stack([self.shared_experts],
-                                                                 r.shared_expert_width)
+                (packed["shared_w1"], packed["shared_w1_scale"], packed["shared_w2"],
+                 packed["shared_w2_scale"]) = stack([self.shared_experts], r.shared_expert_width)
             self._packed = packed
             self._pack_key = key
         return self._packed
@@ -241,7 +251,9 @@ class MoELayer(nn.Module):
             x, w["router_t"], w["w1"], w["w2"], top_k=r.top_k,
             score_fn=_SCORE[r.score_function], activation=_ACT[r.activation],
             aux_coeff=r.aux_loss_coeff, z_coeff=r.z_loss_coeff,
-            shared_w1=w["shared_w1"], shared_w2=w["shared_w2"])
+            shared_w1=w["shared_w1"], shared_w2=w["shared_w2"], w1_scale=w["w1_scale"],
+            w2_scale=w["w2_scale"], shared_w1_scale=w["shared_w1_scale"],
+            shared_w2_scale=w["shared_w2_scale"])
         if dp != r.width:
             out = out[:, :r.width]
         self.last_load = state["counts"].to(torch.int64)

@@ -235,6 +235,61 @@ def _(a, src_row, seg_offsets, w, epilogue, total_rows):
     return a.new_empty((total_rows, rows // 2 if epilogue == nat.EPI_SWIGLU else rows))
 
 
+@torch.library.custom_op("ntmoe::pack_expert_weights", mutates_args=())
+def pack_expert_weights(w: Tensor, epilogue: int) -> Tensor:
+    """Expert weights [S, rows, K] bf16 rearranged for grouped_gemm_packed (same size)."""
+    _on_gpu(w)
+    _require(w.dtype == torch.bfloat16 and w.dim() == 3 and w.is_contiguous(),
+             "pack_expert_weights: w must be contiguous bf16 [S, rows, K]")
+    S, R, K = w.shape
+    out = torch.empty_like(w)
+    st = nat.load().nt_moe_pack_expert_weights_bf16(ptr(w), S, R, K, epilogue, ptr(out),
+                                                    _stream(w.device))
+    nat.check(st, "ntmoe::pack_expert_weights")
+    return out
+
+
+@pack_expert_weights.register_fake
+def _(w, epilogue):
+    return torch.empty_like(w)
+
+
+def packable(K, n_out, epilogue):
+    """Whether a [*, n_out or 2 n_out, K] weight stack qualifies for the packed GEMM."""
+    return K >= 256 and K % 128 == 0 and n_out % (16 if epilogue == nat.EPI_SWIGLU else 32) == 0
+
+
+@torch.library.custom_op("ntmoe::grouped_gemm_packed", mutates_args=())
+def grouped_gemm_packed(a: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor,
+                        w_packed: Tensor, epilogue: int, total_rows: int) -> Tensor:
+    """grouped_gemm on weights packed by pack_expert_weights with the same epilogue."""
+    _on_gpu(a, src_row, seg_offsets, w_packed)
+    _require(a.dtype == torch.bfloat16 and a.dim() == 2 and a.stride(1) == 1,
+             "grouped_gemm_packed: a must be bf16 [*, K] with contiguous rows")
+    _require(w_packed.dtype == torch.bfloat16 and w_packed.dim() == 3 and w_packed.is_contiguous(),
+             "grouped_gemm_packed: w_packed must be contiguous bf16 [S, rows, K]")
+    S, rows, K = w_packed.shape
+    n_out = rows // 2 if epilogue == nat.EPI_SWIGLU else rows
+    _require(a.shape[1] == K, "grouped_gemm_packed: a and w disagree on K")
+    _require(seg_offsets.dtype == torch.int32 and seg_offsets.shape == (S + 1,)
+             and seg_offsets.is_contiguous(), "grouped_gemm_packed: seg_offsets must be int32 [S+1]")
+    if src_row is not None:
+        _require(src_row.dtype == torch.int32 and src_row.is_contiguous(),
+                 "grouped_gemm_packed: src_row must be contiguous int32")
+    c = torch.empty(total_rows, n_out, device=a.device, dtype=torch.bfloat16)
+    st = nat.load().nt_moe_grouped_gemm_bf16_packed(
+        ptr(a), a.stride(0), a.shape[0], ptr(src_row), ptr(seg_offsets), S, total_rows,
+        ptr(w_packed), K, n_out, epilogue, ptr(c), _stream(a.device))
+    nat.check(st, "ntmoe::grouped_gemm_packed")
+    return c
+
+
+@grouped_gemm_packed.register_fake
+def _(a, src_row, seg_offsets, w_packed, epilogue, total_rows):
+    rows = w_packed.shape[1]
+    return a.new_empty((total_rows, rows // 2 if epilogue == nat.EPI_SWIGLU else rows))
+
+
 # ---------------------------------------------------------------------------------------------
 # fp8 (OCP e4m3fn bytes held in uint8 tensors)
 
@@ -363,11 +418,25 @@ def _(y, combine_dest, combine_w, shared_y, prob_partial, z_partial, counts, aux
 # ---------------------------------------------------------------------------------------------
 # the whole layer
 
+_SEGMENTS = {}
+
+
+def _whole_batch_segment(T, device):
+    """Device tensor [0, T]: the shared expert's single segment (cached: no per-call upload)."""
+    key = (T, device)
+    seg = _SEGMENTS.get(key)
+    if seg is None:
+        seg = torch.tensor([0, T], device=device, dtype=torch.int32)
+        if len(_SEGMENTS) < 64:
+            _SEGMENTS[key] = seg
+    return seg
+
+
 def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
                 activation=nat.ACT_SWIGLU, aux_coeff=0.01, z_coeff=0.001, logit_bias=None,
                 shared_w1=None, shared_w2=None, want_logits=False, permute_rows=False,
                 w1_scale=None, w2_scale=None, shared_w1_scale=None, shared_w2_scale=None,
-                mark=None):
+                packed=False, mark=None):
     """The MoE layer forward on the GPU: router -> route plan -> grouped GEMMs -> combine + aux.
 
     x bf16 [T, d]; w_router_t fp32 [d, E]; w1 bf16 [E, F, d] (F = 2H for SwiGLU, H for ReLU^2);
@@ -375,6 +444,8 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
     Returns (out [T, d] bf16, aux fp32 [3] = {lb + z, lb, z}, state with the routing tensors).
     With permute_rows the token rows are first moved into expert order by the permute kernel
     (x_perm); by default the up-projection GEMM gathers them itself.
+    packed: w1 (and shared_w1) were packed by pack_expert_weights with the up epilogue, w2 (and
+    shared_w2) with EPI_NONE; the packed grouped GEMM runs both projections.
     fp8 experts: pass w1/w2 (and the shared expert's) as uint8 e4m3 codes with their 128 x 128
     block scales (w*_scale, from quantize_fp8_blockwise); the token rows and the intermediate
     h are then quantised per row and both projections run on the fp8 grouped GEMM.
@@ -413,7 +484,7 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
         mark("gemm_down")
         shared_y = None
         if shared_w1 is not None:
-            seg = torch.tensor([0, T], device=x.device, dtype=torch.int32)
+            seg = _whole_batch_segment(T, x.device)
             hs_ = grouped_gemm_fp8(xq, xs, None, seg, shared_w1, shared_w1_scale, up_epi, T)
             hsq, hss = quantize_fp8_rowwise(hs_)
             shared_y = grouped_gemm_fp8(hsq, hss, None, seg, shared_w2, shared_w2_scale,
@@ -425,18 +496,19 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
                      src_row=src, perm_w=perm_w, combine_dest=cdest, combine_w=cw, x_q=xq,
                      x_scale=xs)
         return out, aux, state
+    gemm = grouped_gemm_packed if packed else grouped_gemm
     if permute_rows:
-        h = grouped_gemm(x_perm, None, offsets, w1, up_epi, A)
+        h = gemm(x_perm, None, offsets, w1, up_epi, A)
     else:
-        h = grouped_gemm(x, src, offsets, w1, up_epi, A)
+        h = gemm(x, src, offsets, w1, up_epi, A)
     mark("gemm_up")
-    y = grouped_gemm(h, None, offsets, w2, nat.EPI_NONE, A)
+    y = gemm(h, None, offsets, w2, nat.EPI_NONE, A)
     mark("gemm_down")
     shared_y = None
     if shared_w1 is not None:
-        seg = torch.tensor([0, T], device=x.device, dtype=torch.int32)
-        hs = grouped_gemm(x, None, seg, shared_w1, up_epi, T)
-        shared_y = grouped_gemm(hs, None, seg, shared_w2, nat.EPI_NONE, T)
+        seg = _whole_batch_segment(T, x.device)
+        hs = gemm(x, None, seg, shared_w1, up_epi, T)
+        shared_y = gemm(hs, None, seg, shared_w2, nat.EPI_NONE, T)
         mark("shared")
     out, aux = combine_aux(y, cdest, cw, shared_y, pp, zp, counts, aux_coeff, z_coeff)
     mark("combine")

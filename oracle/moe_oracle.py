@@ -235,8 +235,18 @@ def dequantize_rowwise(q, scale):
     return e4m3_decode(q) * scale.float()[:, None]
 
 
+def _fp8_expert(rows, w1q, w1s, w2q, w2s, activation):
+    """fc1 on dequantised operands in fp32, activation, h rounded to bf16 and re-quantised per
+    row, fc2 on dequantised operands."""
+    w1 = dequantize_blockwise(w1q.cpu(), w1s.cpu())
+    w2 = dequantize_blockwise(w2q.cpu(), w2s.cpu())
+    h = act(rows @ w1.t(), activation, w2q.shape[-1]).to(torch.bfloat16).float()
+    hq, hs = quantize_rowwise(h)
+    return dequantize_rowwise(hq, hs) @ w2.t()
+
+
 def moe_forward_fp8(x, router, w1q, w1s, w2q, w2s, k, *, score_fn=SOFTMAX, activation=SWIGLU,
-                    aux_coeff=0.01, z_coeff=0.001, bias=None, tokens=None):
+                    aux_coeff=0.01, z_coeff=0.001, bias=None, tokens=None, shared=None):
     """The fp8 layer on the CPU, the fp32 dequantised reference of the fp8 path.
 
     Routing as moe_forward (fp32 router on the bf16 hidden states). Each token row is quantised
@@ -246,7 +256,8 @@ def moe_forward_fp8(x, router, w1q, w1s, w2q, w2s, k, *, score_fn=SOFTMAX, activ
     outputs are weighted after fc2 and accumulated in ascending expert order.
     The weight tensors may live on any device; only the experts in use are copied to the CPU.
     With `tokens`, out holds only those tokens' rows (each token's output depends on its own
-    row and routing alone).
+    row and routing alone). `shared` = (w1q, w1s, w2q, w2s) of an always-on shared expert
+    ([Fs, d], [d, Hs] matrices), added to every token.
     """
     x = x.detach().cpu()
     logits = router_logits_fixed(x, router, bias)
@@ -259,17 +270,14 @@ def moe_forward_fp8(x, router, w1q, w1s, w2q, w2s, k, *, score_fn=SOFTMAX, activ
     out = torch.zeros(len(sel), x.shape[1], dtype=torch.float32)
     ids64 = ids.long()[sel]
     topw_sel = topw[sel]
-    H = w2q.shape[2]
     for e in range(E):
         token, slot = torch.where(ids64 == e)
         if not token.numel():
             continue
-        w1 = dequantize_blockwise(w1q[e].cpu(), w1s[e].cpu())
-        w2 = dequantize_blockwise(w2q[e].cpu(), w2s[e].cpu())
-        h = act(rows[token] @ w1.t(), activation, H).to(torch.bfloat16).float()
-        hq, hs = quantize_rowwise(h)
-        y = dequantize_rowwise(hq, hs) @ w2.t()
+        y = _fp8_expert(rows[token], w1q[e], w1s[e], w2q[e], w2s[e], activation)
         out.index_add_(0, token, y * topw_sel[token, slot, None])
+    if shared is not None:
+        out = out + _fp8_expert(rows, *shared, activation)
     lb, z = aux_losses(logits, counts, k, aux_coeff, z_coeff, score_fn)
     return dict(out=out, aux=lb + z, lb=lb, z=z, logits=logits, ids=ids, weights=topw,
                 counts=counts, offsets=offsets, src_row=src, dest=dest, x_q=xq, x_scale=xs)

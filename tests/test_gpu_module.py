@@ -111,6 +111,36 @@ def test_module_forward_matches_oracle(kw):
     assert aux.item() == pytest.approx(ref["aux"], rel=AUX_RTOL)
 
 
+@pytest.mark.parametrize("kw", [
+    dict(activation="swiglu", width=512, heads=4, expert_width=256, allow_any_expert_width=True),
+    dict(width=96, heads=2, expert_width=24),  # ReLU^2 + shared, padded to 128
+], ids=["swiglu-512", "relu2-shared-padded"])
+def test_module_fp8_matches_dequantised_reference(kw):
+    from nexttransformer_amd.moe import MoELayer
+    r = _recipe(expert_dtype="fp8", **kw)
+    m = MoELayer(r, 2)
+    _randomise_fc2(m, 6)
+    hidden = torch.randn(2, 40, r.width).to(torch.bfloat16).cuda()
+    with torch.no_grad():
+        out, aux = m(hidden)
+    p = m.packed_weights()
+    assert p["w1"].dtype == torch.uint8 and p["w1_scale"] is not None
+    act = orc.SWIGLU if r.activation == "swiglu" else orc.RELU2
+    dp = p["router_t"].shape[0]
+    x = torch.nn.functional.pad(hidden.reshape(-1, r.width).cpu(), (0, dp - r.width))
+    shared = None
+    if m.shared_experts is not None:
+        shared = tuple(p[n][0].cpu() for n in ("shared_w1", "shared_w1_scale", "shared_w2",
+                                              "shared_w2_scale"))
+    ref = orc.moe_forward_fp8(x, torch.nn.functional.pad(m.router.weight.detach().cpu(),
+                                                         (0, dp - r.width)),
+                              p["w1"].cpu(), p["w1_scale"].cpu(), p["w2"].cpu(),
+                              p["w2_scale"].cpu(), r.top_k, activation=act, shared=shared)
+    ref_out = ref["out"][:, :r.width]
+    assert torch.equal(m.last_load.cpu(), ref["counts"].long())
+    assert rel_l2(out.float().reshape(-1, r.width), ref_out) <= 3e-2
+
+
 def test_module_empty_experts_256_top8():
     """tests/test_megatron_moe.py:157-166: two tokens over 256 experts."""
     from nexttransformer_amd.moe import MoELayer

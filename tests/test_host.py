@@ -307,8 +307,8 @@ def test_module_errors():
         MoELayer(r, 2, SimpleNamespace(ep=SimpleNamespace(size=lambda: 8)), device="cpu")
     with pytest.raises(ValueError, match="CPU math"):
         MoEFFN(r, 2, cpu_math=True, device="cpu")
-    with pytest.raises(ValueError, match="bf16 only"):
-        MoELayer(small_recipe(expert_dtype="fp8"), 2, device="cpu")
+    with pytest.raises(ValueError, match="GPU only"):  # fp8 packing quantises on the GPU
+        MoELayer(small_recipe(expert_dtype="fp8"), 2, device="cpu").packed_weights()
     m = MoELayer(r, 2, device="cpu")
     with pytest.raises(ValueError, match="GPU only"):
         with torch.no_grad():
