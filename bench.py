@@ -91,6 +91,20 @@ def gpu_inputs(case, fp8):
             g[name], g[name + "_scale"] = ops.quantize_fp8_blockwise(cpu[name].to(dev))
         else:
             g[name] = cpu[name].to(torch.bfloat16).to(dev)
+    # bf16: the packed-weight grouped GEMM when every projection qualifies
+    g["packed"] = False
+    if not fp8:
+        from nexttransformer_amd import _native as nat
+        up = nat.EPI_SWIGLU if case.activation == 0 else nat.EPI_RELU2
+        pairs = [("w1", up), ("w2", nat.EPI_NONE)]
+        if g["shared_w1"] is not None:
+            pairs += [("shared_w1", up), ("shared_w2", nat.EPI_NONE)]
+        ok = all(ops.packable(g[n].shape[2], g[n].shape[1] // (2 if e == nat.EPI_SWIGLU else 1), e)
+                 for n, e in pairs)
+        if ok:
+            for n, e in pairs:
+                g[n] = ops.pack_expert_weights(g[n], e)
+            g["packed"] = True
     torch.cuda.synchronize()
     return cpu, g
 
@@ -151,7 +165,8 @@ def describe(case, cfg, permute_rows, fp8):
         text += ", fp8 e4m3 experts (128x128 block scales, per-row activation scales)"
     return {"workload": text + ", dropless", "tokens": case.T, "d_model": case.d,
             "experts": case.E, "top_k": case.k, "expert_hidden": case.H,
-            "shared_hidden": case.shared_H, "rows_gathered_in_gemm": not permute_rows}
+            "shared_hidden": case.shared_H, "rows_gathered_in_gemm": not permute_rows,
+            "expert_weights": "fp8 e4m3 + block scales" if fp8 else "bf16"}
 
 
 def main():
@@ -182,7 +197,7 @@ def main():
                                shared_w2=g["shared_w2"], w1_scale=g["w1_scale"],
                                w2_scale=g["w2_scale"], shared_w1_scale=g["shared_w1_scale"],
                                shared_w2_scale=g["shared_w2_scale"],
-                               permute_rows=args.permute_rows, mark=mark)
+                               permute_rows=args.permute_rows, packed=g["packed"], mark=mark)
 
     state = None
     for _ in range(max(1, args.warmup)):
@@ -245,7 +260,8 @@ def main():
     else:
         up_flop = 2.0 * A * case.d * F
         achieved = up_flop / (up_ms * 1e-3) / 1e12
-        roofline = {"kernel": "grouped_gemm_kernel (up-projection + SwiGLU epilogue)",
+        roofline = {"kernel": ("grouped_gemm_packed_kernel" if g["packed"] else "grouped_gemm_kernel")
+                              + " (up-projection + SwiGLU epilogue)",
                     "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                     "traffic": load_traffic(f"config{args.config}"),
@@ -263,7 +279,8 @@ def main():
         "vs_baseline": None,
         "dtype": "fp8-e4m3 (fp32 accumulate)" if fp8 else "bf16",
         "data": "synthetic: hidden ~N(0,1), router/expert weights ~N(0,0.02) random init, seed 0",
-        "config": describe(case, args.config, args.permute_rows, fp8),
+        "config": dict(describe(case, args.config, args.permute_rows, fp8),
+                       weights_packed=g["packed"]),
         "roofline": roofline,
         "layer_tflops": round(layer_flops(case) / (ms * 1e-3) / 1e12, 2),
         "expert_load_max_over_mean": round(load_ratio, 3),

@@ -276,8 +276,10 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
     // completes A(g+1), A(g+2) and any epilogue stores, so at the next step's barrier every
     // wave's part of A(g+1) has landed. Keeping the wait that names B's registers at the end of
     // the step means no loop-carried copy of those registers can happen before they are valid.
-    auto step = [&](auto check, int kt, u32x4 (&bc)[4], u32x4 (&bn)[4]) {
-      constexpr bool CHECK = decltype(check)::value;
+    auto step = [&](auto nj_c, int kt, u32x4 (&bc)[4], u32x4 (&bn)[4]) {
+      constexpr int NJ = decltype(nj_c)::value;  // 32-token blocks that hold segment rows
+      constexpr int NM = 4 * NJ;                 // MFMAs per wave in this step
+      constexpr int PF = NM < 4 ? NM : 4;        // fragment reads kept in flight
       barrier_nofence();
       const uint16_t* bsrc = wb + (int64_t)kt * kBlockElems;  // past the end: a re-read
       if (kt + 1 < nk) {
@@ -293,36 +295,46 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
       produce();
       asm volatile("" ::: "memory");
       const unsigned char* st = smem + (g % kSA) * kStage;
-      // 32 MFMAs (slice q, token block j) with the token fragments read four ahead.
+      // NM MFMAs (slice q = n / NJ, token block j = n % NJ), token fragments read PF ahead.
       auto frag = [&](int n) {
-        return *reinterpret_cast<const bf16x8*>(st + (n % 8) * 32 * kRB + frag_off[n / 8]);
+        return *reinterpret_cast<const bf16x8*>(st + (n % NJ) * 32 * kRB + frag_off[n / NJ]);
       };
-      bf16x8 fr[4];
+      bf16x8 fr[PF];
 #pragma unroll
-      for (int n = 0; n < 4; ++n)
-        if (!CHECK || (n % 8) * 32 < live_m) fr[n] = frag(n);
+      for (int n = 0; n < PF; ++n) fr[n] = frag(n);
 #pragma unroll
-      for (int n = 0; n < 32; ++n) {
-        const int q = n / 8, j = n % 8;
-        if (!CHECK || j * 32 < live_m)
-          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8, bc[q]), fr[n % 4], acc[j], 0, 0, 0);
-        if (n + 4 < 32 && (!CHECK || ((n + 4) % 8) * 32 < live_m)) fr[n % 4] = frag(n + 4);
+      for (int n = 0; n < NM; ++n) {
+        acc[n % NJ] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            __builtin_bit_cast(bf16x8, bc[n / NJ]), fr[n % PF], acc[n % NJ], 0, 0, 0);
+        if (n + PF < NM) fr[n % PF] = frag(n + PF);
       }
+      // Keep PF fragment reads in flight: PF reads, then (1 MFMA, 1 read) pairs, then PF
+      // MFMAs. Without this the scheduler pulls each read next to its MFMA and waits on it.
+      __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
+#pragma unroll
+      for (int n = 0; n < NM - PF; ++n) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
       asm volatile("s_waitcnt vmcnt(%4)"
                    : "+v"(bn[0]), "+v"(bn[1]), "+v"(bn[2]), "+v"(bn[3])
                    : "n"(kAfterB)
                    : "memory");
       ++g;
     };
-    auto k_loop = [&](auto check) {
+    auto k_loop = [&](auto nj_c) {
       for (int kt = 0; kt < nk; kt += 2) {
-        step(check, kt, b0, b1);
-        step(check, kt + 1, b1, b0);
+        step(nj_c, kt, b0, b1);
+        step(nj_c, kt + 1, b1, b0);
       }
     };
-    if (live_m >= kBM) k_loop(std::integral_constant<bool, false>());
-    else k_loop(std::integral_constant<bool, true>());
+    // A partial tile (the last of a segment) multiplies only the 32-token blocks that hold
+    // rows: 1, 2, 4 or all 8 of them. The loads are the same in every variant.
+    if (live_m > 128) k_loop(std::integral_constant<int, 8>());
+    else if (live_m > 64) k_loop(std::integral_constant<int, 4>());
+    else if (live_m > 32) k_loop(std::integral_constant<int, 2>());
+    else k_loop(std::integral_constant<int, 1>());
 
     // Epilogue: a fixed store count per wave; rows past the segment or columns past n_out get
     // an out-of-range offset and are dropped by the buffer range check.

@@ -166,8 +166,9 @@ class MoELayer(nn.Module):
     def packed_weights(self):
         """Device weights the kernels read, rebuilt only when a master tensor changed:
         router_t fp32 [dp, E]; w1 [E, rows, dp]; w2 [E, dp, Hp]; shared_w1/2 [1, ...];
-        bf16, or for expert_dtype "fp8" e4m3 codes (uint8) with their 128 x 128 block scales
-        (w1_scale, w2_scale, shared_w1_scale, shared_w2_scale).
+        bf16 (in the packed fragment order of pack_expert_weights when `packed`), or for
+        expert_dtype "fp8" e4m3 codes (uint8) with their 128 x 128 block scales (w1_scale,
+        w2_scale, shared_w1_scale, shared_w2_scale).
 
         The bf16 GEMM tiles K and the SwiGLU halves in multiples of 64, the fp8 GEMM's scale
         blocks are 128 wide, so d and the expert widths are zero-padded up to dp, Hp when they
@@ -184,6 +185,12 @@ class MoELayer(nn.Module):
             dp = _round_up(r.width, align)
             gated = r.activation == "swiglu"
             dtype = torch.float32 if fp8 else torch.bfloat16
+            # The packed-weight GEMM (fragment-ordered weights streamed into registers) when every
+            # projection's K and width qualify and the weights live on the GPU.
+            widths = [r.expert_width] + ([r.shared_expert_width] if self.shared_experts else [])
+            use_packed = (not fp8 and self.router.weight.is_cuda and all(
+                ops.packable(dp, _round_up(h, align), nat.EPI_SWIGLU if gated else nat.EPI_RELU2)
+                and ops.packable(_round_up(h, align), dp, nat.EPI_NONE) for h in widths))
 
             def stack(experts, hidden):
                 hp = _round_up(hidden, align)
@@ -204,6 +211,10 @@ class MoELayer(nn.Module):
                             w1[i, :hidden, :r.width] = fc1
                         w2[i, :r.width, :hidden] = e.linear_fc2.weight.detach()
                 if not fp8:
+                    up = nat.EPI_SWIGLU if gated else nat.EPI_RELU2
+                    if use_packed:
+                        return (ops.pack_expert_weights(w1.contiguous(), up), None,
+                                ops.pack_expert_weights(w2.contiguous(), nat.EPI_NONE), None)
                     return w1, None, w2, None
                 w1q, w1s = ops.quantize_fp8_blockwise(w1.contiguous())
                 w2q, w2s = ops.quantize_fp8_blockwise(w2.contiguous())
@@ -213,7 +224,7 @@ class MoELayer(nn.Module):
                                    dtype=torch.float32)
             router_t[:r.width] = self.router.weight.detach().t()
             packed = dict(router_t=router_t, shared_w1=None, shared_w2=None,
-                          shared_w1_scale=None, shared_w2_scale=None)
+                          shared_w1_scale=None, shared_w2_scale=None, packed=use_packed)
             (packed["w1"], packed["w1_scale"], packed["w2"],
              packed["w2_scale"]) = stack(list(self.experts.local_experts), r.expert_width)
             if self.shared_experts is not None:
@@ -253,7 +264,7 @@ class MoELayer(nn.Module):
             aux_coeff=r.aux_loss_coeff, z_coeff=r.z_loss_coeff,
             shared_w1=w["shared_w1"], shared_w2=w["shared_w2"], w1_scale=w["w1_scale"],
             w2_scale=w["w2_scale"], shared_w1_scale=w["shared_w1_scale"],
-            shared_w2_scale=w["shared_w2_scale"])
+            shared_w2_scale=w["shared_w2_scale"], packed=w["packed"])
         if dp != r.width:
             out = out[:, :r.width]
         self.last_load = state["counts"].to(torch.int64)
