@@ -91,9 +91,16 @@ def gpu_inputs(case, fp8):
             g[name], g[name + "_scale"] = ops.quantize_fp8_blockwise(cpu[name].to(dev))
         else:
             g[name] = cpu[name].to(torch.bfloat16).to(dev)
-    # bf16: the packed-weight grouped GEMM when every projection qualifies
+    # the packed-weight grouped GEMMs: always for fp8, for bf16 when every projection qualifies
     g["packed"] = False
-    if not fp8:
+    if fp8:
+        from nexttransformer_amd import _native as nat
+        up = nat.EPI_SWIGLU if case.activation == 0 else nat.EPI_RELU2
+        for n, e in (("w1", up), ("w2", nat.EPI_NONE), ("shared_w1", up), ("shared_w2", nat.EPI_NONE)):
+            if g[n] is not None:
+                g[n] = ops.pack_expert_weights_fp8(g[n], e)
+        g["packed"] = True
+    else:
         from nexttransformer_amd import _native as nat
         up = nat.EPI_SWIGLU if case.activation == 0 else nat.EPI_RELU2
         pairs = [("w1", up), ("w2", nat.EPI_NONE)]

@@ -241,6 +241,25 @@ int nt_moe_grouped_gemm_fp8(const uint8_t* a, int64_t ld_a, int64_t a_rows, cons
                             uint16_t* c, nt_moe_stream_t stream);
 
 /*
+ * Packed fp8 weights: nt_moe_pack_expert_weights_fp8 rearranges e4m3 w [num_segments, rows, K]
+ * (same bytes; the block scales keep their [num_segments, rows/128, K/128] layout) so that each
+ * wave of nt_moe_grouped_gemm_fp8_packed streams its 32 weight rows as consecutive 4 KB blocks,
+ * one per 128-wide K block, instead of 32 strided 128-byte pieces. `epilogue` must match the
+ * GEMM's (SWIGLU packs 16 gate rows with the 16 value rows of the same columns).
+ *   pack: rows % 128 == 0 (rows = 2 n_out for SWIGLU), K % 128 == 0
+ *   gemm: as nt_moe_grouped_gemm_fp8 with w = packed weights.
+ */
+int nt_moe_pack_expert_weights_fp8(const uint8_t* w, int64_t num_segments, int32_t rows,
+                                   int32_t K, int32_t epilogue, uint8_t* packed,
+                                   nt_moe_stream_t stream);
+int nt_moe_grouped_gemm_fp8_packed(const uint8_t* a, int64_t ld_a, int64_t a_rows,
+                                   const float* a_scale, const int32_t* src_row,
+                                   const int32_t* seg_offsets, int32_t num_segments,
+                                   int64_t total_rows, const uint8_t* w_packed,
+                                   const float* w_scale, int32_t K, int32_t n_out,
+                                   int32_t epilogue, uint16_t* c, nt_moe_stream_t stream);
+
+/*
  * Deterministic weighted combine plus the load-balance and z auxiliary losses.
  *   out[t] = sum over j in ascending expert order of combine_w[t,j] * y[combine_dest[t,j]]
  *            (+ shared_y[t] when given), accumulated in fp32, rounded once to bf16.

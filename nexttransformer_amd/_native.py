@@ -46,6 +46,9 @@ SIGNATURES = {
     "nt_moe_quantize_fp8_blockwise": (_i32, [_p, _i64, _i32, _i32, _p, _p, _p]),
     "nt_moe_grouped_gemm_fp8": (_i32, [_p, _i64, _i64, _p, _p, _p, _i32, _i64, _p, _p, _i32, _i32,
                                        _i32, _p, _p]),
+    "nt_moe_pack_expert_weights_fp8": (_i32, [_p, _i64, _i32, _i32, _i32, _p, _p]),
+    "nt_moe_grouped_gemm_fp8_packed": (_i32, [_p, _i64, _i64, _p, _p, _p, _i32, _i64, _p, _p, _i32,
+                                              _i32, _i32, _p, _p]),
     "nt_moe_combine_aux": (_i32, [_p, _p, _p, _i64, _i32, _i32, _p, _i64, _p, _i64, _p, _p, _p,
                                   _i32, _f32, _f32, _p, _p]),
 }

@@ -384,8 +384,55 @@ int nt_moe_grouped_gemm_fp8(const uint8_t* a, int64_t ld_a, int64_t a_rows, cons
   if (total_rows == 0) return ok();
   hipError_t err = launch_grouped_gemm_fp8(a, ld_a, a_rows, a_scale, src_row, seg_offsets,
                                            num_segments, total_rows, w, w_scale, K, n_out,
-                                           epilogue, c, reinterpret_cast<hipStream_t>(stream));
+                                           epilogue, false, c,
+                                           reinterpret_cast<hipStream_t>(stream));
   return launched(err, "grouped_gemm_fp8");
+}
+
+int nt_moe_pack_expert_weights_fp8(const uint8_t* w, int64_t num_segments, int32_t rows,
+                                   int32_t K, int32_t epilogue, uint8_t* packed,
+                                   nt_moe_stream_t stream) {
+  NT_REQUIRE(epilogue == NT_MOE_EPI_SWIGLU || epilogue == NT_MOE_EPI_RELU2 ||
+                 epilogue == NT_MOE_EPI_NONE, "pack_expert_weights_fp8: unknown epilogue %d", epilogue);
+  NT_REQUIRE(num_segments >= 0 && rows > 0 && rows % 128 == 0 && K > 0 && K % 128 == 0,
+             "pack_expert_weights_fp8: rows and K must be multiples of 128, got %d x %d", rows, K);
+  if (num_segments == 0) return ok();
+  NT_REQUIRE(w && packed && aligned16(w) && aligned16(packed),
+             "pack_expert_weights_fp8: null or unaligned buffer");
+  hipError_t err = launch_pack_weights_fp8(w, num_segments, rows, K, epilogue, packed,
+                                           reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "pack_expert_weights_fp8");
+}
+
+int nt_moe_grouped_gemm_fp8_packed(const uint8_t* a, int64_t ld_a, int64_t a_rows,
+                                   const float* a_scale, const int32_t* src_row,
+                                   const int32_t* seg_offsets, int32_t num_segments,
+                                   int64_t total_rows, const uint8_t* w_packed,
+                                   const float* w_scale, int32_t K, int32_t n_out,
+                                   int32_t epilogue, uint16_t* c, nt_moe_stream_t stream) {
+  NT_REQUIRE(K > 0 && K % 128 == 0, "grouped_gemm_fp8_packed: K must be a positive multiple of 128, got %d", K);
+  NT_REQUIRE(epilogue == NT_MOE_EPI_SWIGLU || epilogue == NT_MOE_EPI_RELU2 ||
+                 epilogue == NT_MOE_EPI_NONE, "grouped_gemm_fp8_packed: unknown epilogue %d", epilogue);
+  NT_REQUIRE(n_out > 0 && n_out % (epilogue == NT_MOE_EPI_SWIGLU ? 64 : 128) == 0,
+             "grouped_gemm_fp8_packed: n_out must be a positive multiple of %d, got %d",
+             epilogue == NT_MOE_EPI_SWIGLU ? 64 : 128, n_out);
+  NT_REQUIRE(num_segments >= 1 && num_segments <= NT_MOE_MAX_SEGMENTS,
+             "grouped_gemm_fp8_packed: num_segments must be in [1, %d]", NT_MOE_MAX_SEGMENTS);
+  NT_REQUIRE(total_rows >= 0 && total_rows < ((int64_t)1 << 31), "grouped_gemm_fp8_packed: bad total_rows");
+  NT_REQUIRE(ld_a >= K && ld_a % 32 == 0, "grouped_gemm_fp8_packed: ld_a must be >= K and a multiple of 32");
+  NT_REQUIRE(a_rows >= 1, "grouped_gemm_fp8_packed: a_rows must be positive");
+  NT_REQUIRE(src_row || a_rows >= total_rows,
+             "grouped_gemm_fp8_packed: a needs total_rows rows without src_row");
+  NT_REQUIRE(a && a_scale && seg_offsets && w_packed && w_scale && c,
+             "grouped_gemm_fp8_packed: null buffer");
+  NT_REQUIRE(aligned_to(a, 32) && aligned16(w_packed) && aligned_to(c, 8),
+             "grouped_gemm_fp8_packed: a 32-byte, w_packed 16-byte and c 8-byte aligned");
+  if (total_rows == 0) return ok();
+  hipError_t err = launch_grouped_gemm_fp8(a, ld_a, a_rows, a_scale, src_row, seg_offsets,
+                                           num_segments, total_rows, w_packed, w_scale, K, n_out,
+                                           epilogue, true, c,
+                                           reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "grouped_gemm_fp8_packed");
 }
 
 int nt_moe_combine_aux(const uint16_t* y, const int32_t* combine_dest, const float* combine_w,

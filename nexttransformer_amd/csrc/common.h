@@ -94,8 +94,10 @@ hipError_t launch_grouped_gemm_fp8(const uint8_t* a, int64_t ld_a, int64_t a_row
                                    const float* a_scale, const int32_t* src_row,
                                    const int32_t* seg_offsets, int num_segments,
                                    int64_t total_rows, const uint8_t* w, const float* w_scale,
-                                   int K, int n_out, int epilogue, uint16_t* c,
+                                   int K, int n_out, int epilogue, bool packed, uint16_t* c,
                                    hipStream_t stream);
+hipError_t launch_pack_weights_fp8(const uint8_t* w, int64_t S, int R, int K, int epilogue,
+                                   uint8_t* packed, hipStream_t stream);
 
 hipError_t launch_pack_weights_bf16(const uint16_t* w, int64_t S, int R, int K, int epilogue,
                                     uint16_t* packed, hipStream_t stream);

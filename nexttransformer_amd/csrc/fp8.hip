@@ -128,7 +128,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * u * __builtin_amdgcn_rcpf(1.f + __expf(-g));
 }
 
-template <int EPI>
+template <int EPI, bool PACKED>
 __global__ __launch_bounds__(256) void fp8_grouped_gemm_kernel(
     const uint8_t* __restrict__ a, int64_t ld_a, int64_t a_rows, const float* __restrict__ a_scale,
     const int32_t* __restrict__ src_row, const int32_t* __restrict__ seg_offsets,
@@ -155,7 +155,35 @@ __global__ __launch_bounds__(256) void fp8_grouped_gemm_kernel(
   else
     wrow = col0 + li;
   const bool wvalid = EPI == NT_MOE_EPI_SWIGLU ? (col0 + (li & 15) < n_out) : (wrow < n_out);
-  const uint8_t* wp = w + ((int64_t)seg * w_rows + (wvalid ? wrow : col0)) * K + half * 32;
+  // Unpacked: row wrow of the segment's [R, K] matrix, this lane's 32 bytes of each 64-wide step.
+  // Packed: the wave's 32-row group nb is a run of 4 KB blocks (one per 128-wide K block) in
+  // which the two 16-byte chunks of lane l for step st sit at ((2 st + h) * 64 + l) * 16.
+  const uint8_t* wp;
+  int64_t w_step;  // bytes from one 128-wide K block to the next
+  if (PACKED) {
+    const int nb = col0 / Tile::kColsPerWave;
+    wp = w + (((int64_t)seg * (w_rows / 32) + nb) * kblocks) * 4096 + lane * 16;
+    w_step = 4096;
+  } else {
+    wp = w + ((int64_t)seg * w_rows + (wvalid ? wrow : col0)) * K + half * 32;
+    w_step = kScaleBlock;
+  }
+  auto load_w = [&](int64_t kb, i32x8& s0, i32x8& s1) {
+    if (PACKED) {
+      const uint8_t* b = wp + kb * w_step;
+      const u32x4 c0 = *reinterpret_cast<const u32x4*>(b);
+      const u32x4 c1 = *reinterpret_cast<const u32x4*>(b + 1024);
+      const u32x4 c2 = *reinterpret_cast<const u32x4*>(b + 2048);
+      const u32x4 c3 = *reinterpret_cast<const u32x4*>(b + 3072);
+      s0 = i32x8{(int)c0[0], (int)c0[1], (int)c0[2], (int)c0[3],
+                 (int)c1[0], (int)c1[1], (int)c1[2], (int)c1[3]};
+      s1 = i32x8{(int)c2[0], (int)c2[1], (int)c2[2], (int)c2[3],
+                 (int)c3[0], (int)c3[1], (int)c3[2], (int)c3[3]};
+    } else {
+      s0 = *reinterpret_cast<const i32x8*>(wp + kb * w_step);
+      s1 = *reinterpret_cast<const i32x8*>(wp + kb * w_step + 64);
+    }
+  };
   // scale rows of the gate (or only) half and of the value half
   const float* ws_lo = w_scale + ((int64_t)seg * scale_rows + col0 / kScaleBlock) * kblocks;
   const float* ws_hi =
@@ -172,8 +200,8 @@ __global__ __launch_bounds__(256) void fp8_grouped_gemm_kernel(
     const uint8_t* ap = a + arow * ld_a + half * 32;
 
     const i32x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
-    i32x8 wa0 = *reinterpret_cast<const i32x8*>(wp);
-    i32x8 wa1 = *reinterpret_cast<const i32x8*>(wp + 64);
+    i32x8 wa0, wa1;
+    load_w(0, wa0, wa1);
     i32x8 xb0 = tvalid ? *reinterpret_cast<const i32x8*>(ap) : zero8;
     i32x8 xb1 = tvalid ? *reinterpret_cast<const i32x8*>(ap + 64) : zero8;
     floatx16 acc = {};
@@ -181,8 +209,7 @@ __global__ __launch_bounds__(256) void fp8_grouped_gemm_kernel(
       i32x8 nwa0 = wa0, nwa1 = wa1, nxb0 = xb0, nxb1 = xb1;
       if (kb + 1 < kblocks) {
         const int64_t off = (int64_t)(kb + 1) * kScaleBlock;
-        nwa0 = *reinterpret_cast<const i32x8*>(wp + off);
-        nwa1 = *reinterpret_cast<const i32x8*>(wp + off + 64);
+        load_w(kb + 1, nwa0, nwa1);
         nxb0 = tvalid ? *reinterpret_cast<const i32x8*>(ap + off) : zero8;
         nxb1 = tvalid ? *reinterpret_cast<const i32x8*>(ap + off + 64) : zero8;
       }
@@ -258,30 +285,61 @@ hipError_t launch_grouped_gemm_fp8(const uint8_t* a, int64_t ld_a, int64_t a_row
                                    const float* a_scale, const int32_t* src_row,
                                    const int32_t* seg_offsets, int num_segments,
                                    int64_t total_rows, const uint8_t* w, const float* w_scale,
-                                   int K, int n_out, int epilogue, uint16_t* c,
+                                   int K, int n_out, int epilogue, bool packed, uint16_t* c,
                                    hipStream_t stream) {
   const int per_block = epilogue == NT_MOE_EPI_SWIGLU ? Fp8Tile<NT_MOE_EPI_SWIGLU>::kColsPerBlock
                                                       : Fp8Tile<NT_MOE_EPI_NONE>::kColsPerBlock;
   const int n_tiles = ceil_div(n_out, per_block);
   const dim3 grid((unsigned)((int64_t)num_segments * n_tiles)), block(256);
   if (total_rows == 0) return hipSuccess;
+#define NT_F8(EPI, P)                                                                            \
+  fp8_grouped_gemm_kernel<EPI, P><<<grid, block, 0, stream>>>(a, ld_a, a_rows, a_scale, src_row, \
+                                                              seg_offsets, total_rows, w,        \
+                                                              w_scale, K, n_out, n_tiles, c)
   switch (epilogue) {
     case NT_MOE_EPI_SWIGLU:
-      fp8_grouped_gemm_kernel<NT_MOE_EPI_SWIGLU><<<grid, block, 0, stream>>>(
-          a, ld_a, a_rows, a_scale, src_row, seg_offsets, total_rows, w, w_scale, K, n_out,
-          n_tiles, c);
+      if (packed) NT_F8(NT_MOE_EPI_SWIGLU, true); else NT_F8(NT_MOE_EPI_SWIGLU, false);
       break;
     case NT_MOE_EPI_RELU2:
-      fp8_grouped_gemm_kernel<NT_MOE_EPI_RELU2><<<grid, block, 0, stream>>>(
-          a, ld_a, a_rows, a_scale, src_row, seg_offsets, total_rows, w, w_scale, K, n_out,
-          n_tiles, c);
+      if (packed) NT_F8(NT_MOE_EPI_RELU2, true); else NT_F8(NT_MOE_EPI_RELU2, false);
       break;
     default:
-      fp8_grouped_gemm_kernel<NT_MOE_EPI_NONE><<<grid, block, 0, stream>>>(
-          a, ld_a, a_rows, a_scale, src_row, seg_offsets, total_rows, w, w_scale, K, n_out,
-          n_tiles, c);
+      if (packed) NT_F8(NT_MOE_EPI_NONE, true); else NT_F8(NT_MOE_EPI_NONE, false);
       break;
   }
+#undef NT_F8
+  return hipGetLastError();
+}
+
+// Packs e4m3 weights w [S, R, K] for the packed fp8 GEMM: 32-row groups (for SwiGLU 16 gate
+// rows then the 16 value rows of the same columns), each a run of 4 KB blocks per 128-wide K
+// block, chunk ((2 st + h) * 64 + l) of a block holding row l % 32 and K bytes
+// 128 kb + 64 st + 32 (l / 32) + 16 h .. + 16.
+__global__ __launch_bounds__(256) void pack_fp8_kernel(const uint8_t* __restrict__ w,
+                                                        int64_t chunks, int R, int K, int n_out,
+                                                        int swiglu, uint8_t* __restrict__ out) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= chunks) return;
+  const int KB = K / 128, NB = R / 32;
+  const int l = (int)(c % 64), sh = (int)((c / 64) % 4), st = sh / 2, h = sh % 2;
+  const int kb = (int)((c / 256) % KB);
+  const int64_t rest = c / (256 * (int64_t)KB);
+  const int nb = (int)(rest % NB);
+  const int64_t s = rest / NB;
+  const int i = l % 32;
+  const int row = swiglu ? (i < 16 ? 16 * nb + i : n_out + 16 * nb + (i - 16)) : 32 * nb + i;
+  const int k0 = kb * 128 + st * 64 + 32 * (l / 32) + 16 * h;
+  *reinterpret_cast<u32x4*>(out + c * 16) =
+      *reinterpret_cast<const u32x4*>(w + (s * R + row) * (int64_t)K + k0);
+}
+
+hipError_t launch_pack_weights_fp8(const uint8_t* w, int64_t S, int R, int K, int epilogue,
+                                   uint8_t* packed, hipStream_t stream) {
+  const int n_out = epilogue == NT_MOE_EPI_SWIGLU ? R / 2 : R;
+  const int64_t chunks = S * (int64_t)R * K / 16;
+  if (chunks == 0) return hipSuccess;
+  pack_fp8_kernel<<<dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream>>>(
+      w, chunks, R, K, n_out, epilogue == NT_MOE_EPI_SWIGLU ? 1 : 0, packed);
   return hipGetLastError();
 }
 

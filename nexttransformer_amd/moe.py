@@ -188,7 +188,7 @@ class MoELayer(nn.Module):
             # The packed-weight GEMM (fragment-ordered weights streamed into registers) when every
             # projection's K and width qualify and the weights live on the GPU.
             widths = [r.expert_width] + ([r.shared_expert_width] if self.shared_experts else [])
-            use_packed = (not fp8 and self.router.weight.is_cuda and all(
+            use_packed = fp8 or (self.router.weight.is_cuda and all(
                 ops.packable(dp, _round_up(h, align), nat.EPI_SWIGLU if gated else nat.EPI_RELU2)
                 and ops.packable(_round_up(h, align), dp, nat.EPI_NONE) for h in widths))
 
@@ -218,7 +218,9 @@ class MoELayer(nn.Module):
                     return w1, None, w2, None
                 w1q, w1s = ops.quantize_fp8_blockwise(w1.contiguous())
                 w2q, w2s = ops.quantize_fp8_blockwise(w2.contiguous())
-                return w1q, w1s, w2q, w2s
+                up = nat.EPI_SWIGLU if gated else nat.EPI_RELU2
+                return (ops.pack_expert_weights_fp8(w1q, up), w1s,
+                        ops.pack_expert_weights_fp8(w2q, nat.EPI_NONE), w2s)
 
             router_t = torch.zeros(dp, r.routed_experts, device=self.router.weight.device,
                                    dtype=torch.float32)

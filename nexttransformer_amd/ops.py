@@ -338,10 +338,31 @@ def _(w):
             w.new_empty((S, R // 128, C // 128), dtype=torch.float32))
 
 
+@torch.library.custom_op("ntmoe::pack_expert_weights_fp8", mutates_args=())
+def pack_expert_weights_fp8(w: Tensor, epilogue: int) -> Tensor:
+    """e4m3 expert weights [S, rows, K] (uint8) rearranged for grouped_gemm_fp8(packed=True)."""
+    _on_gpu(w)
+    _require(w.dtype == torch.uint8 and w.dim() == 3 and w.is_contiguous(),
+             "pack_expert_weights_fp8: w must be contiguous uint8 (e4m3) [S, rows, K]")
+    S, R, K = w.shape
+    out = torch.empty_like(w)
+    st = nat.load().nt_moe_pack_expert_weights_fp8(ptr(w), S, R, K, epilogue, ptr(out),
+                                                   _stream(w.device))
+    nat.check(st, "ntmoe::pack_expert_weights_fp8")
+    return out
+
+
+@pack_expert_weights_fp8.register_fake
+def _(w, epilogue):
+    return torch.empty_like(w)
+
+
 @torch.library.custom_op("ntmoe::grouped_gemm_fp8", mutates_args=())
 def grouped_gemm_fp8(a: Tensor, a_scale: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor,
-                     w: Tensor, w_scale: Tensor, epilogue: int, total_rows: int) -> Tensor:
-    """c bf16 [rows, n_out] = epilogue(a_scale . sum_kb w_scale . (a_q . w_q^T)_kb) per segment."""
+                     w: Tensor, w_scale: Tensor, epilogue: int, total_rows: int,
+                     packed: bool = False) -> Tensor:
+    """c bf16 [rows, n_out] = epilogue(a_scale . sum_kb w_scale . (a_q . w_q^T)_kb) per segment;
+    with `packed`, w comes from pack_expert_weights_fp8 (same epilogue)."""
     _on_gpu(a, a_scale, src_row, seg_offsets, w, w_scale)
     _require(a.dtype == torch.uint8 and a.dim() == 2 and a.stride(1) == 1,
              "grouped_gemm_fp8: a must be uint8 (e4m3) [*, K] with contiguous rows")
@@ -360,16 +381,16 @@ def grouped_gemm_fp8(a: Tensor, a_scale: Tensor, src_row: Optional[Tensor], seg_
         _require(src_row.dtype == torch.int32 and src_row.is_contiguous(),
                  "grouped_gemm_fp8: src_row must be contiguous int32")
     c = torch.empty(total_rows, n_out, device=a.device, dtype=torch.bfloat16)
-    st = nat.load().nt_moe_grouped_gemm_fp8(ptr(a), a.stride(0), a.shape[0], ptr(a_scale),
-                                            ptr(src_row), ptr(seg_offsets), S, total_rows, ptr(w),
-                                            ptr(w_scale), K, n_out, epilogue, ptr(c),
-                                            _stream(a.device))
+    fn = (nat.load().nt_moe_grouped_gemm_fp8_packed if packed
+          else nat.load().nt_moe_grouped_gemm_fp8)
+    st = fn(ptr(a), a.stride(0), a.shape[0], ptr(a_scale), ptr(src_row), ptr(seg_offsets), S,
+            total_rows, ptr(w), ptr(w_scale), K, n_out, epilogue, ptr(c), _stream(a.device))
     nat.check(st, "ntmoe::grouped_gemm_fp8")
     return c
 
 
 @grouped_gemm_fp8.register_fake
-def _(a, a_scale, src_row, seg_offsets, w, w_scale, epilogue, total_rows):
+def _(a, a_scale, src_row, seg_offsets, w, w_scale, epilogue, total_rows, packed=False):
     R = w.shape[1]
     return a.new_empty((total_rows, R // 2 if epilogue == nat.EPI_SWIGLU else R),
                        dtype=torch.bfloat16)
@@ -444,8 +465,9 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
     Returns (out [T, d] bf16, aux fp32 [3] = {lb + z, lb, z}, state with the routing tensors).
     With permute_rows the token rows are first moved into expert order by the permute kernel
     (x_perm); by default the up-projection GEMM gathers them itself.
-    packed: w1 (and shared_w1) were packed by pack_expert_weights with the up epilogue, w2 (and
-    shared_w2) with EPI_NONE; the packed grouped GEMM runs both projections.
+    packed: w1 (and shared_w1) were packed by pack_expert_weights (bf16) or
+    pack_expert_weights_fp8 (e4m3) with the up epilogue, w2 (and shared_w2) with EPI_NONE; the
+    packed grouped GEMMs run both projections.
     fp8 experts: pass w1/w2 (and the shared expert's) as uint8 e4m3 codes with their 128 x 128
     block scales (w*_scale, from quantize_fp8_blockwise); the token rows and the intermediate
     h are then quantised per row and both projections run on the fp8 grouped GEMM.
@@ -477,18 +499,19 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
                  "moe_forward: fp8 weights need w1_scale and w2_scale")
         xq, xs = quantize_fp8_rowwise(x)
         mark("quantize")
-        h = grouped_gemm_fp8(xq, xs, src, offsets, w1, w1_scale, up_epi, A)
+        h = grouped_gemm_fp8(xq, xs, src, offsets, w1, w1_scale, up_epi, A, packed)
         mark("gemm_up")
         hq, hs = quantize_fp8_rowwise(h)
-        y = grouped_gemm_fp8(hq, hs, None, offsets, w2, w2_scale, nat.EPI_NONE, A)
+        y = grouped_gemm_fp8(hq, hs, None, offsets, w2, w2_scale, nat.EPI_NONE, A, packed)
         mark("gemm_down")
         shared_y = None
         if shared_w1 is not None:
             seg = _whole_batch_segment(T, x.device)
-            hs_ = grouped_gemm_fp8(xq, xs, None, seg, shared_w1, shared_w1_scale, up_epi, T)
+            hs_ = grouped_gemm_fp8(xq, xs, None, seg, shared_w1, shared_w1_scale, up_epi, T,
+                                   packed)
             hsq, hss = quantize_fp8_rowwise(hs_)
             shared_y = grouped_gemm_fp8(hsq, hss, None, seg, shared_w2, shared_w2_scale,
-                                        nat.EPI_NONE, T)
+                                        nat.EPI_NONE, T, packed)
             mark("shared")
         out, aux = combine_aux(y, cdest, cw, shared_y, pp, zp, counts, aux_coeff, z_coeff)
         mark("combine")

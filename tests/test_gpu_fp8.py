@@ -58,8 +58,34 @@ def _segments(counts):
 
 
 @pytest.mark.parametrize("epilogue", [0, 1, 2], ids=["swiglu", "relu2", "none"])
+def test_fp8_pack_layout(epilogue):
+    """Packed fp8 layout against its definition, rebuilt on the CPU with numpy indexing."""
+    import numpy as np
+    from nexttransformer_amd import ops
+    g = torch.Generator().manual_seed(20 + epilogue)
+    S, R, K = 2, 256, 384
+    n_out = R // 2 if epilogue == 0 else R
+    w = torch.randint(0, 256, (S, R, K), generator=g, dtype=torch.uint8)
+    got = ops.pack_expert_weights_fp8(w.cuda(), epilogue).cpu().numpy().reshape(-1, 16)
+    wn = w.numpy()
+    NB, KB = R // 32, K // 128
+    lanes = np.arange(64)
+    i = lanes % 32
+    want = np.empty((S, NB, KB, 2, 2, 64, 16), dtype=np.uint8)
+    for nb in range(NB):
+        rows = np.where(i < 16, 16 * nb + i, n_out + 16 * nb + i - 16) if epilogue == 0 else 32 * nb + i
+        for kb in range(KB):
+            for st in range(2):
+                for h in range(2):
+                    k0 = kb * 128 + st * 64 + 32 * (lanes // 32) + 16 * h
+                    want[:, nb, kb, st, h] = wn[:, rows[:, None], k0[:, None] + np.arange(16)[None, :]]
+    assert np.array_equal(got, want.reshape(-1, 16))
+
+
+@pytest.mark.parametrize("epilogue", [0, 1, 2], ids=["swiglu", "relu2", "none"])
 @pytest.mark.parametrize("gather", [False, True])
-def test_fp8_grouped_gemm_matches_dequantised_product(epilogue, gather):
+@pytest.mark.parametrize("packed", [False, True], ids=["plain", "packed"])
+def test_fp8_grouped_gemm_matches_dequantised_product(epilogue, gather, packed):
     from nexttransformer_amd import _native as nat
     from nexttransformer_amd import ops
     g = torch.Generator().manual_seed(10 + epilogue)
@@ -74,8 +100,9 @@ def test_fp8_grouped_gemm_matches_dequantised_product(epilogue, gather):
     aq, as_ = orc.quantize_rowwise(a.float())
     wq, ws = orc.quantize_blockwise(w)
     seg = _segments(counts)
+    wdev = ops.pack_expert_weights_fp8(wq.cuda(), epilogue) if packed else wq.cuda()
     c = ops.grouped_gemm_fp8(aq.cuda(), as_.cuda(), None if src is None else src.cuda(),
-                             seg.cuda(), wq.cuda(), ws.cuda(), epilogue, rows)
+                             seg.cuda(), wdev, ws.cuda(), epilogue, rows, packed)
     torch.cuda.synchronize()
     a_deq = orc.dequantize_rowwise(aq, as_).double()
     w_deq = orc.dequantize_blockwise(wq, ws).double()
@@ -105,13 +132,16 @@ def _fp8_layer_inputs(T, d, E, H, seed, device):
 
 @pytest.mark.parametrize("T,d,E,k,H", [(64, 512, 16, 4, 256), (5, 256, 8, 8, 128),
                                          (200, 1024, 32, 2, 512)])
-def test_fp8_layer_matches_dequantised_reference(T, d, E, k, H):
+@pytest.mark.parametrize("packed", [False, True], ids=["plain", "packed"])
+def test_fp8_layer_matches_dequantised_reference(T, d, E, k, H, packed):
     from nexttransformer_amd import ops
     x, router, w1, w2 = _fp8_layer_inputs(T, d, E, H, T + d, "cpu")
     w1q, w1s = ops.quantize_fp8_blockwise(w1.cuda())
     w2q, w2s = ops.quantize_fp8_blockwise(w2.cuda())
-    out, aux, st = ops.moe_forward(x.cuda(), router.t().contiguous().cuda(), w1q, w2q, top_k=k,
-                                   w1_scale=w1s, w2_scale=w2s)
+    pk = (lambda t, e: ops.pack_expert_weights_fp8(t, e)) if packed else (lambda t, e: t)
+    out, aux, st = ops.moe_forward(x.cuda(), router.t().contiguous().cuda(), pk(w1q, 0),
+                                   pk(w2q, 2), top_k=k, w1_scale=w1s, w2_scale=w2s,
+                                   packed=packed)
     torch.cuda.synchronize()
     ref = orc.moe_forward_fp8(x, router, w1q.cpu(), w1s.cpu(), w2q.cpu(), w2s.cpu(), k)
     assert torch.equal(st["ids"].cpu(), ref["ids"])
@@ -131,8 +161,10 @@ def test_fp8_layer_config5_full_size():
     del w1
     w2q, w2s = ops.quantize_fp8_blockwise(w2)
     del w2
-    out, aux, st = ops.moe_forward(x, router.t().contiguous(), w1q, w2q, top_k=case.k,
-                                   w1_scale=w1s, w2_scale=w2s)
+    out, aux, st = ops.moe_forward(x, router.t().contiguous(),
+                                   ops.pack_expert_weights_fp8(w1q, 0),
+                                   ops.pack_expert_weights_fp8(w2q, 2), top_k=case.k,
+                                   w1_scale=w1s, w2_scale=w2s, packed=True)
     torch.cuda.synchronize()
     tokens = [0, 17, 40, 63]
     ref = orc.moe_forward_fp8(x.cpu(), router.cpu(), w1q, w1s, w2q, w2s, case.k, tokens=tokens)

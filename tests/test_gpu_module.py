@@ -116,6 +116,8 @@ def test_module_forward_matches_oracle(kw):
     dict(width=96, heads=2, expert_width=24),  # ReLU^2 + shared, padded to 128
 ], ids=["swiglu-512", "relu2-shared-padded"])
 def test_module_fp8_matches_dequantised_reference(kw):
+    """The module quantises its fp32 masters (zero-padded to multiples of 128) per 128 x 128 block
+    and packs them; the reference quantises the same padded masters with the oracle."""
     from nexttransformer_amd.moe import MoELayer
     r = _recipe(expert_dtype="fp8", **kw)
     m = MoELayer(r, 2)
@@ -124,18 +126,37 @@ def test_module_fp8_matches_dequantised_reference(kw):
     with torch.no_grad():
         out, aux = m(hidden)
     p = m.packed_weights()
-    assert p["w1"].dtype == torch.uint8 and p["w1_scale"] is not None
-    act = orc.SWIGLU if r.activation == "swiglu" else orc.RELU2
+    assert p["w1"].dtype == torch.uint8 and p["packed"]
+    gated = r.activation == "swiglu"
+    act = orc.SWIGLU if gated else orc.RELU2
     dp = p["router_t"].shape[0]
-    x = torch.nn.functional.pad(hidden.reshape(-1, r.width).cpu(), (0, dp - r.width))
+    up128 = lambda n: (n + 127) // 128 * 128
+
+    def padded(experts, hidden_w):
+        hp = up128(hidden_w)
+        n = len(experts)
+        w1 = torch.zeros(n, (2 if gated else 1) * hp, dp)
+        w2 = torch.zeros(n, dp, hp)
+        for i, e in enumerate(experts):
+            fc1 = e.linear_fc1.weight.detach().cpu()
+            if gated:
+                w1[i, :hidden_w, :r.width] = fc1[:hidden_w]
+                w1[i, hp:hp + hidden_w, :r.width] = fc1[hidden_w:]
+            else:
+                w1[i, :hidden_w, :r.width] = fc1
+            w2[i, :r.width, :hidden_w] = e.linear_fc2.weight.detach().cpu()
+        return orc.quantize_blockwise(w1) + orc.quantize_blockwise(w2)
+
+    w1q, w1s, w2q, w2s = padded(list(m.experts.local_experts), r.expert_width)
+    assert torch.equal(w1s, p["w1_scale"].cpu()) and torch.equal(w2s, p["w2_scale"].cpu())
     shared = None
     if m.shared_experts is not None:
-        shared = tuple(p[n][0].cpu() for n in ("shared_w1", "shared_w1_scale", "shared_w2",
-                                              "shared_w2_scale"))
+        sq = padded([m.shared_experts], r.shared_expert_width)
+        shared = tuple(t[0] for t in sq)
+    x = torch.nn.functional.pad(hidden.reshape(-1, r.width).cpu(), (0, dp - r.width))
     ref = orc.moe_forward_fp8(x, torch.nn.functional.pad(m.router.weight.detach().cpu(),
                                                          (0, dp - r.width)),
-                              p["w1"].cpu(), p["w1_scale"].cpu(), p["w2"].cpu(),
-                              p["w2_scale"].cpu(), r.top_k, activation=act, shared=shared)
+                              w1q, w1s, w2q, w2s, r.top_k, activation=act, shared=shared)
     ref_out = ref["out"][:, :r.width]
     assert torch.equal(m.last_load.cpu(), ref["counts"].long())
     assert rel_l2(out.float().reshape(-1, r.width), ref_out) <= 3e-2
