@@ -91,15 +91,17 @@ __device__ __forceinline__ void list_insert(float v, int e, float* lv, int* li) 
 }
 
 // Top-k, weights, full scores and aux partials for the 64 tokens whose logits sit in the
-// LDS tile lg[64][E+1]; overwrites lg with the full scores s_te. Called by all 256 threads.
-template <int KMAX>
+// LDS tile lg[64][E+1]; overwrites lg with the full scores s_te. Called by all 64 * LPT threads
+// of the block: LPT lanes per token, each scanning every LPT-th expert.
+template <int KMAX, int LPT = 4>
 __device__ void topk_and_scores(float* lg, float* zt, int64_t t0, int64_t T, int E, int k,
                                 int score_fn, int32_t* __restrict__ topk_ids,
                                 float* __restrict__ topk_w, float* __restrict__ prob_partial,
                                 float* __restrict__ z_partial) {
+  static_assert(LPT == 4 || LPT == 8 || LPT == 16, "lanes per token");
   const int ldl = E + 1;
-  const int tt = threadIdx.x >> 2;  // token within the block
-  const int sub = threadIdx.x & 3;  // which quarter of the experts this lane scans
+  const int tt = threadIdx.x / LPT;   // token within the block
+  const int sub = threadIdx.x % LPT;  // which of the LPT expert strides this lane scans
   const int64_t t = t0 + tt;
   float* row = lg + tt * ldl;
 
@@ -107,9 +109,9 @@ __device__ void topk_and_scores(float* lg, float* zt, int64_t t0, int64_t T, int
   int li[KMAX];
 #pragma unroll
   for (int j = 0; j < KMAX; ++j) { lv[j] = -INFINITY; li[j] = 0x7fffffff; }
-  for (int e = sub; e < E; e += 4) list_insert<KMAX>(row[e], e, lv, li);
+  for (int e = sub; e < E; e += LPT) list_insert<KMAX>(row[e], e, lv, li);
 
-  // k rounds: best head of the 4 lists (xor butterfly), the owner pops it.
+  // k rounds: best head of the LPT lists (xor butterfly), the owner pops it.
   float ov[KMAX];
   int oi[KMAX];
 #pragma unroll
@@ -117,7 +119,7 @@ __device__ void topk_and_scores(float* lg, float* zt, int64_t t0, int64_t T, int
     float bv = lv[0];
     int bi = li[0];
 #pragma unroll
-    for (int m = 1; m <= 2; m <<= 1) {
+    for (int m = 1; m < LPT; m <<= 1) {
       float v2 = __shfl_xor(bv, m);
       int i2 = __shfl_xor(bi, m);
       if (rank_before(v2, i2, bv, bi)) { bv = v2; bi = i2; }
@@ -145,7 +147,7 @@ __device__ void topk_and_scores(float* lg, float* zt, int64_t t0, int64_t T, int
   if (t < T) {
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) {
-      if (j < k && (j & 3) == sub) {
+      if (j < k && j % LPT == sub) {
         topk_ids[t * k + j] = oi[j];
         topk_w[t * k + j] = wv[j] * winv;
       }
@@ -154,21 +156,22 @@ __device__ void topk_and_scores(float* lg, float* zt, int64_t t0, int64_t T, int
 
   // Full scores s_te for the load-balance loss, logsumexp for the z-loss.
   float part = 0.f, spart = 0.f;
-  for (int e = sub; e < E; e += 4) {
+  for (int e = sub; e < E; e += LPT) {
     part += expf(row[e] - top);
     if (score_fn == NT_MOE_SCORE_SIGMOID) spart += 1.f / (1.f + expf(-row[e]));
   }
-  part += __shfl_xor(part, 1);
-  part += __shfl_xor(part, 2);
-  spart += __shfl_xor(spart, 1);
-  spart += __shfl_xor(spart, 2);
+#pragma unroll
+  for (int m = 1; m < LPT; m <<= 1) {
+    part += __shfl_xor(part, m);
+    spart += __shfl_xor(spart, m);
+  }
   const float lse = top + logf(part);
   if (score_fn == NT_MOE_SCORE_SOFTMAX) {
     const float inv = 1.f / part;
-    for (int e = sub; e < E; e += 4) row[e] = expf(row[e] - top) * inv;
+    for (int e = sub; e < E; e += LPT) row[e] = expf(row[e] - top) * inv;
   } else {
     const float inv = 1.f / spart;
-    for (int e = sub; e < E; e += 4) row[e] = inv / (1.f + expf(-row[e]));
+    for (int e = sub; e < E; e += LPT) row[e] = inv / (1.f + expf(-row[e]));
   }
   if (sub == 0) zt[tt] = lse * lse;
   __syncthreads();
@@ -272,10 +275,45 @@ __global__ __launch_bounds__(256) void router_partial_kernel(
   }
 }
 
+// Sums the nchunk partial planes of the split router into plane 0, in place, in the fixed order
+// ((p0 + p1) + p2) + ... then + bias[e]: four consecutive (t, e) values per thread, the planes'
+// loads issued together. This keeps the plane reduction off the top-k kernel, whose grid has one
+// block per 64 tokens and so cannot hide the loads' latency when T is small.
+__global__ __launch_bounds__(256) void router_sum_planes_kernel(float* __restrict__ partials,
+                                                                 int nchunk,
+                                                                 const float* __restrict__ bias,
+                                                                 int64_t n4, int E) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const int64_t plane4 = n4;  // plane size in float4 units
+  floatx4* p = reinterpret_cast<floatx4*>(partials) + i;
+  floatx4 v = p[0];
+  for (int c0 = 1; c0 < nchunk; c0 += 8) {
+    floatx4 part[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (c0 + j < nchunk) part[j] = p[(int64_t)(c0 + j) * plane4];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (c0 + j < nchunk) {
+        v[0] = v[0] + part[j][0];
+        v[1] = v[1] + part[j][1];
+        v[2] = v[2] + part[j][2];
+        v[3] = v[3] + part[j][3];
+      }
+  }
+  if (bias) {
+    const int e0 = (int)((i * 4) % E);  // E % 4 == 0: the four values share a row
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = v[j] + bias[e0 + j];
+  }
+  p[0] = v;
+}
+
 // Sum nchunk partial planes in ascending order (+ bias), then top-k. With nchunk = 1 and no
 // bias this is top-k on caller-supplied logits.
 template <int KMAX>
-__global__ __launch_bounds__(256) void router_topk_kernel(
+__global__ __launch_bounds__(1024) void router_topk_kernel(
     const float* __restrict__ partials, int nchunk, const float* __restrict__ bias, int64_t T,
     int E, int k, int score_fn, float* __restrict__ logits, int32_t* __restrict__ topk_ids,
     float* __restrict__ topk_w, float* __restrict__ prob_partial, float* __restrict__ z_partial) {
@@ -286,7 +324,35 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   // Chunk planes are summed in ascending order; loads go out 8 planes at a time so the sum is
   // not a chain of dependent memory round trips.
   const int64_t plane = T * E;
-  for (int idx = threadIdx.x; idx < kRouteBlock * E; idx += blockDim.x) {
+  if (nchunk == 1) {
+    // One plane (the split router's planes are summed by router_sum_planes_kernel): eight loads
+    // per thread go out together, so a block does not wait on one round trip per element.
+    for (int base = threadIdx.x; base < kRouteBlock * E; base += 8 * blockDim.x) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int idx = base + j * blockDim.x;
+        const int r = idx / E, e = idx - r * E;
+        const int64_t t = t0 + r;
+        v[j] = (idx < kRouteBlock * E && t < T) ? partials[t * E + e] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int idx = base + j * blockDim.x;
+        if (idx >= kRouteBlock * E) break;
+        const int r = idx / E, e = idx - r * E;
+        const int64_t t = t0 + r;
+        float val = v[j];
+        if (t < T) {
+          if (bias) val = val + bias[e];
+          if (logits) logits[t * E + e] = val;
+        }
+        lg[r * (E + 1) + e] = val;
+      }
+    }
+  }
+  for (int idx = nchunk == 1 ? kRouteBlock * E : threadIdx.x; idx < kRouteBlock * E;
+       idx += blockDim.x) {
     int r = idx / E, e = idx - r * E;
     int64_t t = t0 + r;
     float v = 0.f;
@@ -307,7 +373,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     lg[r * (E + 1) + e] = v;
   }
   __syncthreads();
-  topk_and_scores<KMAX>(lg, zt, t0, T, E, k, score_fn, topk_ids, topk_w, prob_partial,
+  topk_and_scores<KMAX, 16>(lg, zt, t0, T, E, k, score_fn, topk_ids, topk_w, prob_partial,
                         z_partial);
 }
 
@@ -339,7 +405,7 @@ hipError_t launch_topk_k(const float* partials, int nchunk, const float* bias, i
   hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(router_topk_kernel<KMAX>),
                                      router_lds_bytes(E));
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL((router_topk_kernel<KMAX>), grid, dim3(256), router_lds_bytes(E), stream,
+  hipLaunchKernelGGL((router_topk_kernel<KMAX>), grid, dim3(1024), router_lds_bytes(E), stream,
                      partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp);
   return hipGetLastError();
 }
@@ -412,8 +478,11 @@ hipError_t launch_router(const uint16_t* x, int64_t ld_x, const float* wt, const
       default: return hipErrorInvalidValue;
     }
   }
-  // Split: smaller expert groups give more blocks when T is small.
+  // Split: smaller expert groups give more blocks when T is small (aim for >= 4 per CU: each
+  // block is a single wave whose weight loads nothing else on the CU would hide).
   int epw_split = epw < 16 ? epw : 16;
+  const int64_t row_chunks = (int64_t)ceil_div(T, kRouteBlock) * ceil_div(d, kRouterChunk);
+  while (epw_split > 1 && row_chunks * ceil_div(E, 4 * epw_split) < 4LL * num_cus()) epw_split /= 2;
   hipError_t err;
   switch (epw_split) {
     case 1: err = launch_partial_e<1>(x, ld_x, wt, T, d, E, partials, stream); break;
@@ -423,8 +492,18 @@ hipError_t launch_router(const uint16_t* x, int64_t ld_x, const float* wt, const
     default: err = launch_partial_e<16>(x, ld_x, wt, T, d, E, partials, stream); break;
   }
   if (err != hipSuccess) return err;
-  return launch_topk_any(partials, ceil_div(d, kRouterChunk), bias, T, E, k, score_fn, logits,
-                         topk_ids, topk_w, prob_partial, z_partial, stream);
+  const int nchunk = ceil_div(d, kRouterChunk);
+  if (E % 4 == 0) {
+    const int64_t n4 = T * E / 4;
+    router_sum_planes_kernel<<<dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream>>>(
+        partials, nchunk, bias, n4, E);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    return launch_topk_any(partials, 1, nullptr, T, E, k, score_fn, logits, topk_ids, topk_w,
+                           prob_partial, z_partial, stream);
+  }
+  return launch_topk_any(partials, nchunk, bias, T, E, k, score_fn, logits, topk_ids, topk_w,
+                         prob_partial, z_partial, stream);
 }
 
 hipError_t launch_topk_from_logits(const float* logits, int64_t T, int E, int k,
