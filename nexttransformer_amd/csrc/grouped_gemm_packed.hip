@@ -5,8 +5,9 @@
 //   c[r, j] = epilogue(a_src(r) . w_s[j, :])   for every row r of segment s.
 // What changes is how the two operands reach the matrix cores:
 //   * token rows (A, gathered through src_row for the up projection) are shared by all 8 waves
-//     of a workgroup, so they go through LDS, in a ring of 4 stages that the loads fill three
-//     K steps ahead (direct-to-LDS loads, XOR-swizzled so fragment reads are conflict-free);
+//     of a workgroup, so they go through LDS, in a ring of 4 stages: while one pair of K steps
+//     is computed from two stages, the next pair's two are loaded (direct-to-LDS loads,
+//     XOR-swizzled so fragment reads are conflict-free);
 //   * expert weights are not shared between waves (wave w owns weight rows [32 w, 32 w + 32) of
 //     the 256-row tile), so they skip LDS: each wave streams its own 4 KB per K step into
 //     registers, one K step ahead. The weights are packed once (pack kernel below) so that the
@@ -23,9 +24,13 @@
 // list, as the unpacked kernel does. The load pipeline runs across tile boundaries; the gather
 // indices of the next tile go into an LDS table four K steps before they are needed, so the
 // in-order completion of vector memory operations already guarantees them when they are read.
-// Waits count outstanding vector memory operations (loads and stores retire in order on this
-// GPU family): the issue order per K step g is B(g + 1) (weights, registers), then A(g + 3)
-// (token rows, LDS), then at the end of a tile the epilogue's fixed number of stores.
+// K steps go in pairs (g even, g + 1) with one workgroup barrier per pair: a barrier per K step
+// idles the matrix cores far more than its own latency (the waves of a SIMD, released together,
+// finish together and leave the pipe empty while the workgroup gathers). Waits count
+// outstanding vector memory operations (loads and stores retire in order on this GPU family):
+// the even step issues B(g + 1) (weights, registers), then A(g + 2) and A(g + 3) (token rows,
+// LDS, each with one gather-index load); the odd step issues B(g + 2); at the end of a tile the
+// epilogue's fixed number of stores follow.
 #include <math.h>
 #include <type_traits>
 
@@ -84,7 +89,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
     const uint16_t* __restrict__ A, int64_t ld_a, const int32_t* __restrict__ src_row,
     const int32_t* __restrict__ seg_offsets, int S, int total_rows, int64_t a_rows,
     const uint16_t* __restrict__ Wp, int K, int n_out, uint16_t* __restrict__ Cout) {
-  constexpr int ST = Ep<EPI>::kStores;
+  constexpr int G = GATHER ? 1 : 0;
   extern __shared__ __align__(16) unsigned char smem[];
   int* src_tab = reinterpret_cast<int*>(smem + kSA * kStage);  // [2][kBM]
   int* src_dummy = src_tab + 2 * kBM;                           // [kWaves][64] sink
@@ -157,7 +162,12 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
   // LDS; rows past the segment end repeat its last row (their results are dropped).
   const char* abase = reinterpret_cast<const char*>(A);
   // Byte offsets of this lane's four A chunks (one per load instruction) for tile t.
+  // Instruction q covers rows (wave kAQ + q) kRPI + [0, kRPI); a row's swizzle depends only on
+  // q % 2 and the lane, so two per-lane values serve every instruction.
+  static_assert(2 * kRPI == kWIN * kCH, "swizzle period of two load instructions");
   const int lrow = lane / kCH, lphys = lane % kCH;
+  const uint32_t aswz[2] = {(uint32_t)swz(lrow, lphys) * 16,
+                            (uint32_t)swz(kRPI + lrow, lphys) * 16};
   auto a_offsets = [&](const Tile& t, int slot, uint32_t (&aoff)[kAQ]) {
 #pragma unroll
     for (int q = 0; q < kAQ; ++q) {
@@ -166,30 +176,35 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
       if (GATHER) r = src_tab[slot * kBM + row];
       else r = t.m0 + row < t.seg_end ? t.m0 + row : t.seg_end - 1;
       r = r < 0 ? 0 : (r >= a_rows ? a_rows - 1 : r);
-      aoff[q] = (uint32_t)(r * ld_a * 2) + swz(row, lphys) * 16;
+      aoff[q] = (uint32_t)(r * ld_a * 2) + aswz[q % 2];
     }
   };
-  // This wave's packed weight blocks for tile t (clamped in a partial N tile).
+  // This wave's packed weight blocks for tile t (clamped in a partial N tile): a wave-uniform
+  // address, to which each lane adds lane * 16 bytes.
   auto w_base = [&](const Tile& t) {
     int nb = t.nt * kWaves + wave;
     nb = nb < NB ? nb : NB - 1;
-    return Wp + ((int64_t)t.s * NB + nb) * (int64_t)nk * kBlockElems + lane * 8;
+    return Wp + ((int64_t)t.s * NB + nb) * (int64_t)nk * kBlockElems;
   };
+  const uint32_t b_lane = lane * 16;
   // Weight loads are issued from inline assembly: the compiler then neither counts them nor
   // inserts its own (conservative, loop-merged) waits for their registers; the explicit wait
-  // before their use names the registers, so no use can be scheduled above it.
+  // before their use names the registers, so no use can be scheduled above it. The block address
+  // is a scalar operand, the lane offset the only vector one.
   auto load_b = [&](const uint16_t* blk, u32x4 (&b)[4]) {
-    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(b[0]) : "v"(blk) : "memory");
-    asm volatile("global_load_dwordx4 %0, %1, off offset:1024" : "=v"(b[1]) : "v"(blk) : "memory");
-    asm volatile("global_load_dwordx4 %0, %1, off offset:2048" : "=v"(b[2]) : "v"(blk) : "memory");
-    asm volatile("global_load_dwordx4 %0, %1, off offset:3072" : "=v"(b[3]) : "v"(blk) : "memory");
+    asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(b[0]) : "v"(b_lane), "s"(blk) : "memory");
+    asm volatile("global_load_dwordx4 %0, %1, %2 offset:1024"
+                 : "=v"(b[1]) : "v"(b_lane), "s"(blk) : "memory");
+    asm volatile("global_load_dwordx4 %0, %1, %2 offset:2048"
+                 : "=v"(b[2]) : "v"(b_lane), "s"(blk) : "memory");
+    asm volatile("global_load_dwordx4 %0, %1, %2 offset:3072"
+                 : "=v"(b[3]) : "v"(b_lane), "s"(blk) : "memory");
   };
 
-  // ---- producer: one A stage (+ one gather-index load) per K step, three steps ahead ---------
-  // Every K step issues the same vector memory operations -- 4 weight loads, 4 token-row loads,
-  // and with GATHER one gather-index load -- whether or not they are needed (past the end they
-  // re-read valid addresses into slots nobody reads), so the wait counts are the same in every
-  // step.
+  // ---- producer: one A stage (+ one gather-index load) per call, two calls per pair ----------
+  // Every call issues the same vector memory operations -- 4 token-row loads and, with GATHER,
+  // one gather-index load -- whether or not they are needed (past the end they re-read valid
+  // addresses into slots nobody reads), so the wait counts are the same in every pair.
   Tile pt, pnext;
   int p_idx = 0, p_kt = 0, p_slot = 0, produced = 0;
   uint32_t aoff[kAQ];
@@ -208,7 +223,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
 
   auto produce = [&]() {
     const bool live = produced < total_steps;
-    if (live && p_kt == nk) {  // next tile: its gather indices went out four steps ago
+    if (live && p_kt == nk) {  // next tile: its gather indices went out four stages ago
       pt = pnext;
       ++p_idx;
       p_kt = 0;
@@ -247,53 +262,44 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
   Tile ct = pt;
   const uint16_t* wb = w_base(ct);
   u32x4 b0[4], b1[4];
-  // Prologue: A(0), A(1), B(0), A(2); then B(0) (and with it A(0), A(1)) must land.
+  // Prologue: A(0), A(1), B(0), all landed before the first pair's barrier.
   produce();
   asm volatile("" ::: "memory");
   produce();
   asm volatile("" ::: "memory");
   load_b(wb, b0);
-  asm volatile("" ::: "memory");
-  produce();
-  asm volatile("s_waitcnt vmcnt(%4)"
-               : "+v"(b0[0]), "+v"(b0[1]), "+v"(b0[2]), "+v"(b0[3])
-               : "n"(kAQ + (GATHER ? 1 : 0))
-               : "memory");
+  asm volatile("s_waitcnt vmcnt(0)" : "+v"(b0[0]), "+v"(b0[1]), "+v"(b0[2]), "+v"(b0[3]) :: "memory");
 
-  // Operations issued after B(g+1) within step g: A(g+3) and, with GATHER, one index load.
-  constexpr int kAfterB = kAQ + (GATHER ? 1 : 0);
   int g = 0;          // global K step of this workgroup
   for (int ti = 0; ti < n_my; ++ti) {
     if (ti > 0) locate(ti, ct);
     const int live_m = ct.seg_end - ct.m0;  // token rows of this tile that exist (uniform)
+    const bool has_next = ti + 1 < n_my;
+    const uint16_t* wb_next = wb;
+    if (has_next) {
+      Tile nx;
+      locate(ti + 1, nx);
+      wb_next = w_base(nx);
+    }
     floatx16 acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = floatx16{};
-    const uint16_t* wb_next = wb;
 
-    // One K step: barrier, issue B(g+1), A(g+3) (+ gather indices), compute, then wait until
-    // B(g+1) is in its registers. That wait (vmcnt = the loads issued after B(g+1)) also
-    // completes A(g+1), A(g+2) and any epilogue stores, so at the next step's barrier every
-    // wave's part of A(g+1) has landed. Keeping the wait that names B's registers at the end of
-    // the step means no loop-carried copy of those registers can happen before they are valid.
-    auto step = [&](auto nj_c, int kt, u32x4 (&bc)[4], u32x4 (&bn)[4]) {
+    // K steps go in pairs (g even, g + 1) with one workgroup barrier per pair. The even step
+    // issues B(g + 1) and both token-row stages of the next pair, A(g + 2) and A(g + 3) (each
+    // with its index load), into the two slots the previous pair read; the odd step issues
+    // B(g + 2). Each step computes with B(g) and ends by waiting for the weights of the next
+    // step, which names their registers so no copy of them can happen before they are valid;
+    // the odd step's wait (vmcnt 0) also lands this wave's part of the next pair's stages,
+    // which the next barrier then publishes to every wave.
+    auto step = [&](auto nj_c, auto odd_c, int kt, u32x4 (&bc)[4], u32x4 (&bn)[4]) {
       constexpr int NJ = decltype(nj_c)::value;  // 32-token blocks that hold segment rows
+      constexpr bool ODD = decltype(odd_c)::value;
       constexpr int NM = 4 * NJ;                 // MFMAs per wave in this step
       constexpr int PF = NM < 4 ? NM : 4;        // fragment reads kept in flight
-      barrier_nofence();
-      const uint16_t* bsrc = wb + (int64_t)kt * kBlockElems;  // past the end: a re-read
-      if (kt + 1 < nk) {
-        bsrc = wb + (int64_t)(kt + 1) * kBlockElems;
-      } else if (ti + 1 < n_my) {
-        Tile nx;
-        locate(ti + 1, nx);
-        wb_next = w_base(nx);
-        bsrc = wb_next;
-      }
-      load_b(bsrc, bn);
-      asm volatile("" ::: "memory");
-      produce();
-      asm volatile("" ::: "memory");
+      if (!ODD) barrier_nofence();
+      // The first PF token fragments go out first, so their latency overlaps the issue of this
+      // step's loads instead of idling the matrix core.
       const unsigned char* st = smem + (g % kSA) * kStage;
       // NM MFMAs (slice q = n / NJ, token block j = n % NJ), token fragments read PF ahead.
       auto frag = [&](int n) {
@@ -302,31 +308,43 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
       bf16x8 fr[PF];
 #pragma unroll
       for (int n = 0; n < PF; ++n) fr[n] = frag(n);
+      asm volatile("" ::: "memory");
+      const uint16_t* bsrc = wb + (int64_t)kt * kBlockElems;  // past the end: a re-read
+      if (kt + 1 < nk) bsrc = wb + (int64_t)(kt + 1) * kBlockElems;
+      else if (has_next) bsrc = wb_next;
+      load_b(bsrc, bn);
+      asm volatile("" ::: "memory");
+      if (!ODD) {
+        produce();
+        asm volatile("" ::: "memory");
+        produce();
+        asm volatile("" ::: "memory");
+      }
 #pragma unroll
       for (int n = 0; n < NM; ++n) {
         acc[n % NJ] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
             __builtin_bit_cast(bf16x8, bc[n / NJ]), fr[n % PF], acc[n % NJ], 0, 0, 0);
         if (n + PF < NM) fr[n % PF] = frag(n + PF);
       }
-      // Keep PF fragment reads in flight: PF reads, then (1 MFMA, 1 read) pairs, then PF
-      // MFMAs. Without this the scheduler pulls each read next to its MFMA and waits on it.
-      __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
+      // Keep PF fragment reads in flight: (1 MFMA, 1 read) pairs, then the last PF MFMAs.
+      // Without this the scheduler pulls each read next to its MFMA and waits on it.
 #pragma unroll
       for (int n = 0; n < NM - PF; ++n) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
       __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
+      // Even step: the two stages and index loads issued after B(g + 1) may stay in flight.
       asm volatile("s_waitcnt vmcnt(%4)"
                    : "+v"(bn[0]), "+v"(bn[1]), "+v"(bn[2]), "+v"(bn[3])
-                   : "n"(kAfterB)
+                   : "n"(ODD ? 0 : 2 * (kAQ + G))
                    : "memory");
       ++g;
     };
     auto k_loop = [&](auto nj_c) {
       for (int kt = 0; kt < nk; kt += 2) {
-        step(nj_c, kt, b0, b1);
-        step(nj_c, kt + 1, b1, b0);
+        step(nj_c, std::false_type(), kt, b0, b1);
+        step(nj_c, std::true_type(), kt + 1, b1, b0);
       }
     };
     // A partial tile (the last of a segment) multiplies only the 32-token blocks that hold
