@@ -178,7 +178,8 @@ int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
 /*
  * Packed-weight variant of the grouped GEMM. nt_moe_pack_expert_weights_bf16 rearranges
  * w [num_segments, rows, K] once (same bytes, fragment order: 32-row x 64-K blocks in which
- * each lane's 16-byte operand chunk is contiguous with its neighbours'); the packed GEMM then
+ * each lane's 16-byte operand chunk is contiguous with its neighbours', rows inside a block
+ * ordered so that each lane's accumulators are 8 consecutive output columns); the packed GEMM then
  * streams each wave's weights straight into registers and stages only the token rows in LDS.
  * `epilogue` must be the one the packed weights will be used with (for SWIGLU the gate and value
  * rows of the same output columns are packed together). No counterpart in the reference beyond
@@ -186,7 +187,8 @@ int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
  *   pack:  w bf16 [num_segments, rows, K] -> packed bf16 [num_segments, rows, K] (same size)
  *          rows % 32 == 0 (rows = 2 n_out for SWIGLU), K % 64 == 0
  *   gemm:  as nt_moe_grouped_gemm_bf16 with w = packed weights; K % 128 == 0 and K >= 256;
- *          n_out % 16 == 0 (SWIGLU) or % 32; total_rows * n_out * 2 < 2^31.
+ *          n_out % 16 == 0 (SWIGLU) or % 32; total_rows * n_out * 2 < 2^31; a, w_packed and
+ *          c 16-byte aligned.
  */
 int nt_moe_pack_expert_weights_bf16(const uint16_t* w, int64_t num_segments, int32_t rows,
                                     int32_t K, int32_t epilogue, uint16_t* packed,

@@ -319,8 +319,8 @@ int nt_moe_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int64_t a_r
   NT_REQUIRE(src_row || a_rows >= total_rows,
              "grouped_gemm_packed: a needs total_rows rows without src_row");
   NT_REQUIRE(a && seg_offsets && w_packed && c, "grouped_gemm_packed: null buffer");
-  NT_REQUIRE(aligned16(a) && aligned16(w_packed) && aligned_to(c, 8),
-             "grouped_gemm_packed: a and w_packed must be 16-byte aligned, c 8-byte aligned");
+  NT_REQUIRE(aligned16(a) && aligned16(w_packed) && aligned16(c),
+             "grouped_gemm_packed: a, w_packed and c must be 16-byte aligned");
   int rc = check_gemm_extent(a_rows, ld_a, 0, 0);
   if (rc) return rc;
   if (total_rows == 0) return ok();

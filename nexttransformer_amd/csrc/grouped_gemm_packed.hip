@@ -58,11 +58,19 @@ constexpr int kStage = kBM * kRB;  // 32 KB
 constexpr int kBlockElems = 32 * kBK;  // packed weight block (32 rows x 64 K) = 2048 bf16
 constexpr int kMinK = 4 * kBK;     // the gather table needs four K steps of lead
 
+// Row order inside a packed 32-row block. A 32 x 32 accumulator holds, in element i of lane
+// half h, block position 8 (i / 4) + 4 h + i % 4; the pack kernel puts logical row
+// 8 (2 (i / 8) + h) + i % 8 there, so elements 0-7 and 8-15 of a lane are each 8 consecutive
+// logical rows (one 16-byte store of bf16 outputs). Position p holds logical row
+// block_row(p): the middle two 4-row groups of each 16-row half are swapped.
+__host__ __device__ constexpr int block_row(int p) { return p ^ (((p >> 2) ^ (p >> 3)) & 1) * 12; }
+static_assert(block_row(4) == 8 && block_row(8) == 4 && block_row(20) == 24 && block_row(3) == 3,
+              "middle groups swapped");
+
 template <int EPI>
 struct Ep {
-  static constexpr int kGroups = EPI == NT_MOE_EPI_SWIGLU ? 2 : 4;  // 4-column stores per tile
-  static constexpr int kStores = 8 * kGroups;                       // per wave per tile
-};
+  static constexpr int kStores = EPI == NT_MOE_EPI_SWIGLU ? 1 : 2;  // 16-byte stores per lane
+};                                                                   // per 32-token block
 
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row / kWIN) % kCH); }
 
@@ -355,7 +363,10 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
     else k_loop(std::integral_constant<int, 1>());
 
     // Epilogue: a fixed store count per wave; rows past the segment or columns past n_out get
-    // an out-of-range offset and are dropped by the buffer range check.
+    // an out-of-range offset and are dropped by the buffer range check. Lane (token j, half h)
+    // holds logical block rows 8 h + [0, 8) in elements 0-7 and 16 + 8 h + [0, 8) in 8-15:
+    // for SwiGLU gate and value of output columns 16 nb + 8 h + [0, 8), otherwise columns
+    // 32 nb + 8 h + [0, 8) and 32 nb + 16 + 8 h + [0, 8).
     const int nb = ct.nt * kWaves + wave;
     const int hbit = lane >> 5;
 #pragma unroll
@@ -363,29 +374,30 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
       const int m = ct.m0 + j * 32 + (lane & 31);
       const bool row_ok = m < ct.seg_end;
 #pragma unroll
-      for (int g4 = 0; g4 < Ep<EPI>::kGroups; ++g4) {
+      for (int st = 0; st < Ep<EPI>::kStores; ++st) {
         int col;
-        float v[4];
+        float v[8];
         if (EPI == NT_MOE_EPI_SWIGLU) {
-          col = nb * 16 + 8 * g4 + 4 * hbit;
+          col = nb * 16 + 8 * hbit;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float a = acc[j][4 * g4 + r], u = acc[j][4 * (g4 + 2) + r];
+          for (int r = 0; r < 8; ++r) {
+            const float a = acc[j][r], u = acc[j][8 + r];
             v[r] = a * u * __builtin_amdgcn_rcpf(1.f + __expf(-a));
           }
         } else {
-          col = nb * 32 + 8 * g4 + 4 * hbit;
+          col = nb * 32 + 16 * st + 8 * hbit;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float a = acc[j][4 * g4 + r];
+          for (int r = 0; r < 8; ++r) {
+            const float a = acc[j][8 * st + r];
             v[r] = EPI == NT_MOE_EPI_RELU2 ? (a > 0.f ? a * a : 0.f) : a;
           }
         }
-        const uint32_t lo = pack_bf16x2(v[0], v[1]), hi = pack_bf16x2(v[2], v[3]);
+        const u32x4 packed = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                              pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
         const uint32_t voff = (row_ok && nb < NB && col < n_out)
                                   ? (uint32_t)(((int64_t)m * n_out + col) * 2)
                                   : 0x80000000u;
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{lo, hi}, out_rsrc, voff, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(packed, out_rsrc, voff, 0, 0);
       }
     }
     wb = wb_next;
@@ -394,9 +406,9 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
 }
 
 // Packs w [S, R, K] (bf16) into 32-row x 64-K blocks of fragment order: block (s, nb, kb) holds,
-// at 16-byte chunk q * 64 + l, row i = l % 32 of the block and K elements
-// kb * 64 + 32 (l / 32) + 8 q .. + 8. Row i of block nb is w row 32 nb + i, or for SwiGLU
-// (R = 2 n_out) gate row 16 nb + i (i < 16) and value row n_out + 16 nb + i - 16.
+// at 16-byte chunk q * 64 + l, logical row i = block_row(l % 32) of the block and K elements
+// kb * 64 + 32 (l / 32) + 8 q .. + 8. Logical row i of block nb is w row 32 nb + i, or for
+// SwiGLU (R = 2 n_out) gate row 16 nb + i (i < 16) and value row n_out + 16 nb + i - 16.
 __global__ __launch_bounds__(256) void pack_weights_kernel(const uint16_t* __restrict__ w,
                                                             int64_t chunks, int R, int K,
                                                             int n_out, int swiglu,
@@ -409,7 +421,7 @@ __global__ __launch_bounds__(256) void pack_weights_kernel(const uint16_t* __res
   const int64_t rest = c / (256 * (int64_t)KB);
   const int nb = (int)(rest % NB);
   const int64_t s = rest / NB;
-  const int i = l % 32;
+  const int i = block_row(l % 32);
   const int row = swiglu ? (i < 16 ? 16 * nb + i : n_out + 16 * nb + (i - 16)) : 32 * nb + i;
   const int k0 = kb * kBK + 32 * (l / 32) + 8 * q;
   *reinterpret_cast<u32x4*>(out + c * 8) =

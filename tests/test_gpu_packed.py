@@ -23,7 +23,11 @@ def _pack_reference(w, epilogue):
     wn = w.view(torch.int16).numpy()
     out = np.empty((S, NB, KB, 4, 64, 8), dtype=np.int16)
     lanes = np.arange(64)
-    i = lanes % 32
+    pos = lanes % 32
+    # block position p holds logical row p with its middle 4-row groups swapped per 16-row half
+    # (positions 4-7 <-> 8-11, 20-23 <-> 24-27), so that accumulator element i of lane half h is
+    # logical row 8 (2 (i // 8) + h) + i % 8
+    i = np.array([[0, 2, 1, 3][(p % 16) // 4] * 4 + p % 4 + 16 * (p // 16) for p in pos])
     for nb in range(NB):
         rows = np.where(i < 16, 16 * nb + i, n_out + 16 * nb + i - 16) if epilogue == 0 else 32 * nb + i
         for kb in range(KB):
