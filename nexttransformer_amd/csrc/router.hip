@@ -246,7 +246,9 @@ __global__ __launch_bounds__(256) void router_fused_kernel(
                         z_partial);
 }
 
-// Split: one chunk of one expert group for 64 tokens -> partials[chunk][t][e].
+// Split: one chunk of one expert group for 64 tokens -> partials[chunk][e][t]. Expert-major
+// planes make every store of a wave 64 consecutive floats (token-major rows of E floats would
+// scatter each store over 64 rows, which cost more than the FMAs).
 template <int EPW>
 __global__ __launch_bounds__(256) void router_partial_kernel(
     const uint16_t* __restrict__ x, int64_t ld_x, const float* __restrict__ wt, int64_t T, int d,
@@ -266,23 +268,23 @@ __global__ __launch_bounds__(256) void router_partial_kernel(
   chunk_fma<EPW>(xs + lane * kXStride, wt, E, ws, c0, clen, acc);
   const int64_t t = t0 + lane;
   if (t < T) {
-    float* out = partials + ((int64_t)blockIdx.y * T + t) * E;
+    float* out = partials + (int64_t)blockIdx.y * E * T + t;
 #pragma unroll
     for (int i = 0; i < EPW; ++i) {
       int e = ws + i;
-      if (e >= e0 && e < E) out[e] = acc[i];
+      if (e >= e0 && e < E) out[(int64_t)e * T] = acc[i];
     }
   }
 }
 
-// Sums the nchunk partial planes of the split router into plane 0, in place, in the fixed order
-// ((p0 + p1) + p2) + ... then + bias[e]: four consecutive (t, e) values per thread, the planes'
-// loads issued together. This keeps the plane reduction off the top-k kernel, whose grid has one
-// block per 64 tokens and so cannot hide the loads' latency when T is small.
+// Sums the nchunk partial planes ([e][t]) of the split router into plane 0, in place, in the
+// fixed order ((p0 + p1) + p2) + ... then + bias[e]: four consecutive values per thread, the
+// planes' loads issued together. This keeps the plane reduction off the top-k kernel, whose grid
+// has one block per 64 tokens and so cannot hide the loads' latency when T is small.
 __global__ __launch_bounds__(256) void router_sum_planes_kernel(float* __restrict__ partials,
                                                                  int nchunk,
                                                                  const float* __restrict__ bias,
-                                                                 int64_t n4, int E) {
+                                                                 int64_t n4, int64_t T) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n4) return;
   const int64_t plane4 = n4;  // plane size in float4 units
@@ -303,20 +305,21 @@ __global__ __launch_bounds__(256) void router_sum_planes_kernel(float* __restric
       }
   }
   if (bias) {
-    const int e0 = (int)((i * 4) % E);  // E % 4 == 0: the four values share a row
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = v[j] + bias[e0 + j];
+    for (int j = 0; j < 4; ++j) v[j] = v[j] + bias[(i * 4 + j) / T];
   }
   p[0] = v;
 }
 
-// Sum nchunk partial planes in ascending order (+ bias), then top-k. With nchunk = 1 and no
-// bias this is top-k on caller-supplied logits.
+// Sum nchunk partial planes in ascending order (+ bias), then top-k. Element (t, e) of a plane
+// sits at t + e T (expert-major, the split router's planes) or t E + e (token-major: caller-
+// supplied logits, with nchunk = 1 and no bias); the tile loads walk the contiguous index.
 template <int KMAX>
 __global__ __launch_bounds__(1024) void router_topk_kernel(
-    const float* __restrict__ partials, int nchunk, const float* __restrict__ bias, int64_t T,
-    int E, int k, int score_fn, float* __restrict__ logits, int32_t* __restrict__ topk_ids,
-    float* __restrict__ topk_w, float* __restrict__ prob_partial, float* __restrict__ z_partial) {
+    const float* __restrict__ partials, int nchunk, bool expert_major,
+    const float* __restrict__ bias, int64_t T, int E, int k, int score_fn,
+    float* __restrict__ logits, int32_t* __restrict__ topk_ids, float* __restrict__ topk_w,
+    float* __restrict__ prob_partial, float* __restrict__ z_partial) {
   extern __shared__ __align__(16) unsigned char smem[];
   float* lg = reinterpret_cast<float*>(smem);
   float* zt = reinterpret_cast<float*>(smem + zt_offset(E));
@@ -324,6 +327,12 @@ __global__ __launch_bounds__(1024) void router_topk_kernel(
   // Chunk planes are summed in ascending order; loads go out 8 planes at a time so the sum is
   // not a chain of dependent memory round trips.
   const int64_t plane = T * E;
+  // Tile index idx -> (token row r, expert e), contiguous in memory along idx.
+  auto split_idx = [&](int idx, int& r, int& e) {
+    if (expert_major) { e = idx / kRouteBlock; r = idx - e * kRouteBlock; }
+    else { r = idx / E; e = idx - r * E; }
+  };
+  auto at = [&](int64_t t, int e) { return expert_major ? t + e * T : t * E + e; };
   if (nchunk == 1) {
     // One plane (the split router's planes are summed by router_sum_planes_kernel): eight loads
     // per thread go out together, so a block does not wait on one round trip per element.
@@ -332,15 +341,17 @@ __global__ __launch_bounds__(1024) void router_topk_kernel(
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int idx = base + j * blockDim.x;
-        const int r = idx / E, e = idx - r * E;
+        int r, e;
+        split_idx(idx, r, e);
         const int64_t t = t0 + r;
-        v[j] = (idx < kRouteBlock * E && t < T) ? partials[t * E + e] : 0.f;
+        v[j] = (idx < kRouteBlock * E && t < T) ? partials[at(t, e)] : 0.f;
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int idx = base + j * blockDim.x;
         if (idx >= kRouteBlock * E) break;
-        const int r = idx / E, e = idx - r * E;
+        int r, e;
+        split_idx(idx, r, e);
         const int64_t t = t0 + r;
         float val = v[j];
         if (t < T) {
@@ -353,11 +364,12 @@ __global__ __launch_bounds__(1024) void router_topk_kernel(
   }
   for (int idx = nchunk == 1 ? kRouteBlock * E : threadIdx.x; idx < kRouteBlock * E;
        idx += blockDim.x) {
-    int r = idx / E, e = idx - r * E;
+    int r, e;
+    split_idx(idx, r, e);
     int64_t t = t0 + r;
     float v = 0.f;
     if (t < T) {
-      const float* p = partials + t * E + e;
+      const float* p = partials + at(t, e);
       v = p[0];
       for (int c0 = 1; c0 < nchunk; c0 += 8) {
         float part[8];
@@ -398,25 +410,27 @@ int router_mode_override() {
 }
 
 template <int KMAX>
-hipError_t launch_topk_k(const float* partials, int nchunk, const float* bias, int64_t T, int E,
-                         int k, int score_fn, float* logits, int32_t* ids, float* w, float* pp,
-                         float* zp, hipStream_t stream) {
+hipError_t launch_topk_k(const float* partials, int nchunk, bool expert_major, const float* bias,
+                         int64_t T, int E, int k, int score_fn, float* logits, int32_t* ids,
+                         float* w, float* pp, float* zp, hipStream_t stream) {
   dim3 grid(ceil_div(T, kRouteBlock));
   hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(router_topk_kernel<KMAX>),
                                      router_lds_bytes(E));
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL((router_topk_kernel<KMAX>), grid, dim3(1024), router_lds_bytes(E), stream,
-                     partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp);
+                     partials, nchunk, expert_major, bias, T, E, k, score_fn, logits, ids, w, pp,
+                     zp);
   return hipGetLastError();
 }
 
-hipError_t launch_topk_any(const float* partials, int nchunk, const float* bias, int64_t T,
-                           int E, int k, int score_fn, float* logits, int32_t* ids, float* w,
-                           float* pp, float* zp, hipStream_t stream) {
+hipError_t launch_topk_any(const float* partials, int nchunk, bool expert_major,
+                           const float* bias, int64_t T, int E, int k, int score_fn,
+                           float* logits, int32_t* ids, float* w, float* pp, float* zp,
+                           hipStream_t stream) {
   switch (kmax_for(k)) {
-    case 2: return launch_topk_k<2>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
-    case 4: return launch_topk_k<4>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
-    default: return launch_topk_k<8>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    case 2: return launch_topk_k<2>(partials, nchunk, expert_major, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    case 4: return launch_topk_k<4>(partials, nchunk, expert_major, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    default: return launch_topk_k<8>(partials, nchunk, expert_major, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
   }
 }
 
@@ -496,21 +510,21 @@ hipError_t launch_router(const uint16_t* x, int64_t ld_x, const float* wt, const
   if (E % 4 == 0) {
     const int64_t n4 = T * E / 4;
     router_sum_planes_kernel<<<dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream>>>(
-        partials, nchunk, bias, n4, E);
+        partials, nchunk, bias, n4, T);
     err = hipGetLastError();
     if (err != hipSuccess) return err;
-    return launch_topk_any(partials, 1, nullptr, T, E, k, score_fn, logits, topk_ids, topk_w,
-                           prob_partial, z_partial, stream);
+    return launch_topk_any(partials, 1, true, nullptr, T, E, k, score_fn, logits, topk_ids,
+                           topk_w, prob_partial, z_partial, stream);
   }
-  return launch_topk_any(partials, nchunk, bias, T, E, k, score_fn, logits, topk_ids, topk_w,
-                         prob_partial, z_partial, stream);
+  return launch_topk_any(partials, nchunk, true, bias, T, E, k, score_fn, logits, topk_ids,
+                         topk_w, prob_partial, z_partial, stream);
 }
 
 hipError_t launch_topk_from_logits(const float* logits, int64_t T, int E, int k,
                                    int score_fn, int32_t* topk_ids, float* topk_w,
                                    float* prob_partial, float* z_partial, hipStream_t stream) {
-  return launch_topk_any(logits, 1, nullptr, T, E, k, score_fn, nullptr, topk_ids, topk_w,
-                         prob_partial, z_partial, stream);
+  return launch_topk_any(logits, 1, false, nullptr, T, E, k, score_fn, nullptr, topk_ids,
+                         topk_w, prob_partial, z_partial, stream);
 }
 
 }  // namespace ntmoe
