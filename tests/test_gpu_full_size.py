@@ -18,28 +18,37 @@ pytestmark = pytest.mark.gpu
 BF16_TOL = 1e-2
 
 
-def _run(case):
+def _run(case, packed):
+    from nexttransformer_amd import _native as nat
     from nexttransformer_amd import ops
     cpu = make_inputs(case)
     dev = torch.device("cuda")
-    bf = lambda t: None if t is None else t.to(torch.bfloat16).to(dev)
-    g = dict(x=cpu["x"].to(dev), wt=cpu["router"].t().contiguous().to(dev), w1=bf(cpu["w1"]),
-             w2=bf(cpu["w2"]), sw1=bf(cpu["shared_w1"]), sw2=bf(cpu["shared_w2"]),
+    up = nat.EPI_SWIGLU if case.activation == 0 else nat.EPI_RELU2
+
+    def bf(t, epi):
+        if t is None:
+            return None
+        t = t.to(torch.bfloat16).to(dev)
+        return ops.pack_expert_weights(t, epi) if packed else t
+    g = dict(x=cpu["x"].to(dev), wt=cpu["router"].t().contiguous().to(dev),
+             w1=bf(cpu["w1"], up), w2=bf(cpu["w2"], nat.EPI_NONE),
+             sw1=bf(cpu["shared_w1"], up), sw2=bf(cpu["shared_w2"], nat.EPI_NONE),
              bias=None if cpu["bias"] is None else cpu["bias"].to(dev))
 
     def fwd():
         return ops.moe_forward(g["x"], g["wt"], g["w1"], g["w2"], top_k=case.k,
                                score_fn=case.score_fn, activation=case.activation,
                                logit_bias=g["bias"], shared_w1=g["sw1"], shared_w2=g["sw2"],
-                               want_logits=True)
+                               want_logits=True, packed=packed)
     return cpu, fwd
 
 
+@pytest.mark.parametrize("packed", [False, True], ids=["plain", "packed"])
 @pytest.mark.parametrize("cfg", [2, 3, 4])
-def test_full_size_layer(cfg):
+def test_full_size_layer(cfg, packed):
     case = CONFIGS[cfg]
-    print(f"[full-size] config {cfg}: {case}", flush=True)
-    cpu, fwd = _run(case)
+    print(f"[full-size] config {cfg} packed={packed}: {case}", flush=True)
+    cpu, fwd = _run(case, packed)
     out, aux, st = fwd()
     torch.cuda.synchronize()
     T, E, k = case.T, case.E, case.k

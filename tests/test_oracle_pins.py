@@ -327,6 +327,33 @@ def test_e4m3_rowwise_and_blockwise_quantisation():
     assert ((back - w).abs() <= w.abs() * 2.0 ** -4 + sb.amax() * 2.0 ** -9).all()
 
 
+def test_fp8_layer_reduces_to_the_fp32_layer_on_dequantised_weights():
+    """moe_forward_fp8 against moe_forward: with token rows that are e4m3 values whose row
+    maximum is 448 (row scale 1, so quantising them is exact) and the dequantised 128 x 128-block
+    weights as the fp32 layer's weights, the two differ only by the per-row e4m3 re-quantisation
+    of h (relative error <= 2^-4 per element). Routing and aux are the same bits; a transposed or
+    mis-scaled weight, a dropped term or a wrong expert order would miss the bound."""
+    g = torch.Generator().manual_seed(21)
+    T, d, E, k, H = 48, 256, 4, 2, 128
+    codes = torch.randint(0, 256, (T, d), generator=g).to(torch.uint8)
+    codes[(codes & 0x7F) >= 0x7E] = 0x38  # no NaN, nothing above 448 but the planted maximum
+    x = orc.e4m3_decode(codes)
+    x[:, 7] = 448.0
+    x = x.to(torch.bfloat16)  # e4m3 values are exact in bf16
+    router = torch.randn(E, d, generator=g) * 0.02
+    w1q, w1s = orc.quantize_blockwise(torch.randn(E, 2 * H, d, generator=g) * 0.02)
+    w2q, w2s = orc.quantize_blockwise(torch.randn(E, d, H, generator=g) * 0.02)
+    fp8 = orc.moe_forward_fp8(x, router, w1q, w1s, w2q, w2s, k)
+    xq, xs = orc.quantize_rowwise(x.float())
+    assert (xs == 1).all() and torch.equal(orc.e4m3_decode(xq), x.float())
+    ref = orc.moe_forward(x, orc.Weights(router=router, w1=orc.dequantize_blockwise(w1q, w1s),
+                                         w2=orc.dequantize_blockwise(w2q, w2s)), k)
+    assert torch.equal(fp8["ids"], ref["ids"]) and torch.equal(fp8["counts"], ref["counts"])
+    assert fp8["aux"] == ref["aux"]
+    err = ((fp8["out"] - ref["out"]).norm() / ref["out"].norm()).item()
+    assert 1e-4 < err < 4e-2  # the h re-quantisation is visible, and bounded
+
+
 # ---------------------------------------------------------------------------------------------
 # committed golden vectors (written by tests/golden/make_golden.py) still reproduce
 
