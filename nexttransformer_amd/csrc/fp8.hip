@@ -26,6 +26,7 @@
 // (A rows 0-15 gate, 16-31 value), so both land in the same lane of the accumulator layout
 // (row i of a 32 x 32 fragment sits in lane (i / 4) % 2 * 32 + column, element (i / 8) * 4 + i % 4).
 #include <math.h>
+#include <stdlib.h>
 
 #include "common.h"
 
@@ -128,7 +129,9 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * u * __builtin_amdgcn_rcpf(1.f + __expf(-g));
 }
 
-template <int EPI, bool PACKED>
+// D: K blocks of weights in flight per wave beyond the one being multiplied (a register ring of
+// D + 1 blocks). The kernel streams weights, so bytes in flight per CU set its bandwidth.
+template <int EPI, bool PACKED, int D>
 __global__ __launch_bounds__(256) void fp8_grouped_gemm_kernel(
     const uint8_t* __restrict__ a, int64_t ld_a, int64_t a_rows, const float* __restrict__ a_scale,
     const int32_t* __restrict__ src_row, const int32_t* __restrict__ seg_offsets,
@@ -168,20 +171,23 @@ __global__ __launch_bounds__(256) void fp8_grouped_gemm_kernel(
     wp = w + ((int64_t)seg * w_rows + (wvalid ? wrow : col0)) * K + half * 32;
     w_step = kScaleBlock;
   }
-  auto load_w = [&](int64_t kb, i32x8& s0, i32x8& s1) {
-    if (PACKED) {
-      const uint8_t* b = wp + kb * w_step;
-      const u32x4 c0 = *reinterpret_cast<const u32x4*>(b);
-      const u32x4 c1 = *reinterpret_cast<const u32x4*>(b + 1024);
-      const u32x4 c2 = *reinterpret_cast<const u32x4*>(b + 2048);
-      const u32x4 c3 = *reinterpret_cast<const u32x4*>(b + 3072);
-      s0 = i32x8{(int)c0[0], (int)c0[1], (int)c0[2], (int)c0[3],
-                 (int)c1[0], (int)c1[1], (int)c1[2], (int)c1[3]};
-      s1 = i32x8{(int)c2[0], (int)c2[1], (int)c2[2], (int)c2[3],
-                 (int)c3[0], (int)c3[1], (int)c3[2], (int)c3[3]};
+  // One K block = four 16-byte loads of weights and four of activations per lane, issued from
+  // inline assembly: the compiler neither counts them nor adds its own (conservative, loop-
+  // merged) waits; the explicit wait before a block is used names that block's registers, so
+  // no use of them, and no copy, can be scheduled above it. Weights: packed, bytes
+  // {0, 1024, 2048, 3072} of the block's 4 KB run; plain, bytes {0, 16, 64, 80} of the lane's
+  // row at K offset 128 kb. Activations: bytes {0, 16, 64, 80} of the token row at 128 kb.
+  auto load4 = [&](const uint8_t* p, bool wide, u32x4 (&r)[4]) {
+    if (wide) {
+      asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r[0]) : "v"(p) : "memory");
+      asm volatile("global_load_dwordx4 %0, %1, off offset:1024" : "=v"(r[1]) : "v"(p) : "memory");
+      asm volatile("global_load_dwordx4 %0, %1, off offset:2048" : "=v"(r[2]) : "v"(p) : "memory");
+      asm volatile("global_load_dwordx4 %0, %1, off offset:3072" : "=v"(r[3]) : "v"(p) : "memory");
     } else {
-      s0 = *reinterpret_cast<const i32x8*>(wp + kb * w_step);
-      s1 = *reinterpret_cast<const i32x8*>(wp + kb * w_step + 64);
+      asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r[0]) : "v"(p) : "memory");
+      asm volatile("global_load_dwordx4 %0, %1, off offset:16" : "=v"(r[1]) : "v"(p) : "memory");
+      asm volatile("global_load_dwordx4 %0, %1, off offset:64" : "=v"(r[2]) : "v"(p) : "memory");
+      asm volatile("global_load_dwordx4 %0, %1, off offset:80" : "=v"(r[3]) : "v"(p) : "memory");
     }
   };
   // scale rows of the gate (or only) half and of the value half
@@ -199,33 +205,50 @@ __global__ __launch_bounds__(256) void fp8_grouped_gemm_kernel(
     arow = arow < 0 ? 0 : (arow >= a_rows ? a_rows - 1 : arow);
     const uint8_t* ap = a + arow * ld_a + half * 32;
 
-    const i32x8 zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
-    i32x8 wa0, wa1;
-    load_w(0, wa0, wa1);
-    i32x8 xb0 = tvalid ? *reinterpret_cast<const i32x8*>(ap) : zero8;
-    i32x8 xb1 = tvalid ? *reinterpret_cast<const i32x8*>(ap + 64) : zero8;
-    floatx16 acc = {};
-    for (int kb = 0; kb < kblocks; ++kb) {
-      i32x8 nwa0 = wa0, nwa1 = wa1, nxb0 = xb0, nxb1 = xb1;
-      if (kb + 1 < kblocks) {
-        const int64_t off = (int64_t)(kb + 1) * kScaleBlock;
-        load_w(kb + 1, nwa0, nwa1);
-        nxb0 = tvalid ? *reinterpret_cast<const i32x8*>(ap + off) : zero8;
-        nxb1 = tvalid ? *reinterpret_cast<const i32x8*>(ap + off + 64) : zero8;
-      }
-      floatx16 part = {};
-      part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wa0, xb0, part, 0, 0, 0, kScaleOne, 0,
-                                                             kScaleOne);
-      part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wa1, xb1, part, 0, 0, 0, kScaleOne, 0,
-                                                             kScaleOne);
-      const float s_lo = ws_lo[kb], s_hi = ws_hi[kb];
+    // Ring of D + 1 K blocks: slot kb % (D + 1) holds block kb's weights (wq) and activations
+    // (xq). Every step issues one block (past the last one it re-reads the last; a token past
+    // the segment reads a valid row whose results are not stored), so the number of loads
+    // issued after block kb is always 8 D when block kb is needed.
+    u32x4 wq[D + 1][4], xq[D + 1][4];
+    auto issue = [&](int kb, int slot_unused, u32x4 (&w4)[4], u32x4 (&x4)[4]) {
+      (void)slot_unused;
+      const int kc = kb < kblocks ? kb : kblocks - 1;
+      load4(wp + (int64_t)kc * w_step, PACKED, w4);
+      load4(ap + (int64_t)kc * kScaleBlock, false, x4);
+    };
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[i] = fmaf(part[i], i < 8 ? s_lo : s_hi, acc[i]);
-      wa0 = nwa0;
-      wa1 = nwa1;
-      xb0 = nxb0;
-      xb1 = nxb1;
+    for (int j = 0; j < D; ++j) issue(j, j, wq[j], xq[j]);
+    floatx16 acc = {};
+    for (int kb0 = 0; kb0 < kblocks; kb0 += D + 1) {
+#pragma unroll
+      for (int u = 0; u <= D; ++u) {
+        const int kb = kb0 + u;
+        issue(kb + D, (u + D) % (D + 1), wq[(u + D) % (D + 1)], xq[(u + D) % (D + 1)]);
+        asm volatile("s_waitcnt vmcnt(%8)"
+                     : "+v"(wq[u][0]), "+v"(wq[u][1]), "+v"(wq[u][2]), "+v"(wq[u][3]),
+                       "+v"(xq[u][0]), "+v"(xq[u][1]), "+v"(xq[u][2]), "+v"(xq[u][3])
+                     : "n"(8 * D)
+                     : "memory");
+        if (kb >= kblocks) continue;  // the ring's trailing re-reads (uniform)
+        const i32x8 w0 = {(int)wq[u][0][0], (int)wq[u][0][1], (int)wq[u][0][2], (int)wq[u][0][3],
+                          (int)wq[u][1][0], (int)wq[u][1][1], (int)wq[u][1][2], (int)wq[u][1][3]};
+        const i32x8 w1 = {(int)wq[u][2][0], (int)wq[u][2][1], (int)wq[u][2][2], (int)wq[u][2][3],
+                          (int)wq[u][3][0], (int)wq[u][3][1], (int)wq[u][3][2], (int)wq[u][3][3]};
+        const i32x8 x0 = {(int)xq[u][0][0], (int)xq[u][0][1], (int)xq[u][0][2], (int)xq[u][0][3],
+                          (int)xq[u][1][0], (int)xq[u][1][1], (int)xq[u][1][2], (int)xq[u][1][3]};
+        const i32x8 x1 = {(int)xq[u][2][0], (int)xq[u][2][1], (int)xq[u][2][2], (int)xq[u][2][3],
+                          (int)xq[u][3][0], (int)xq[u][3][1], (int)xq[u][3][2], (int)xq[u][3][3]};
+        floatx16 part = {};
+        part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w0, x0, part, 0, 0, 0, kScaleOne,
+                                                               0, kScaleOne);
+        part = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w1, x1, part, 0, 0, 0, kScaleOne,
+                                                               0, kScaleOne);
+        const float s_lo = ws_lo[kb], s_hi = ws_hi[kb];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = fmaf(part[i], i < 8 ? s_lo : s_hi, acc[i]);
+      }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring's last re-reads
     if (!tvalid) continue;
     const float as = a_scale[arow];
     uint16_t* crow = c + tok * n_out;
@@ -281,6 +304,42 @@ hipError_t launch_quantize_fp8_blockwise(const float* w, int64_t S, int R, int C
   return hipGetLastError();
 }
 
+// Weight blocks in flight per wave (NT_MOE_FP8_DEPTH overrides, for tuning runs).
+int fp8_weight_depth() {
+  static int n = [] {
+    const char* s = getenv("NT_MOE_FP8_DEPTH");
+    int v = s ? atoi(s) : 0;
+    return v >= 1 && v <= 3 ? v : 2;
+  }();
+  return n;
+}
+
+template <int EPI, bool P>
+hipError_t launch_fp8(dim3 grid, hipStream_t stream, const uint8_t* a, int64_t ld_a,
+                      int64_t a_rows, const float* a_scale, const int32_t* src_row,
+                      const int32_t* seg_offsets, int64_t total_rows, const uint8_t* w,
+                      const float* w_scale, int K, int n_out, int n_tiles, uint16_t* c) {
+  const dim3 block(256);
+  switch (fp8_weight_depth()) {
+    case 1:
+      fp8_grouped_gemm_kernel<EPI, P, 1><<<grid, block, 0, stream>>>(
+          a, ld_a, a_rows, a_scale, src_row, seg_offsets, total_rows, w, w_scale, K, n_out,
+          n_tiles, c);
+      break;
+    case 2:
+      fp8_grouped_gemm_kernel<EPI, P, 2><<<grid, block, 0, stream>>>(
+          a, ld_a, a_rows, a_scale, src_row, seg_offsets, total_rows, w, w_scale, K, n_out,
+          n_tiles, c);
+      break;
+    default:
+      fp8_grouped_gemm_kernel<EPI, P, 3><<<grid, block, 0, stream>>>(
+          a, ld_a, a_rows, a_scale, src_row, seg_offsets, total_rows, w, w_scale, K, n_out,
+          n_tiles, c);
+      break;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_grouped_gemm_fp8(const uint8_t* a, int64_t ld_a, int64_t a_rows,
                                    const float* a_scale, const int32_t* src_row,
                                    const int32_t* seg_offsets, int num_segments,
@@ -290,25 +349,22 @@ hipError_t launch_grouped_gemm_fp8(const uint8_t* a, int64_t ld_a, int64_t a_row
   const int per_block = epilogue == NT_MOE_EPI_SWIGLU ? Fp8Tile<NT_MOE_EPI_SWIGLU>::kColsPerBlock
                                                       : Fp8Tile<NT_MOE_EPI_NONE>::kColsPerBlock;
   const int n_tiles = ceil_div(n_out, per_block);
-  const dim3 grid((unsigned)((int64_t)num_segments * n_tiles)), block(256);
+  const dim3 grid((unsigned)((int64_t)num_segments * n_tiles));
   if (total_rows == 0) return hipSuccess;
-#define NT_F8(EPI, P)                                                                            \
-  fp8_grouped_gemm_kernel<EPI, P><<<grid, block, 0, stream>>>(a, ld_a, a_rows, a_scale, src_row, \
-                                                              seg_offsets, total_rows, w,        \
-                                                              w_scale, K, n_out, n_tiles, c)
+#define NT_F8_ARGS grid, stream, a, ld_a, a_rows, a_scale, src_row, seg_offsets, total_rows, w, \
+                   w_scale, K, n_out, n_tiles, c
   switch (epilogue) {
     case NT_MOE_EPI_SWIGLU:
-      if (packed) NT_F8(NT_MOE_EPI_SWIGLU, true); else NT_F8(NT_MOE_EPI_SWIGLU, false);
-      break;
+      return packed ? launch_fp8<NT_MOE_EPI_SWIGLU, true>(NT_F8_ARGS)
+                    : launch_fp8<NT_MOE_EPI_SWIGLU, false>(NT_F8_ARGS);
     case NT_MOE_EPI_RELU2:
-      if (packed) NT_F8(NT_MOE_EPI_RELU2, true); else NT_F8(NT_MOE_EPI_RELU2, false);
-      break;
+      return packed ? launch_fp8<NT_MOE_EPI_RELU2, true>(NT_F8_ARGS)
+                    : launch_fp8<NT_MOE_EPI_RELU2, false>(NT_F8_ARGS);
     default:
-      if (packed) NT_F8(NT_MOE_EPI_NONE, true); else NT_F8(NT_MOE_EPI_NONE, false);
-      break;
+      return packed ? launch_fp8<NT_MOE_EPI_NONE, true>(NT_F8_ARGS)
+                    : launch_fp8<NT_MOE_EPI_NONE, false>(NT_F8_ARGS);
   }
-#undef NT_F8
-  return hipGetLastError();
+#undef NT_F8_ARGS
 }
 
 // Packs e4m3 weights w [S, R, K] for the packed fp8 GEMM: 32-row groups (for SwiGLU 16 gate
