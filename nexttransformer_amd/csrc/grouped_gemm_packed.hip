@@ -147,13 +147,21 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
   const int xcd = blockIdx.x % 8, local = blockIdx.x / 8, per_xcd = gridDim.x / 8;
   const int t_begin = (int)((int64_t)total * xcd / 8);
   const int t_end = (int)((int64_t)total * (xcd + 1) / 8);
-  const int first = t_begin + local;
-  if (first >= t_end) return;
-  const int n_my = (t_end - first + per_xcd - 1) / per_xcd;  // tiles of this workgroup
+  // Round-robin over the XCD's workgroups. When the last round would leave more than half of
+  // them idle, its tiles are split into two 128-row halves, so twice as many workgroups share
+  // it and the busiest does half a tile less (a half still streams the tile's weights, so it
+  // costs more than half a tile: worth it only when the workgroups would idle anyway).
+  const int n_x = t_end - t_begin;
+  const int full_rounds = n_x / per_xcd, rem = n_x - full_rounds * per_xcd;
+  const bool split_tail = rem > 0 && 2 * rem <= per_xcd;
+  const int n_my = full_rounds + (local < (split_tail ? 2 * rem : rem) ? 1 : 0);
+  if (n_my == 0) return;
   const int total_steps = n_my * nk;
 
-  auto locate = [&](int idx, Tile& t) {  // idx-th tile of this workgroup
-    const int tl = first + idx * per_xcd;
+  auto locate = [&](int idx, Tile& t) {  // idx-th tile (or half tile) of this workgroup
+    const bool half_tile = split_tail && idx == full_rounds;
+    const int tl = half_tile ? t_begin + full_rounds * per_xcd + (local >> 1)
+                             : t_begin + local + idx * per_xcd;
     int lo = 0, hi = S;
     while (hi - lo > 1) {
       int mid = (lo + hi) >> 1;
@@ -165,6 +173,11 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
     t.nt = lt - mt * n_tiles;
     t.seg_end = __builtin_amdgcn_readfirstlane(seg_lo[t.s + 1]);
     t.m0 = __builtin_amdgcn_readfirstlane(seg_lo[t.s]) + mt * kBM;
+    if (half_tile) {  // rows [m0, m0 + 128) or [m0 + 128, m0 + 256) of the tile
+      const int tile_end = t.seg_end < t.m0 + kBM ? t.seg_end : t.m0 + kBM;
+      if (local & 1) t.m0 += kBM / 2;
+      t.seg_end = (local & 1) ? tile_end : (tile_end < t.m0 + kBM / 2 ? tile_end : t.m0 + kBM / 2);
+    }
   };
   // Gather indices of tile t into table slot `slot`: waves 0-3 load 64 rows each, straight to
   // LDS; rows past the segment end repeat its last row (their results are dropped).

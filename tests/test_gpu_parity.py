@@ -25,6 +25,13 @@ SMALL = [
     Case("single-token", 1, 64, 4, 1, 64, seed=7),
 ]
 
+# Mid-size batches (256 64-token blocks on a 256-CU part): the split router's item order, plane
+# layout and top-k at the sizes the benchmark configurations use, with a ragged last block.
+MID = [
+    Case("quarter-T16411-d512-E24-k3-bias", 16411, 512, 24, 3, 64, zipf_bias=1.2, seed=8),
+    Case("quarter-T16400-d1024-E32-k4-sigmoid", 16400, 1024, 32, 4, 64, score_fn=1, seed=9),
+]
+
 
 def gpu_inputs(case):
     cpu = make_inputs(case)
@@ -48,7 +55,7 @@ def oracle_weights(cpu):
                        bias=cpu["bias"])
 
 
-@pytest.mark.parametrize("case", SMALL, ids=lambda c: c.name)
+@pytest.mark.parametrize("case", SMALL + MID, ids=lambda c: c.name)
 def test_router_logits_and_topk_bit_exact(case):
     from nexttransformer_amd import ops
     cpu, g = gpu_inputs(case)
