@@ -15,13 +15,14 @@
 // through scalar loads (w_router_t is [d, E], E contiguous); each lane keeps EPW fp32
 // accumulators. x is staged through LDS one 128-feature chunk at a time (coalesced global
 // loads, padded rows so per-lane row reads are conflict-free).
-// When T is small the fused grid cannot fill the chip: the split variant gives every
-// (token block, chunk, expert group) its own block, writes the chunk sums c_j to a
-// workspace, and the top-k kernel adds them in ascending j -- the same order.
+// Unless T is very large the fused grid has too few waves per CU: the split variant gives every
+// (token block, chunk, expert group) its own block and writes the chunk sums c_j to a
+// workspace (expert-major planes); a plane-sum kernel adds them in ascending j -- the same
+// order -- and a top-k kernel ranks.
 //
-// Top-k: logits go to an LDS tile [64][E+1]; 4 lanes share a token, each scans every 4th
-// expert into a sorted register list, then k rounds of an xor-shuffle butterfly over the 4
-// lanes emit the global order.
+// Top-k: logits go to an LDS tile [64][E+1]; LPT lanes share a token (4 in the fused kernel,
+// 16 in the top-k kernel), each scans every LPT-th expert into a sorted register list, then k
+// rounds of an xor-shuffle butterfly over the LPT lanes emit the global order.
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -176,18 +177,27 @@ __device__ void topk_and_scores(float* lg, float* zt, int64_t t0, int64_t T, int
   if (sub == 0) zt[tt] = lse * lse;
   __syncthreads();
 
-  // Per-block column sums in token order (deterministic).
+  // Per-block column sums in a fixed order (deterministic): P consecutive lanes per expert,
+  // lane p summing tokens p, p + P, ..., then a butterfly over the P lanes; P is the largest
+  // power of two <= 64 with E P <= the block's threads. The z sum likewise over one wave.
   const int nvalid = (int)((T - t0) < kRouteBlock ? (T - t0) : kRouteBlock);
   const int64_t blk = t0 / kRouteBlock;
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+  int P = 64;
+  while (P > 1 && E * P > (int)blockDim.x) P >>= 1;
+  for (int base = 0; base < E * P; base += blockDim.x) {
+    const int idx = base + threadIdx.x;
+    const int e = idx / P, p = idx % P;
     float s = 0.f;
-    for (int r = 0; r < nvalid; ++r) s += lg[r * ldl + e];
-    prob_partial[blk * E + e] = s;
+    if (e < E)
+      for (int r = p; r < nvalid; r += P) s += lg[r * ldl + e];
+    for (int m = P >> 1; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+    if (e < E && p == 0) prob_partial[blk * E + e] = s;
   }
-  if (threadIdx.x == 0) {
-    float s = 0.f;
-    for (int r = 0; r < nvalid; ++r) s += zt[r];
-    z_partial[blk] = s;
+  if (threadIdx.x < 64) {
+    float s = threadIdx.x < nvalid ? zt[threadIdx.x] : 0.f;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+    if (threadIdx.x == 0) z_partial[blk] = s;
   }
 }
 
@@ -469,13 +479,17 @@ hipError_t launch_partial_e(const uint16_t* x, int64_t ld_x, const float* wt, in
 
 }  // namespace
 
-// Chunks of the split variant when it is used for this shape, else 0 (fused).
+// Chunks of the split variant when it is used for this shape, else 0 (fused). The fused kernel
+// has one 4-wave block per 64 tokens, too few waves per CU to hide its scalar weight loads until
+// there are several blocks per CU (measured: at T = 32768, d = 2048, E = 64 the split variant is
+// 24 % faster); the split variant's partial planes are capped at 512 MB of workspace.
 int router_split_chunks(int64_t T, int d, int E) {
-  (void)E;
   int mode = router_mode_override();
   if (mode == 1) return 0;
-  int blocks = ceil_div(T, kRouteBlock);
-  if (mode == 2 || blocks < 2 * num_cus()) return ceil_div(d, kRouterChunk);
+  const int nchunk = ceil_div(d, kRouterChunk);
+  const int64_t blocks = ceil_div(T, kRouteBlock);
+  const int64_t plane_bytes = (int64_t)nchunk * T * E * (int64_t)sizeof(float);
+  if (mode == 2 || (blocks < 8LL * num_cus() && plane_bytes <= (512LL << 20))) return nchunk;
   return 0;
 }
 
