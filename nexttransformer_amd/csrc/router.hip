@@ -338,10 +338,10 @@ __global__ __launch_bounds__(1024) void router_topk_kernel(
   // not a chain of dependent memory round trips.
   const int64_t plane = T * E;
   // Tile index idx -> (token row r, expert e), contiguous in memory along idx.
-  auto split_idx = [&](int idx, int& r, int& e) {
-    if (expert_major) { e = idx / kRouteBlock; r = idx - e * kRouteBlock; }
-    else { r = idx / E; e = idx - r * E; }
-  };
+  // (Plain selects, not assignments through references: the latter made the compiler keep r
+  // and e in scratch memory with a dynamic index.)
+  auto row_of = [&](int idx) { return expert_major ? idx % kRouteBlock : idx / E; };
+  auto col_of = [&](int idx) { return expert_major ? idx / kRouteBlock : idx % E; };
   auto at = [&](int64_t t, int e) { return expert_major ? t + e * T : t * E + e; };
   if (nchunk == 1) {
     // One plane (the split router's planes are summed by router_sum_planes_kernel): eight loads
@@ -351,8 +351,7 @@ __global__ __launch_bounds__(1024) void router_topk_kernel(
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int idx = base + j * blockDim.x;
-        int r, e;
-        split_idx(idx, r, e);
+        const int r = row_of(idx), e = col_of(idx);
         const int64_t t = t0 + r;
         v[j] = (idx < kRouteBlock * E && t < T) ? partials[at(t, e)] : 0.f;
       }
@@ -360,8 +359,7 @@ __global__ __launch_bounds__(1024) void router_topk_kernel(
       for (int j = 0; j < 8; ++j) {
         const int idx = base + j * blockDim.x;
         if (idx >= kRouteBlock * E) break;
-        int r, e;
-        split_idx(idx, r, e);
+        const int r = row_of(idx), e = col_of(idx);
         const int64_t t = t0 + r;
         float val = v[j];
         if (t < T) {
@@ -374,8 +372,7 @@ __global__ __launch_bounds__(1024) void router_topk_kernel(
   }
   for (int idx = nchunk == 1 ? kRouteBlock * E : threadIdx.x; idx < kRouteBlock * E;
        idx += blockDim.x) {
-    int r, e;
-    split_idx(idx, r, e);
+    const int r = row_of(idx), e = col_of(idx);
     int64_t t = t0 + r;
     float v = 0.f;
     if (t < T) {
