@@ -4,26 +4,33 @@
 // over MasterLinear, :58-78, with the SwiGLU / ReLU^2 epilogue fused):
 //   c[r, j] = epilogue(a_src(r) . w_s[j, :])   for every row r of segment s.
 // What changes is how the two operands reach the matrix cores:
-//   * token rows (A, gathered through src_row for the up projection) are shared by all 8 waves
+//   * token rows (A, gathered through src_row for the up projection) are shared by all waves
 //     of a workgroup, so they go through LDS, in a ring of 4 stages: while one pair of K steps
 //     is computed from two stages, the next pair's two are loaded (direct-to-LDS loads,
 //     XOR-swizzled so fragment reads are conflict-free);
-//   * expert weights are not shared between waves (wave w owns weight rows [32 w, 32 w + 32) of
-//     the 256-row tile), so they skip LDS: each wave streams its own 4 KB per K step into
+//   * expert weights are not shared between waves (each wave owns 32 or 64 of the tile's 256
+//     weight rows), so they skip LDS: each wave streams its own 4 KB blocks per K step into
 //     registers, one K step ahead. The weights are packed once (pack kernel below) so that the
 //     16-byte fragment chunk of lane l for K slice q sits at offset (q * 64 + l) * 16 of a 4 KB
 //     block: every weight load instruction reads 1 KB of consecutive bytes.
 // K order. Inside a 64-wide K step, lane half h of both operands holds K elements
 // [32 h + 8 q, +8) for MFMA slice q (instead of [16 q + 8 h, +8)): the same permutation on both
 // operands, so each product still pairs equal K indices and the 4 slices cover the step.
-// Tile: 256 tokens x 256 weight rows x 64 K, 8 waves in a 1 x 8 layout; a wave computes 8
-// 32 x 32 accumulators (its 32 weight rows against the 256 tokens). For SwiGLU a wave's 32
-// rows are 16 gate rows and the 16 value rows of the same output columns (packed together), so
-// gate and value of an output land in the same lane (elements 4 g + r and 4 (g + 2) + r).
+// Tile: 128 tokens x 256 weight rows x 64 K, 4 waves, two workgroups per CU (the default); or
+// 256 tokens x 256 rows with 8 waves, one workgroup per CU. A wave computes 8 32 x 32
+// accumulators: its 64 weight rows against 128 tokens (each token fragment read from LDS
+// feeds two MFMAs), or 32 rows against 256 tokens. For SwiGLU a 32-row block is 16 gate rows
+// and the 16 value rows of the same output columns (packed together), so gate and value of an
+// output land in the same lane (elements 4 g + r and 4 (g + 2) + r).
+// Two workgroups per CU: while one waits at its barrier or in its epilogue, the other keeps
+// the matrix cores busy, and LDS fragment reads are halved; the weights are then streamed once
+// per 128 tokens instead of 256.
 // Scheduling: persistent workgroups walk an XCD-contiguous share of the (segment, m, n) tile
 // list, as the unpacked kernel does. The load pipeline runs across tile boundaries; the gather
 // indices of the next tile go into an LDS table four K steps before they are needed, so the
 // in-order completion of vector memory operations already guarantees them when they are read.
+// The producer locates that next tile (one ballot over the segment table), and the consumer
+// takes it from there.
 // K steps go in pairs (g even, g + 1) with one workgroup barrier per pair: a barrier per K step
 // idles the matrix cores far more than its own latency (the waves of a SIMD, released together,
 // finish together and leave the pipe empty while the workgroup gathers). Waits count
@@ -32,6 +39,7 @@
 // LDS, each with one gather-index load); the odd step issues B(g + 2); at the end of a tile the
 // epilogue's fixed number of stores follow.
 #include <math.h>
+#include <stdlib.h>
 #include <type_traits>
 
 #include "common.h"
@@ -44,19 +52,36 @@ typedef __attribute__((address_space(3))) void lvoid;
 
 constexpr int kBufferWord3 = 0x00020000;
 
-constexpr int kBM = 256;           // tokens per tile
 constexpr int kBK = 64;            // K per step
 constexpr int kSA = 4;             // LDS stages of token rows
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;
 constexpr int kRB = kBK * 2;       // bytes per staged token row
 constexpr int kCH = kRB / 16;      // 16-byte chunks per row (8)
 constexpr int kWIN = 256 / kRB;    // rows per 256-byte bank window (2)
 constexpr int kRPI = 64 / kCH;     // rows per load instruction (8)
-constexpr int kAQ = kBM / kRPI / kWaves;  // A load instructions per wave per stage (4)
-constexpr int kStage = kBM * kRB;  // 32 KB
 constexpr int kBlockElems = 32 * kBK;  // packed weight block (32 rows x 64 K) = 2048 bf16
 constexpr int kMinK = 4 * kBK;     // the gather table needs four K steps of lead
+constexpr int kTileBlocks = 8;     // packed 32-row weight blocks per N tile (256 weight rows)
+
+// Two workgroup shapes share the kernel. WAVES = 8: 256 tokens per tile, one weight block per
+// wave, one workgroup per CU. WAVES = 4: 128 tokens per tile, two weight blocks per wave (each
+// token fragment read from LDS feeds two MFMAs), two workgroups per CU, so one workgroup's
+// barrier waits and epilogue run while the other's waves keep the matrix cores busy.
+template <int WAVES>
+struct Geo {
+  static constexpr int kWaves = WAVES;
+  static constexpr int kThreads = WAVES * 64;
+  static constexpr int kWB = kTileBlocks / WAVES;   // weight blocks per wave
+  static constexpr int kBM = WAVES * 32;            // tokens per tile
+  static constexpr int kNJ = kBM / 32;              // 32-token blocks per tile
+  static constexpr int kAQ = kBM / kRPI / WAVES;    // A load instructions per wave per stage (4)
+  static constexpr int kStage = kBM * kRB;          // bytes per LDS stage
+  static constexpr int kIdxWaves = kBM / 64;        // waves that load a tile's gather indices
+  static constexpr int kPerCU = 8 / WAVES;          // workgroups per CU
+  static constexpr size_t lds(int S) {
+    return (size_t)kSA * kStage + (2 * kBM + kWaves * 64) * sizeof(int) +
+           (size_t)(2 * S + 2) * sizeof(int);
+  }
+};
 
 // Row order inside a packed 32-row block. A 32 x 32 accumulator holds, in element i of lane
 // half h, block position 8 (i / 4) + 4 h + i % 4; the pack kernel puts logical row
@@ -92,11 +117,14 @@ struct Tile {
   int s, nt, m0, seg_end;
 };
 
-template <int EPI, bool GATHER>
-__global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
+template <int EPI, bool GATHER, int WAVES>
+__global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
     const uint16_t* __restrict__ A, int64_t ld_a, const int32_t* __restrict__ src_row,
     const int32_t* __restrict__ seg_offsets, int S, int total_rows, int64_t a_rows,
     const uint16_t* __restrict__ Wp, int K, int n_out, uint16_t* __restrict__ Cout) {
+  using Gm = Geo<WAVES>;
+  constexpr int kBM = Gm::kBM, kWaves = Gm::kWaves, kAQ = Gm::kAQ, kStage = Gm::kStage;
+  constexpr int kWB = Gm::kWB, kNJ = Gm::kNJ, kIdxWaves = Gm::kIdxWaves;
   constexpr int G = GATHER ? 1 : 0;
   extern __shared__ __align__(16) unsigned char smem[];
   int* src_tab = reinterpret_cast<int*>(smem + kSA * kStage);  // [2][kBM]
@@ -106,7 +134,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
 
   const int lane = lane_id(), wave = wave_id();
   const int NB = (EPI == NT_MOE_EPI_SWIGLU ? 2 * n_out : n_out) / 32;  // packed 32-row blocks
-  const int n_tiles = (NB + kWaves - 1) / kWaves;
+  const int n_tiles = (NB + kTileBlocks - 1) / kTileBlocks;
   const int nk = K / kBK;
   __builtin_assume(nk >= kMinK / kBK && nk % 2 == 0);  // the launcher guarantees both
 
@@ -147,40 +175,49 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
   const int xcd = blockIdx.x % 8, local = blockIdx.x / 8, per_xcd = gridDim.x / 8;
   const int t_begin = (int)((int64_t)total * xcd / 8);
   const int t_end = (int)((int64_t)total * (xcd + 1) / 8);
-  // Round-robin over the XCD's workgroups. When the last round would leave more than half of
-  // them idle, its tiles are split into two 128-row halves, so twice as many workgroups share
-  // it and the busiest does half a tile less (a half still streams the tile's weights, so it
-  // costs more than half a tile: worth it only when the workgroups would idle anyway).
   const int n_x = t_end - t_begin;
+  // Round-robin over the XCD's workgroups. When the last round would leave more than half of
+  // them idle, its tiles are split into two kBM/2-row halves, so twice as many workgroups share
+  // it (a half still streams the tile's weights, so it costs more than half a tile: worth it
+  // only when the workgroups would idle anyway). With two workgroups per CU, the first
+  // dispatched (lower local index) wins instruction arbitration, so the leftover tiles, which
+  // go to the lowest local indices, land on the faster ones.
   const int full_rounds = n_x / per_xcd, rem = n_x - full_rounds * per_xcd;
   const bool split_tail = rem > 0 && 2 * rem <= per_xcd;
   const int n_my = full_rounds + (local < (split_tail ? 2 * rem : rem) ? 1 : 0);
   if (n_my == 0) return;
-  const int total_steps = n_my * nk;
 
-  auto locate = [&](int idx, Tile& t) {  // idx-th tile (or half tile) of this workgroup
-    const bool half_tile = split_tail && idx == full_rounds;
-    const int tl = half_tile ? t_begin + full_rounds * per_xcd + (local >> 1)
-                             : t_begin + local + idx * per_xcd;
-    int lo = 0, hi = S;
-    while (hi - lo > 1) {
-      int mid = (lo + hi) >> 1;
-      if (tile_prefix[mid] <= tl) lo = mid; else hi = mid;
+  // Tile number tl (half: -1 whole, 0 or 1 for the lower or upper kBM/2 rows) -> segment and
+  // position. The segment is the last one whose tile prefix is <= tl: one ballot per 64 segments.
+  auto locate_tl = [&](int tl, int half, Tile& t) {
+    int cnt = 0;
+    for (int base = 0; base < S; base += 64) {
+      const int i = base + lane;
+      const bool le = i < S && tile_prefix[i] <= tl;
+      cnt += __popcll(__ballot(le));
     }
-    t.s = __builtin_amdgcn_readfirstlane(lo);
+    t.s = __builtin_amdgcn_readfirstlane(cnt - 1);
     const int lt = tl - __builtin_amdgcn_readfirstlane(tile_prefix[t.s]);
     const int mt = lt / n_tiles;
     t.nt = lt - mt * n_tiles;
     t.seg_end = __builtin_amdgcn_readfirstlane(seg_lo[t.s + 1]);
     t.m0 = __builtin_amdgcn_readfirstlane(seg_lo[t.s]) + mt * kBM;
-    if (half_tile) {  // rows [m0, m0 + 128) or [m0 + 128, m0 + 256) of the tile
+    if (half >= 0) {  // rows [m0, m0 + kBM/2) or [m0 + kBM/2, m0 + kBM) of the tile
       const int tile_end = t.seg_end < t.m0 + kBM ? t.seg_end : t.m0 + kBM;
-      if (local & 1) t.m0 += kBM / 2;
-      t.seg_end = (local & 1) ? tile_end : (tile_end < t.m0 + kBM / 2 ? tile_end : t.m0 + kBM / 2);
+      if (half) t.m0 += kBM / 2;
+      t.seg_end = half ? tile_end : (tile_end < t.m0 + kBM / 2 ? tile_end : t.m0 + kBM / 2);
     }
   };
-  // Gather indices of tile t into table slot `slot`: waves 0-3 load 64 rows each, straight to
-  // LDS; rows past the segment end repeat its last row (their results are dropped).
+  // The idx-th tile of this workgroup.
+  auto locate_static = [&](int idx, Tile& t) {
+    if (split_tail && idx == full_rounds)
+      locate_tl(t_begin + full_rounds * per_xcd + (local >> 1), local & 1, t);
+    else
+      locate_tl(t_begin + local + idx * per_xcd, -1, t);
+  };
+
+  // Gather indices of tile t into table slot `slot`: the first kBM / 64 waves load 64 rows each,
+  // straight to LDS; rows past the segment end repeat its last row (their results are dropped).
   const char* abase = reinterpret_cast<const char*>(A);
   // Byte offsets of this lane's four A chunks (one per load instruction) for tile t.
   // Instruction q covers rows (wave kAQ + q) kRPI + [0, kRPI); a row's swizzle depends only on
@@ -200,19 +237,22 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
       aoff[q] = (uint32_t)(r * ld_a * 2) + aswz[q % 2];
     }
   };
-  // This wave's packed weight blocks for tile t (clamped in a partial N tile): a wave-uniform
-  // address, to which each lane adds lane * 16 bytes.
-  auto w_base = [&](const Tile& t) {
-    int nb = t.nt * kWaves + wave;
-    nb = nb < NB ? nb : NB - 1;
-    return Wp + ((int64_t)t.s * NB + nb) * (int64_t)nk * kBlockElems;
+  // This wave's packed weight blocks for tile t (clamped in a partial N tile): wave-uniform
+  // addresses, to which each lane adds lane * 16 bytes.
+  auto w_base = [&](const Tile& t, const uint16_t* (&wb)[kWB]) {
+#pragma unroll
+    for (int rb = 0; rb < kWB; ++rb) {
+      int nb = t.nt * kTileBlocks + wave * kWB + rb;
+      nb = nb < NB ? nb : NB - 1;
+      wb[rb] = Wp + ((int64_t)t.s * NB + nb) * (int64_t)nk * kBlockElems;
+    }
   };
   const uint32_t b_lane = lane * 16;
   // Weight loads are issued from inline assembly: the compiler then neither counts them nor
   // inserts its own (conservative, loop-merged) waits for their registers; the explicit wait
   // before their use names the registers, so no use can be scheduled above it. The block address
   // is a scalar operand, the lane offset the only vector one.
-  auto load_b = [&](const uint16_t* blk, u32x4 (&b)[4]) {
+  auto load_blk = [&](const uint16_t* blk, u32x4 (&b)[4]) {
     asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(b[0]) : "v"(b_lane), "s"(blk) : "memory");
     asm volatile("global_load_dwordx4 %0, %1, %2 offset:1024"
                  : "=v"(b[1]) : "v"(b_lane), "s"(blk) : "memory");
@@ -221,18 +261,68 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
     asm volatile("global_load_dwordx4 %0, %1, %2 offset:3072"
                  : "=v"(b[3]) : "v"(b_lane), "s"(blk) : "memory");
   };
+  // K step kt of this wave's blocks (kt = nk: the first step of the blocks in wn).
+  auto load_b = [&](const uint16_t* const (&wc)[kWB], const uint16_t* const (&wn)[kWB], int kt,
+                    u32x4 (&b)[kWB][4]) {
+#pragma unroll
+    for (int rb = 0; rb < kWB; ++rb)
+      load_blk(kt < nk ? wc[rb] + (int64_t)kt * kBlockElems : wn[rb], b[rb]);
+  };
+  // Waits until at most N vector memory operations are outstanding, naming the registers of
+  // the weight blocks b: no read of them can be scheduled above the wait.
+  auto wait_b = [&](auto n_c, u32x4 (&b)[kWB][4]) {
+    constexpr int N = decltype(n_c)::value;
+    if constexpr (kWB == 1) {
+      asm volatile("s_waitcnt vmcnt(%4)"
+                   : "+v"(b[0][0]), "+v"(b[0][1]), "+v"(b[0][2]), "+v"(b[0][3])
+                   : "n"(N)
+                   : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(%8)"
+                   : "+v"(b[0][0]), "+v"(b[0][1]), "+v"(b[0][2]), "+v"(b[0][3]),
+                     "+v"(b[1][0]), "+v"(b[1][1]), "+v"(b[1][2]), "+v"(b[1][3])
+                   : "n"(N)
+                   : "memory");
+    }
+  };
+
+  // ---- producer: one A stage (+ one gather-index load) per call, two calls per pair ----------
+  // Every call issues the same vector memory operations -- 4 token-row loads and, with GATHER,
+  // one gather-index load -- whether or not they are needed (past the end they re-read valid
 
   // ---- producer: one A stage (+ one gather-index load) per call, two calls per pair ----------
   // Every call issues the same vector memory operations -- 4 token-row loads and, with GATHER,
   // one gather-index load -- whether or not they are needed (past the end they re-read valid
   // addresses into slots nobody reads), so the wait counts are the same in every pair.
-  Tile pt, pnext;
+  // The producer also finds the workgroup's next tile, four K steps before its first stage:
+  // tile i goes to tq[i % 2] (tile_ok[i % 2] says whether it exists), which is where the
+  // consumer takes it from.
+  Tile pt, tq0, tq1;
+  bool ok0 = true, ok1 = false;
   int p_idx = 0, p_kt = 0, p_slot = 0, produced = 0;
+  int total_steps = 0x7fffffff;  // known once the producer finds there is no next tile
   uint32_t aoff[kAQ];
   const int src_lead_kt = nk - 4;  // K step of a tile at which the next tile's indices go out
+  // Selects between the values (not between the two variables' addresses, which would put
+  // them in scratch memory).
+  auto pick = [](bool o, int x1, int x0) {
+    const int a1 = __builtin_amdgcn_readfirstlane(x1), a0 = __builtin_amdgcn_readfirstlane(x0);
+    return o ? a1 : a0;
+  };
+  auto tile_at = [&](int i) {
+    Tile r;
+    const bool o = i & 1;
+    r.s = pick(o, tq1.s, tq0.s);
+    r.nt = pick(o, tq1.nt, tq0.nt);
+    r.m0 = pick(o, tq1.m0, tq0.m0);
+    r.seg_end = pick(o, tq1.seg_end, tq0.seg_end);
+    return r;
+  };
+  auto tile_ok = [&](int i) { return pick(i & 1, ok1, ok0) != 0; };
 
-  locate(0, pt);
-  if (GATHER && wave < 4) {  // the first tile's gather indices, before anything else
+  locate_static(0, pt);
+  tq0 = pt;
+  if (GATHER && wave < kIdxWaves) {  // the first tile's gather indices, before anything else
     const int r = wave * 64 + lane;
     const int gr = pt.m0 + r < pt.seg_end ? pt.m0 + r : pt.seg_end - 1;
     __builtin_amdgcn_global_load_lds((gvoid*)(src_row + gr), (lvoid*)(src_tab + wave * 64), 4,
@@ -245,7 +335,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
   auto produce = [&]() {
     const bool live = produced < total_steps;
     if (live && p_kt == nk) {  // next tile: its gather indices went out four stages ago
-      pt = pnext;
+      pt = tile_at(p_idx + 1);
       ++p_idx;
       p_kt = 0;
       p_slot ^= 1;
@@ -257,13 +347,25 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
     for (int q = 0; q < kAQ; ++q)
       __builtin_amdgcn_global_load_lds((gvoid*)(abase + kt_load * kRB + aoff[q]),
                                        (lvoid*)(sb + (wave * kAQ + q) * 1024), 16, 0, 0);
-    const bool locate_next = live && p_kt == src_lead_kt && p_idx + 1 < n_my;
-    if (locate_next) locate(p_idx + 1, pnext);
+    bool real = false;
+    Tile nx;
+    if (live && p_kt == src_lead_kt) {  // find tile p_idx + 1
+      real = p_idx + 1 < n_my;
+      if (real) locate_static(p_idx + 1, nx);
+      if ((p_idx + 1) & 1) {
+        tq1 = nx;
+        ok1 = real;
+      } else {
+        tq0 = nx;
+        ok0 = real;
+      }
+      if (!real) total_steps = (p_idx + 1) * nk;
+    }
     if (GATHER) {
-      const bool real = locate_next && wave < 4;
-      const int r = (wave & 3) * 64 + lane;
-      const int gr = real ? (pnext.m0 + r < pnext.seg_end ? pnext.m0 + r : pnext.seg_end - 1) : 0;
-      int* dst = real ? src_tab + (p_slot ^ 1) * kBM + wave * 64 : src_dummy + wave * 64;
+      const bool load_idx = real && wave < kIdxWaves;
+      const int r = (wave % kIdxWaves) * 64 + lane;
+      const int gr = load_idx ? (nx.m0 + r < nx.seg_end ? nx.m0 + r : nx.seg_end - 1) : 0;
+      int* dst = load_idx ? src_tab + (p_slot ^ 1) * kBM + wave * 64 : src_dummy + wave * 64;
       __builtin_amdgcn_global_load_lds((gvoid*)(src_row + gr), (lvoid*)dst, 4, 0, 0);
     }
     if (live) ++p_kt;
@@ -281,30 +383,29 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
 
   // ---- consumer ---------------------------------------------------------------------------
   Tile ct = pt;
-  const uint16_t* wb = w_base(ct);
-  u32x4 b0[4], b1[4];
+  const uint16_t* wb[kWB];
+  w_base(ct, wb);
+  u32x4 b0[kWB][4], b1[kWB][4];
   // Prologue: A(0), A(1), B(0), all landed before the first pair's barrier.
   produce();
   asm volatile("" ::: "memory");
   produce();
   asm volatile("" ::: "memory");
-  load_b(wb, b0);
-  asm volatile("s_waitcnt vmcnt(0)" : "+v"(b0[0]), "+v"(b0[1]), "+v"(b0[2]), "+v"(b0[3]) :: "memory");
+  load_b(wb, wb, 0, b0);
+  wait_b(std::integral_constant<int, 0>(), b0);
 
-  int g = 0;          // global K step of this workgroup
-  for (int ti = 0; ti < n_my; ++ti) {
-    if (ti > 0) locate(ti, ct);
+  int g = 0;   // global K step of this workgroup
+  int ti = 0;  // this workgroup's tile number
+  for (;;) {
     const int live_m = ct.seg_end - ct.m0;  // token rows of this tile that exist (uniform)
-    const bool has_next = ti + 1 < n_my;
-    const uint16_t* wb_next = wb;
-    if (has_next) {
-      Tile nx;
-      locate(ti + 1, nx);
-      wb_next = w_base(nx);
-    }
-    floatx16 acc[8];
+    const uint16_t* wb_next[kWB];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = floatx16{};
+    for (int rb = 0; rb < kWB; ++rb) wb_next[rb] = wb[rb];
+    floatx16 acc[kWB][kNJ];
+#pragma unroll
+    for (int rb = 0; rb < kWB; ++rb)
+#pragma unroll
+      for (int j = 0; j < kNJ; ++j) acc[rb][j] = floatx16{};
 
     // K steps go in pairs (g even, g + 1) with one workgroup barrier per pair. The even step
     // issues B(g + 1) and both token-row stages of the next pair, A(g + 2) and A(g + 3) (each
@@ -313,16 +414,16 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
     // step, which names their registers so no copy of them can happen before they are valid;
     // the odd step's wait (vmcnt 0) also lands this wave's part of the next pair's stages,
     // which the next barrier then publishes to every wave.
-    auto step = [&](auto nj_c, auto odd_c, int kt, u32x4 (&bc)[4], u32x4 (&bn)[4]) {
+    auto step = [&](auto nj_c, auto odd_c, int kt, u32x4 (&bc)[kWB][4], u32x4 (&bn)[kWB][4]) {
       constexpr int NJ = decltype(nj_c)::value;  // 32-token blocks that hold segment rows
       constexpr bool ODD = decltype(odd_c)::value;
-      constexpr int NM = 4 * NJ;                 // MFMAs per wave in this step
+      constexpr int NM = 4 * NJ;                 // token fragments per step (kWB MFMAs each)
       constexpr int PF = NM < 4 ? NM : 4;        // fragment reads kept in flight
       if (!ODD) barrier_nofence();
       // The first PF token fragments go out first, so their latency overlaps the issue of this
       // step's loads instead of idling the matrix core.
       const unsigned char* st = smem + (g % kSA) * kStage;
-      // NM MFMAs (slice q = n / NJ, token block j = n % NJ), token fragments read PF ahead.
+      // NM token fragments (slice q = n / NJ, token block j = n % NJ), read PF ahead.
       auto frag = [&](int n) {
         return *reinterpret_cast<const bf16x8*>(st + (n % NJ) * 32 * kRB + frag_off[n / NJ]);
       };
@@ -330,10 +431,8 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
 #pragma unroll
       for (int n = 0; n < PF; ++n) fr[n] = frag(n);
       asm volatile("" ::: "memory");
-      const uint16_t* bsrc = wb + (int64_t)kt * kBlockElems;  // past the end: a re-read
-      if (kt + 1 < nk) bsrc = wb + (int64_t)(kt + 1) * kBlockElems;
-      else if (has_next) bsrc = wb_next;
-      load_b(bsrc, bn);
+      if (kt + 1 == nk && tile_ok(ti + 1)) w_base(tile_at(ti + 1), wb_next);
+      load_b(wb, wb_next, kt + 1, bn);  // past the last tile: re-reads of its first step
       asm volatile("" ::: "memory");
       if (!ODD) {
         produce();
@@ -343,23 +442,22 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
       }
 #pragma unroll
       for (int n = 0; n < NM; ++n) {
-        acc[n % NJ] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            __builtin_bit_cast(bf16x8, bc[n / NJ]), fr[n % PF], acc[n % NJ], 0, 0, 0);
+#pragma unroll
+        for (int rb = 0; rb < kWB; ++rb)
+          acc[rb][n % NJ] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8, bc[rb][n / NJ]), fr[n % PF], acc[rb][n % NJ], 0, 0, 0);
         if (n + PF < NM) fr[n % PF] = frag(n + PF);
       }
-      // Keep PF fragment reads in flight: (1 MFMA, 1 read) pairs, then the last PF MFMAs.
-      // Without this the scheduler pulls each read next to its MFMA and waits on it.
+      // Keep PF fragment reads in flight: (kWB MFMAs, 1 read) groups, then the last PF groups'
+      // MFMAs. Without this the scheduler pulls each read next to its MFMA and waits on it.
 #pragma unroll
       for (int n = 0; n < NM - PF; ++n) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, kWB, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, kWB * PF, 0);
       // Even step: the two stages and index loads issued after B(g + 1) may stay in flight.
-      asm volatile("s_waitcnt vmcnt(%4)"
-                   : "+v"(bn[0]), "+v"(bn[1]), "+v"(bn[2]), "+v"(bn[3])
-                   : "n"(ODD ? 0 : 2 * (kAQ + G))
-                   : "memory");
+      wait_b(std::integral_constant<int, ODD ? 0 : 2 * (kAQ + G)>(), bn);
       ++g;
     };
     auto k_loop = [&](auto nj_c) {
@@ -369,10 +467,10 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
       }
     };
     // A partial tile (the last of a segment) multiplies only the 32-token blocks that hold
-    // rows: 1, 2, 4 or all 8 of them. The loads are the same in every variant.
-    if (live_m > 128) k_loop(std::integral_constant<int, 8>());
-    else if (live_m > 64) k_loop(std::integral_constant<int, 4>());
-    else if (live_m > 32) k_loop(std::integral_constant<int, 2>());
+    // rows. The loads are the same in every variant.
+    if (live_m > kBM / 2) k_loop(std::integral_constant<int, kNJ>());
+    else if (live_m > kBM / 4) k_loop(std::integral_constant<int, kNJ / 2>());
+    else if (kNJ >= 8 && live_m > kBM / 8) k_loop(std::integral_constant<int, kNJ / 4 ? kNJ / 4 : 1>());
     else k_loop(std::integral_constant<int, 1>());
 
     // Epilogue: a fixed store count per wave; rows past the segment or columns past n_out get
@@ -380,40 +478,47 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_packed_kernel(
     // holds logical block rows 8 h + [0, 8) in elements 0-7 and 16 + 8 h + [0, 8) in 8-15:
     // for SwiGLU gate and value of output columns 16 nb + 8 h + [0, 8), otherwise columns
     // 32 nb + 8 h + [0, 8) and 32 nb + 16 + 8 h + [0, 8).
-    const int nb = ct.nt * kWaves + wave;
     const int hbit = lane >> 5;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int m = ct.m0 + j * 32 + (lane & 31);
-      const bool row_ok = m < ct.seg_end;
+    for (int rb = 0; rb < kWB; ++rb) {
+      const int nb = ct.nt * kTileBlocks + wave * kWB + rb;
 #pragma unroll
-      for (int st = 0; st < Ep<EPI>::kStores; ++st) {
-        int col;
-        float v[8];
-        if (EPI == NT_MOE_EPI_SWIGLU) {
-          col = nb * 16 + 8 * hbit;
+      for (int j = 0; j < kNJ; ++j) {
+        const int m = ct.m0 + j * 32 + (lane & 31);
+        const bool row_ok = m < ct.seg_end;
 #pragma unroll
-          for (int r = 0; r < 8; ++r) {
-            const float a = acc[j][r], u = acc[j][8 + r];
-            v[r] = a * u * __builtin_amdgcn_rcpf(1.f + __expf(-a));
+        for (int st = 0; st < Ep<EPI>::kStores; ++st) {
+          int col;
+          float v[8];
+          if (EPI == NT_MOE_EPI_SWIGLU) {
+            col = nb * 16 + 8 * hbit;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+              const float a = acc[rb][j][r], u = acc[rb][j][8 + r];
+              v[r] = a * u * __builtin_amdgcn_rcpf(1.f + __expf(-a));
+            }
+          } else {
+            col = nb * 32 + 16 * st + 8 * hbit;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+              const float a = acc[rb][j][8 * st + r];
+              v[r] = EPI == NT_MOE_EPI_RELU2 ? (a > 0.f ? a * a : 0.f) : a;
+            }
           }
-        } else {
-          col = nb * 32 + 16 * st + 8 * hbit;
-#pragma unroll
-          for (int r = 0; r < 8; ++r) {
-            const float a = acc[j][8 * st + r];
-            v[r] = EPI == NT_MOE_EPI_RELU2 ? (a > 0.f ? a * a : 0.f) : a;
-          }
+          const u32x4 packed = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+          const uint32_t voff = (row_ok && nb < NB && col < n_out)
+                                    ? (uint32_t)(((int64_t)m * n_out + col) * 2)
+                                    : 0x80000000u;
+          __builtin_amdgcn_raw_buffer_store_b128(packed, out_rsrc, voff, 0, 0);
         }
-        const u32x4 packed = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
-                              pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
-        const uint32_t voff = (row_ok && nb < NB && col < n_out)
-                                  ? (uint32_t)(((int64_t)m * n_out + col) * 2)
-                                  : 0x80000000u;
-        __builtin_amdgcn_raw_buffer_store_b128(packed, out_rsrc, voff, 0, 0);
       }
     }
-    wb = wb_next;
+    if (!tile_ok(ti + 1)) break;
+    ++ti;
+    ct = tile_at(ti);
+#pragma unroll
+    for (int rb = 0; rb < kWB; ++rb) wb[rb] = wb_next[rb];
   }
   vm_wait<0>();  // the trailing re-reads land in LDS before the workgroup's LDS is released
 }
@@ -441,24 +546,33 @@ __global__ __launch_bounds__(256) void pack_weights_kernel(const uint16_t* __res
       *reinterpret_cast<const u32x4*>(w + (s * R + row) * (int64_t)K + k0);
 }
 
-template <int EPI, bool GATHER>
+template <int EPI, bool GATHER, int WAVES>
 hipError_t launch_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows, const int32_t* src_row,
                          const int32_t* seg_offsets, int S, int64_t total_rows,
                          const uint16_t* wp, int K, int n_out, uint16_t* c, hipStream_t stream) {
+  using Gm = Geo<WAVES>;
   const int NB = (EPI == NT_MOE_EPI_SWIGLU ? 2 * n_out : n_out) / 32;
-  const int64_t n_tiles = (NB + kWaves - 1) / kWaves;
-  const int64_t upper = ((total_rows + kBM - 1) / kBM + S) * n_tiles;
-  int64_t grid = num_cus();
+  const int64_t n_tiles = (NB + kTileBlocks - 1) / kTileBlocks;
+  const int64_t upper = ((total_rows + Gm::kBM - 1) / Gm::kBM + S) * n_tiles;
+  int64_t grid = (int64_t)num_cus() * Gm::kPerCU;
   if (upper < grid) grid = upper;
   grid = ((grid + 7) / 8) * 8;
-  const size_t lds = (size_t)kSA * kStage + (2 * kBM + kWaves * 64) * sizeof(int) +
-                     (size_t)(2 * S + 2) * sizeof(int);
-  auto kern = grouped_gemm_packed_kernel<EPI, GATHER>;
+  const size_t lds = Gm::lds(S);
+  auto kern = grouped_gemm_packed_kernel<EPI, GATHER, WAVES>;
   hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), lds, stream, a, ld_a, src_row,
-                     seg_offsets, S, (int)total_rows, a_rows, wp, K, n_out, c);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(Gm::kThreads), lds, stream, a, ld_a,
+                     src_row, seg_offsets, S, (int)total_rows, a_rows, wp, K, n_out, c);
   return hipGetLastError();
+}
+
+// Workgroup shape of the packed kernel: 4 (two workgroups per CU) unless NT_MOE_PACKED_WAVES=8.
+int packed_waves() {
+  static const int w = [] {
+    const char* s = getenv("NT_MOE_PACKED_WAVES");
+    return s && atoi(s) == 8 ? 8 : 4;
+  }();
+  return w;
 }
 
 }  // namespace
@@ -481,19 +595,26 @@ hipError_t launch_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int6
                                            const uint16_t* wp, int K, int n_out, int epilogue,
                                            uint16_t* c, hipStream_t stream) {
   if (total_rows == 0) return hipSuccess;
-#define NT_P(EPI)                                                                          \
-  return src_row ? launch_packed<EPI, true>(a, ld_a, a_rows, src_row, seg_offsets,         \
-                                            num_segments, total_rows, wp, K, n_out, c,      \
-                                            stream)                                         \
-                 : launch_packed<EPI, false>(a, ld_a, a_rows, src_row, seg_offsets,        \
-                                             num_segments, total_rows, wp, K, n_out, c,     \
-                                             stream)
+#define NT_PW(EPI, W)                                                                      \
+  return src_row ? launch_packed<EPI, true, W>(a, ld_a, a_rows, src_row, seg_offsets,      \
+                                               num_segments, total_rows, wp, K, n_out, c,   \
+                                               stream)                                      \
+                 : launch_packed<EPI, false, W>(a, ld_a, a_rows, src_row, seg_offsets,     \
+                                                num_segments, total_rows, wp, K, n_out, c,  \
+                                                stream)
+#define NT_P(EPI)                  \
+  if (packed_waves() == 8) {       \
+    NT_PW(EPI, 8);                 \
+  } else {                         \
+    NT_PW(EPI, 4);                 \
+  }
   switch (epilogue) {
     case NT_MOE_EPI_SWIGLU: NT_P(NT_MOE_EPI_SWIGLU);
     case NT_MOE_EPI_RELU2: NT_P(NT_MOE_EPI_RELU2);
     default: NT_P(NT_MOE_EPI_NONE);
   }
 #undef NT_P
+#undef NT_PW
 }
 
 }  // namespace ntmoe

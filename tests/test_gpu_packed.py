@@ -88,6 +88,47 @@ def test_packed_gemm_matches_fp32(K, epilogue, gather):
     assert rel_l2(c.float(), _ref_gemm(a, src, seg, w, epilogue)) <= BF16_TOL
 
 
+@pytest.mark.parametrize("K", [512, 1024])
+@pytest.mark.parametrize("epilogue", [0, 2], ids=["swiglu", "plain"])
+@pytest.mark.parametrize("gather", [False, True])
+@pytest.mark.parametrize("rows_scale", [1, 3])
+def test_packed_gemm_many_tiles(K, epilogue, gather, rows_scale):
+    # Enough tiles for full rounds of the two-workgroups-per-CU schedule plus a last partial
+    # round (split into halves or not, by size); every output row must be written, and sampled
+    # rows of every segment match fp32.
+    from nexttransformer_amd import ops
+    g = torch.Generator().manual_seed(7 * K + epilogue + rows_scale)
+    counts = [c * rows_scale for c in [9000, 0, 7777, 129, 12000, 1, 6500, 4200]]
+    S, n_out = len(counts), 512
+    R = 2 * n_out if epilogue == 0 else n_out
+    rows = sum(counts)
+    seg = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32)
+    a_rows = 20000 if gather else rows
+    a = torch.randn(a_rows, K, generator=g).to(torch.bfloat16)
+    src = torch.randint(0, a_rows, (rows,), generator=g, dtype=torch.int32) if gather else None
+    w = (torch.randn(S, R, K, generator=g) * 0.05).to(torch.bfloat16)
+    wp = ops.pack_expert_weights(w.cuda(), epilogue)
+    c = ops.grouped_gemm_packed(a.cuda(), None if src is None else src.cuda(), seg.cuda(), wp,
+                                epilogue, rows)
+    c2 = ops.grouped_gemm_packed(a.cuda(), None if src is None else src.cuda(), seg.cuda(), wp,
+                                 epilogue, rows)
+    torch.cuda.synchronize()
+    c = c.cpu()
+    assert torch.isfinite(c.float()).all() and torch.equal(c, c2.cpu())
+    pick = torch.cat([torch.arange(lo, min(lo + 40, hi)) for lo, hi in
+                      zip(seg[:-1].tolist(), seg[1:].tolist()) if hi > lo]
+                     + [torch.randint(0, rows, (200,), generator=g)])
+    a_idx = src[pick].long() if gather else pick
+    seg_of = torch.searchsorted(seg[1:].long(), pick, right=True)
+    ref = torch.empty(len(pick), n_out, dtype=torch.float64)
+    for s_ in range(S):
+        m = seg_of == s_
+        if m.any():
+            z = a[a_idx[m]].double() @ w[s_].double().t()
+            ref[m] = torch.nn.functional.silu(z[:, :n_out]) * z[:, n_out:] if epilogue == 0 else z
+    assert rel_l2(c[pick].float(), ref) <= BF16_TOL
+
+
 PACKED_CASES = [
     Case("cfg1-shape", 512, 256, 8, 2, 512),
     Case("ragged-T1000-E32-k4", 1000, 1024, 32, 4, 512, seed=1),
