@@ -419,7 +419,20 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
       constexpr bool ODD = decltype(odd_c)::value;
       constexpr int NM = 4 * NJ;                 // token fragments per step (kWB MFMAs each)
       constexpr int PF = NM < 4 ? NM : 4;        // fragment reads kept in flight
-      if (!ODD) barrier_nofence();
+      if (!ODD) {
+        barrier_nofence();
+        // Two workgroups share each CU (b and b + gridDim.x / 2) and the one dispatched first
+        // would win instruction arbitration throughout, leaving its partner to finish alone.
+        // Instead the two take turns at the higher wave priority, switching every 2^11 ticks
+        // (about 20 us) of the 100 MHz real-time counter, so both progress alike.
+        if (kWaves == 4) {
+          uint64_t now;
+          asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(now));
+          const bool high = (((now >> 11) & 1) != 0) != (blockIdx.x >= gridDim.x / 2);
+          if (high) __builtin_amdgcn_s_setprio(1);
+          else __builtin_amdgcn_s_setprio(0);
+        }
+      }
       // The first PF token fragments go out first, so their latency overlaps the issue of this
       // step's loads instead of idling the matrix core.
       const unsigned char* st = smem + (g % kSA) * kStage;
