@@ -118,8 +118,7 @@ const char* nt_moe_last_error(void) { return g_error; }
 size_t nt_moe_router_workspace_bytes(int64_t T, int32_t d, int32_t E, int32_t k) {
   (void)k;
   if (T <= 0 || d <= 0 || E <= 0) return 0;
-  int nchunk = router_split_chunks(T, d, E);
-  return (size_t)nchunk * (size_t)T * (size_t)E * sizeof(float);
+  return router_workspace_need(T, d, E);
 }
 
 int nt_moe_router_fwd(const uint16_t* x, int64_t ld_x, const float* w_router_t,
@@ -137,12 +136,12 @@ int nt_moe_router_fwd(const uint16_t* x, int64_t ld_x, const float* w_router_t,
   NT_REQUIRE(x && w_router_t && topk_ids && topk_w && prob_partial && z_partial,
              "router: null buffer");
   NT_REQUIRE(aligned16(x), "router: x must be 16-byte aligned");
-  int nchunk = router_split_chunks(T, d, E);
-  size_t need = (size_t)nchunk * (size_t)T * (size_t)E * sizeof(float);
-  bool split = nchunk > 0 && workspace && workspace_bytes >= need;
+  NT_REQUIRE(E <= 128 || (workspace && workspace_bytes >= router_workspace_need(T, d, E)) ||
+                 (logits && d <= 16 * 128),
+             "router: more than 128 experts need the workspace");
   hipError_t err = launch_router(x, ld_x, w_router_t, logit_bias, T, d, E, k, score_fn, logits,
                                  topk_ids, topk_w, prob_partial, z_partial,
-                                 reinterpret_cast<float*>(workspace), split,
+                                 reinterpret_cast<float*>(workspace), workspace_bytes,
                                  reinterpret_cast<hipStream_t>(stream));
   return launched(err, "router");
 }

@@ -51,11 +51,12 @@ inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 hipError_t launch_router(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
                          int64_t T, int d, int E, int k, int score_fn, float* logits,
                          int32_t* topk_ids, float* topk_w, float* prob_partial,
-                         float* z_partial, float* partials, bool split, hipStream_t stream);
+                         float* z_partial, float* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
 hipError_t launch_topk_from_logits(const float* logits, int64_t T, int E, int k,
                                    int score_fn, int32_t* topk_ids, float* topk_w,
                                    float* prob_partial, float* z_partial, hipStream_t stream);
-int router_split_chunks(int64_t T, int d, int E);
+size_t router_workspace_need(int64_t T, int d, int E);
 
 hipError_t launch_histogram_scan(const int32_t* topk_ids, int64_t T, int k, int E,
                                  int32_t* counts, int32_t* offsets, int32_t* ranks,

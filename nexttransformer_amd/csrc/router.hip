@@ -10,15 +10,20 @@
 //   logit = ((c_0 + c_1) + c_2) + ...   then  + bias[e]
 // Ties in top-k: equal logits rank the lower expert index first.
 //
-// Work mapping. A block of 256 threads (4 waves) owns 64 tokens; lane = token. Wave w owns a
-// window of EPW consecutive experts, so its router weights are wave-uniform and come in
-// through scalar loads (w_router_t is [d, E], E contiguous); each lane keeps EPW fp32
-// accumulators. x is staged through LDS one 128-feature chunk at a time (coalesced global
-// loads, padded rows so per-lane row reads are conflict-free).
-// Unless T is very large the fused grid has too few waves per CU: the split variant gives every
-// (token block, chunk, expert group) its own block and writes the chunk sums c_j to a
-// workspace (expert-major planes); a plane-sum kernel adds them in ascending j -- the same
-// order -- and a top-k kernel ranks.
+// Work mapping. The chains run on the matrix cores: v_mfma_f32_32x32x2_f32 computes, for a
+// 32 x 32 output block, acc = fma(a1, b1, fma(a0, b0, acc)) -- two steps of the same sequential
+// fp32 fma chain (features 2n, then 2n + 1), bit for bit -- so 64 of them in ascending feature
+// order are exactly c_j for 32 tokens x 32 experts. Lane l supplies token/expert l % 32 and
+// feature parity l / 32. A block owns 64 tokens; one wave per (32-token half, 32-expert block,
+// feature range). x comes straight from global memory (16 bytes = 8 features per lane, the
+// lane's parity picked out with one byte permute), router weights from w_router_t [d, E] (for a
+// feature pair, the two lane halves read two 128-byte rows); both are prefetched half a chunk
+// ahead. With one expert block the features are split over two waves per output block: the
+// first keeps the running sum of its chunks, the second its chunk sums, added to that running
+// sum in chunk order after a barrier.
+// For small T (too few waves for the chip) the split variant gives every (token block, chunk,
+// expert block) its own waves and writes the chunk sums c_j to a workspace (token-major planes);
+// a plane-sum kernel adds them in ascending j -- the same order -- and a top-k kernel ranks.
 //
 // Top-k: logits go to an LDS tile [64][E+1]; LPT lanes share a token (4 in the fused kernel,
 // 16 in the top-k kernel), each scans every LPT-th expert into a sorted register list, then k
@@ -32,50 +37,24 @@
 namespace ntmoe {
 namespace {
 
-constexpr int kXStride = kRouterChunk + 8;  // bf16 per padded LDS row (272 bytes)
-constexpr int kXTileBytes = kRouteBlock * kXStride * 2;
-
 __host__ __device__ inline int lg_tile_bytes(int E) { return kRouteBlock * (E + 1) * 4; }
-__host__ __device__ inline int zt_offset(int E) {
-  int lg = lg_tile_bytes(E);
-  return lg > kXTileBytes ? lg : kXTileBytes;
-}
+__host__ __device__ inline int zt_offset(int E) { return (lg_tile_bytes(E) + 15) & ~15; }
 inline size_t router_lds_bytes(int E) { return zt_offset(E) + kRouteBlock * sizeof(float); }
 
-// acc[e] = fma chain over the clen features of the staged chunk (row of this lane's token).
-template <int EPW>
-__device__ __forceinline__ void chunk_fma(const uint16_t* xs_row, const float* __restrict__ wt,
-                                          int E, int ws, int c0, int clen, float* acc) {
-  for (int kk = 0; kk < clen; kk += 8) {
-    u32x4 raw = *reinterpret_cast<const u32x4*>(xs_row + kk);
-    float xf[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      xf[2 * i] = __builtin_bit_cast(float, raw[i] << 16);
-      xf[2 * i + 1] = __builtin_bit_cast(float, raw[i] & 0xffff0000u);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float* wrow = wt + (size_t)(c0 + kk + i) * E + ws;
-#pragma unroll
-      for (int e = 0; e < EPW; ++e) acc[e] = __builtin_fmaf(xf[i], wrow[e], acc[e]);
-    }
-  }
-}
+// LDS stages of the fused kernel: for each feature range, 64 features of x (64 tokens, rows
+// padded to kXPitch bf16) and of the router weights for all expert blocks, stored so that a
+// lane's 4 weights for MFMAs 4q .. 4q + 3 (features 8q + 2j + h, expert e) are one 16-byte
+// word: float index ((q * 2 + h) * Ew + e) * 4 + j, Ew = 32 EB. Lane (t, h) reads x[t][8q ..
+// 8q + 8) and those weights with one ds_read_b128 each; both reads are conflict-free.
+constexpr int kStageF = 64;                       // features per stage
+constexpr int kXPitch = kStageF + 8;              // bf16 per staged x row
+constexpr int kXStageBytes = kRouteBlock * kXPitch * 2;
+__host__ __device__ inline int w_stage_bytes(int EB) { return kStageF * 32 * EB * 4; }
+__host__ __device__ inline int range_stage_bytes(int EB) { return kXStageBytes + w_stage_bytes(EB); }
 
-// Stage x[t0 .. t0+63][c0 .. c0+clen) into LDS (zeros beyond T).
-__device__ __forceinline__ void stage_x(const uint16_t* __restrict__ x, int64_t ld_x, int64_t T,
-                                        int64_t t0, int c0, int clen, uint16_t* xs) {
-  const int groups = clen >> 3;  // 16-byte groups per row
-  for (int g = threadIdx.x; g < kRouteBlock * 16; g += blockDim.x) {
-    int row = g >> 4, col = g & 15;
-    if (col >= groups) continue;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    int64_t t = t0 + row;
-    if (t < T) v = *reinterpret_cast<const u32x4*>(x + t * ld_x + c0 + col * 8);
-    *reinterpret_cast<u32x4*>(xs + row * kXStride + col * 8) = v;
-  }
-}
+// Element i of a lane's 32 x 32 accumulator is token row 8 (i / 4) + 4 (lane / 32) + i % 4 and
+// expert column lane % 32 of the block.
+__device__ __forceinline__ int acc_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
 
 template <int KMAX>
 __device__ __forceinline__ void list_insert(float v, int e, float* lv, int* li) {
@@ -99,7 +78,7 @@ __device__ void topk_and_scores(float* lg, float* zt, int64_t t0, int64_t T, int
                                 int score_fn, int32_t* __restrict__ topk_ids,
                                 float* __restrict__ topk_w, float* __restrict__ prob_partial,
                                 float* __restrict__ z_partial) {
-  static_assert(LPT == 4 || LPT == 8 || LPT == 16, "lanes per token");
+  static_assert(LPT == 2 || LPT == 4 || LPT == 8 || LPT == 16, "lanes per token");
   const int ldl = E + 1;
   const int tt = threadIdx.x / LPT;   // token within the block
   const int sub = threadIdx.x % LPT;  // which of the LPT expert strides this lane scans
@@ -209,92 +188,264 @@ __device__ __forceinline__ void write_logits_out(const float* lg, int64_t t0, in
   }
 }
 
-// Fused: all chunks and all experts for 64 tokens, then top-k in the same block.
-template <int EPW, int KMAX>
-__global__ __launch_bounds__(256) void router_fused_kernel(
+// One workgroup's chunk sums on the matrix cores: tokens [t0, t0 + 64), experts
+// [e0, e0 + 32 EBW), chunks [c_lo, c_hi) split into R ranges of whole chunks. Wave = (range r,
+// 32-token half sub, expert block ebl), 128 EBW R threads. Every step stages 64 features of each
+// range (x and router weights, double-buffered in smem: router_stage_bytes) and runs 32 MFMAs
+// per wave from LDS. Range 0 keeps the running sum of its chunk sums, ranges r > 0 their chunk
+// sums (at most 4); then, in range order, each adds its chunk sums to the running sum left in
+// xch (LDS, row pitch xp floats, block (sub, ebl) at rows 32 sub, columns 32 ebl). Returns the
+// complete sum ((c_lo + c_lo+1) + ...) to the waves of range R - 1 (others: partial values),
+// every element also left in xch, which may alias the stage buffers (smem): it is touched only
+// after the last step's barrier.
+template <int EBW, int R>
+struct RouterBlock {
+  static constexpr int NT = 128 * EBW * R;
+  static constexpr int Ew = 32 * EBW;
+  static constexpr int XP = 4 / EBW;  // x pieces (16 bytes) per thread per step: 512 R / NT
+  static constexpr int WP = 16;       // weights per thread per step: 64 Ew R / NT
+  static constexpr int kRS = kXStageBytes + 64 * Ew * 4;  // one range's stage
+  static constexpr int PMAX = 4;
+  static_assert(XP >= 1 && XP * NT == 512 * R && WP * NT == 64 * Ew * R, "stage split");
+  static constexpr size_t stage_bytes() { return (size_t)2 * R * kRS; }
+
+  __device__ __forceinline__ static floatx16 run(const uint16_t* __restrict__ x, int64_t ld_x,
+                                 const float* __restrict__ wt, int64_t T, int d, int E,
+                                 int64_t t0, int e0, int c_lo, int c_hi, unsigned char* smem,
+                                 float* xch, int xp) {
+    const int lane = lane_id(), wave = wave_id(), h = lane >> 5;
+    const int r = wave % R, ob = wave / R, sub = ob & 1, ebl = ob >> 1;
+    const int nch = c_hi - c_lo;
+    auto F = [&](int rr) { return (c_lo + rr * nch / R) * kRouterChunk; };
+    auto FE = [&](int rr) {
+      const int e = (c_lo + (rr + 1) * nch / R) * kRouterChunk;
+      return e < d ? e : d;
+    };
+    const int n_stages = (FE(0) - F(0) + kStageF - 1) / kStageF;  // range 0 is the longest
+    struct Regs {
+      u32x4 x[XP];
+      float w[WP];
+    };
+    // Stage st (clamped to the last stage: a load past the end re-reads it, unused) -> regs.
+    auto load_stage = [&](int st, Regs& g) {
+      st = st < n_stages ? st : n_stages - 1;
+#pragma unroll
+      for (int i = 0; i < XP; ++i) {
+        const int p = i * NT + threadIdx.x;  // [range][row][col]
+        const int rr = p / 512, row = (p / 8) % 64, col = p % 8;
+        const int64_t t = t0 + row < T ? t0 + row : T - 1;
+        int f = F(rr) + st * kStageF + 8 * col;
+        f = f < FE(rr) ? f : FE(rr) - 8;
+        g.x[i] = *reinterpret_cast<const u32x4*>(x + t * ld_x + f);
+      }
+#pragma unroll
+      for (int i = 0; i < WP; ++i) {
+        const int p = i * NT + threadIdx.x;  // [range][feature][expert]
+        const int rr = p / (64 * Ew), rem = p % (64 * Ew);
+        int f = F(rr) + st * kStageF + rem / Ew;
+        f = f < FE(rr) ? f : FE(rr) - 1;
+        const int e = e0 + rem % Ew < E ? e0 + rem % Ew : E - 1;
+        g.w[i] = wt[(int64_t)f * E + e];
+      }
+    };
+    auto store_stage = [&](int buf, const Regs& g) {
+#pragma unroll
+      for (int i = 0; i < XP; ++i) {
+        const int p = i * NT + threadIdx.x;
+        const int rr = p / 512, row = (p / 8) % 64, col = p % 8;
+        *reinterpret_cast<u32x4*>(smem + (buf * R + rr) * kRS + (row * kXPitch + col * 8) * 2) =
+            g.x[i];
+      }
+#pragma unroll
+      for (int i = 0; i < WP; ++i) {
+        const int p = i * NT + threadIdx.x;
+        const int rr = p / (64 * Ew), rem = p % (64 * Ew), f = rem / Ew, e = rem % Ew;
+        float* ws = reinterpret_cast<float*>(smem + (buf * R + rr) * kRS + kXStageBytes);
+        ws[(((f >> 3) * 2 + (f & 1)) * Ew + e) * 4 + ((f & 7) >> 1)] = g.w[i];
+      }
+    };
+    const uint32_t sel = h ? 0x07060C0Cu : 0x05040C0Cu;
+    auto compute = [&](int buf, int nq, floatx16 chain) {
+      const unsigned char* base = smem + (buf * R + r) * kRS;
+      const unsigned char* xs = base + ((sub * 32 + (lane & 31)) * kXPitch) * 2;
+      const float* ws =
+          reinterpret_cast<const float*>(base + kXStageBytes) + (ebl * 32 + (lane & 31)) * 4;
+      auto group = [&](int q, floatx16 c) {
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(xs + q * 16);
+        const floatx4 wv = *reinterpret_cast<const floatx4*>(ws + (q * 2 + h) * Ew * 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a = __builtin_bit_cast(float, __builtin_amdgcn_perm(xv[j], 0u, sel));
+          c = __builtin_amdgcn_mfma_f32_32x32x2f32(a, wv[j], c, 0, 0, 0);
+        }
+        return c;
+      };
+      if (nq == 8) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) chain = group(q, chain);
+      } else {
+        for (int q = 0; q < nq; ++q) chain = group(q, chain);
+      }
+      return chain;
+    };
+    auto groups_at = [&](int st) {  // real 8-feature groups of this wave's range in stage st
+      const int left = FE(r) - (F(r) + st * kStageF);
+      return left <= 0 ? 0 : (left >= kStageF ? 8 : left / 8);
+    };
+
+    // Two stages of loads in flight: stage st + 1 lands while stage st is computed, stage st + 2
+    // is issued meanwhile. One loop iteration is one chunk (stages 2 i, 2 i + 1).
+    floatx16 sum = {};
+    floatx16 part[PMAX];
+    Regs ga, gb;
+    load_stage(0, ga);
+    load_stage(1, gb);
+    store_stage(0, ga);
+    __syncthreads();
+    auto chunk = [&](int i) {  // stages 2 i (buffer 0) and 2 i + 1 (buffer 1)
+      const int st = 2 * i;
+      load_stage(st + 2, ga);
+      floatx16 chain = compute(0, groups_at(st), floatx16{});
+      store_stage(1, gb);  // stage st + 1 (a re-read of stage st past the end: unused)
+      __syncthreads();
+      load_stage(st + 3, gb);
+      chain = compute(1, groups_at(st + 1), chain);
+      store_stage(0, ga);  // stage st + 2
+      __syncthreads();
+      return chain;
+    };
+    const int n_iter = (n_stages + 1) / 2;
+    if (R == 1) {
+      for (int i = 0; i < n_iter; ++i) {
+        const floatx16 chain = chunk(i);
+        sum = i == 0 ? chain : sum + chain;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < PMAX; ++i) {
+        if (i < n_iter) {
+          const floatx16 chain = chunk(i);
+          if (groups_at(2 * i) > 0) {  // this range has chunk i
+            if (r == 0) sum = i == 0 ? chain : sum + chain;
+            else part[i] = chain;
+          }
+        }
+      }
+    }
+    // In range order: range 0 leaves its running sum in xch, range r adds its chunk sums.
+    float* xb = xch + (sub * 32) * xp + ebl * 32 + (lane & 31);
+    const int r_chunks = (FE(r) - F(r) + kRouterChunk - 1) / kRouterChunk;
+#pragma unroll
+    for (int step_r = 0; step_r < R; ++step_r) {
+      if (r == step_r) {
+        if (step_r > 0) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sum[i] = xb[acc_row(i, lane) * xp];
+#pragma unroll
+          for (int p = 0; p < PMAX; ++p)
+            if (p < r_chunks) sum = sum + part[p];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xb[acc_row(i, lane) * xp] = sum[i];
+      }
+      __syncthreads();
+    }
+    return sum;
+  }
+};
+
+// Fused (no workspace): 64 tokens x all E experts per block, 2 EB R waves; the logits (+ bias) go
+// to the LDS tile lg[64][E+1], then top-k in the same block, 2 EB R lanes per token.
+template <int EB, int R, int KMAX>
+__global__ __launch_bounds__(128 * EB * R) void router_mfma_kernel(
     const uint16_t* __restrict__ x, int64_t ld_x, const float* __restrict__ wt,
     const float* __restrict__ bias, int64_t T, int d, int E, int k, int score_fn,
     float* __restrict__ logits, int32_t* __restrict__ topk_ids, float* __restrict__ topk_w,
     float* __restrict__ prob_partial, float* __restrict__ z_partial) {
+  using RB = RouterBlock<EB, R>;
   extern __shared__ __align__(16) unsigned char smem[];
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-  float* lg = reinterpret_cast<float*>(smem);
-  float* zt = reinterpret_cast<float*>(smem + zt_offset(E));
+  float* lg = reinterpret_cast<float*>(smem + RB::stage_bytes());
+  float* zt = reinterpret_cast<float*>(smem + RB::stage_bytes() + zt_offset(E));
   const int64_t t0 = (int64_t)blockIdx.x * kRouteBlock;
-  const int lane = lane_id();
-  const int e0 = wave_id() * EPW;
-  const int ws = e0 < E - EPW ? e0 : E - EPW;  // window start kept inside [0, E)
-
-  float total[EPW];
-#pragma unroll
-  for (int e = 0; e < EPW; ++e) total[e] = 0.f;
-  for (int c0 = 0; c0 < d; c0 += kRouterChunk) {
-    const int clen = d - c0 < kRouterChunk ? d - c0 : kRouterChunk;
-    __syncthreads();
-    stage_x(x, ld_x, T, t0, c0, clen, xs);
-    __syncthreads();
-    float acc[EPW];
-#pragma unroll
-    for (int e = 0; e < EPW; ++e) acc[e] = 0.f;
-    chunk_fma<EPW>(xs + lane * kXStride, wt, E, ws, c0, clen, acc);
-#pragma unroll
-    for (int e = 0; e < EPW; ++e) total[e] = c0 == 0 ? acc[e] : total[e] + acc[e];
-  }
-  if (bias) {
-#pragma unroll
-    for (int e = 0; e < EPW; ++e) total[e] = total[e] + bias[ws + e];
-  }
-  __syncthreads();  // the x tile is dead; lg aliases it
-#pragma unroll
-  for (int i = 0; i < EPW; ++i) {
-    int e = ws + i;
-    if (e >= e0 && e < E) lg[lane * (E + 1) + e] = total[i];
+  const int nchunk = (d + kRouterChunk - 1) / kRouterChunk;
+  constexpr int xp = 32 * EB + 1;
+  const float* xch = reinterpret_cast<const float*>(smem);  // [64][32 EB + 1] over the stages
+  RB::run(x, ld_x, wt, T, d, E, t0, 0, 0, nchunk, smem, reinterpret_cast<float*>(smem), xp);
+  for (int idx = threadIdx.x; idx < kRouteBlock * E; idx += blockDim.x) {
+    const int row = idx / E, e = idx - row * E;
+    float v = xch[row * xp + e];
+    if (bias) v = v + bias[e];
+    lg[row * (E + 1) + e] = v;
   }
   __syncthreads();
   if (logits) write_logits_out(lg, t0, T, E, logits);
-  topk_and_scores<KMAX>(lg, zt, t0, T, E, k, score_fn, topk_ids, topk_w, prob_partial,
-                        z_partial);
+  topk_and_scores<KMAX, 2 * EB * R>(lg, zt, t0, T, E, k, score_fn, topk_ids, topk_w,
+                                    prob_partial, z_partial);
 }
 
-// Split: one chunk of one expert group for 64 tokens -> partials[chunk][e][t]. Expert-major
-// planes make every store of a wave 64 consecutive floats (token-major rows of E floats would
-// scatter each store over 64 rows, which cost more than the FMAs).
-template <int EPW>
-__global__ __launch_bounds__(256) void router_partial_kernel(
-    const uint16_t* __restrict__ x, int64_t ld_x, const float* __restrict__ wt, int64_t T, int d,
-    int E, float* __restrict__ partials) {
-  __shared__ __align__(16) uint16_t xs[kRouteBlock * kXStride];
+inline size_t router_mfma_lds_bytes(int EB, int R, int E) {
+  return (size_t)2 * R * (kXStageBytes + 64 * 32 * EB * 4) + router_lds_bytes(E);
+}
+
+// Logits: one 64-token block x one 32-expert block (blockIdx.y) per workgroup, 2 R waves; the
+// complete logits (+ bias) go to out[t][e] (token-major), for the top-k kernel.
+template <int R>
+__global__ __launch_bounds__(128 * R) void router_logits_kernel(
+    const uint16_t* __restrict__ x, int64_t ld_x, const float* __restrict__ wt,
+    const float* __restrict__ bias, int64_t T, int d, int E, float* __restrict__ out) {
+  using RB = RouterBlock<1, R>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* xch = reinterpret_cast<float*>(smem);  // [64][33] over the stages
   const int64_t t0 = (int64_t)blockIdx.x * kRouteBlock;
-  const int c0 = blockIdx.y * kRouterChunk;
-  const int clen = d - c0 < kRouterChunk ? d - c0 : kRouterChunk;
-  const int lane = lane_id();
-  const int e0 = (blockIdx.z * 4 + wave_id()) * EPW;
-  const int ws = e0 < E - EPW ? e0 : E - EPW;
-  stage_x(x, ld_x, T, t0, c0, clen, xs);
-  __syncthreads();
-  float acc[EPW];
+  const int e0 = blockIdx.y * 32;
+  const int nchunk = (d + kRouterChunk - 1) / kRouterChunk;
+  const floatx16 sum = RB::run(x, ld_x, wt, T, d, E, t0, e0, 0, nchunk, smem, xch, 33);
+  const int lane = lane_id(), wave = wave_id();
+  const int e = e0 + (lane & 31);
+  if (wave % R == R - 1 && e < E) {
+    const int sub = wave / R;
+    const float bv = bias ? bias[e] : 0.f;
 #pragma unroll
-  for (int e = 0; e < EPW; ++e) acc[e] = 0.f;
-  chunk_fma<EPW>(xs + lane * kXStride, wt, E, ws, c0, clen, acc);
-  const int64_t t = t0 + lane;
-  if (t < T) {
-    float* out = partials + (int64_t)blockIdx.y * E * T + t;
-#pragma unroll
-    for (int i = 0; i < EPW; ++i) {
-      int e = ws + i;
-      if (e >= e0 && e < E) out[(int64_t)e * T] = acc[i];
+    for (int i = 0; i < 16; ++i) {
+      const int64_t t = t0 + sub * 32 + acc_row(i, lane);
+      if (t < T) out[t * E + e] = bias ? sum[i] + bv : sum[i];
     }
   }
 }
 
-// Sums the nchunk partial planes ([e][t]) of the split router into plane 0, in place, in the
+inline size_t router_logits_lds_bytes(int R) { return (size_t)2 * R * (kXStageBytes + 64 * 32 * 4); }
+
+// Split: the chunk sum c_j (blockIdx.y = j) of a 64-token x 32-expert block (blockIdx.z) ->
+// partials[j][t][e], token-major (a wave's store covers 32 consecutive experts of a token).
+__global__ __launch_bounds__(128) void router_mfma_partial_kernel(
+    const uint16_t* __restrict__ x, int64_t ld_x, const float* __restrict__ wt, int64_t T, int d,
+    int E, float* __restrict__ partials) {
+  using RB = RouterBlock<1, 1>;
+  __shared__ __align__(16) unsigned char smem[RB::stage_bytes()];
+  float* xch = reinterpret_cast<float*>(smem);
+  const int64_t t0 = (int64_t)blockIdx.x * kRouteBlock;
+  const int c = blockIdx.y, e0 = blockIdx.z * 32;
+  const floatx16 sum = RB::run(x, ld_x, wt, T, d, E, t0, e0, c, c + 1, smem, xch, 33);
+  const int lane = lane_id(), sub = wave_id();
+  const int e = e0 + (lane & 31);
+  if (e < E) {
+    float* out = partials + (int64_t)c * T * E + e;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t t = t0 + sub * 32 + acc_row(i, lane);
+      if (t < T) out[t * E] = sum[i];
+    }
+  }
+}
+
+// Sums the nchunk partial planes ([t][e]) of the split router into plane 0, in place, in the
 // fixed order ((p0 + p1) + p2) + ... then + bias[e]: four consecutive values per thread, the
 // planes' loads issued together. This keeps the plane reduction off the top-k kernel, whose grid
 // has one block per 64 tokens and so cannot hide the loads' latency when T is small.
 __global__ __launch_bounds__(256) void router_sum_planes_kernel(float* __restrict__ partials,
                                                                  int nchunk,
                                                                  const float* __restrict__ bias,
-                                                                 int64_t n4, int64_t T) {
+                                                                 int64_t n4, int E) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n4) return;
   const int64_t plane4 = n4;  // plane size in float4 units
@@ -316,18 +467,18 @@ __global__ __launch_bounds__(256) void router_sum_planes_kernel(float* __restric
   }
   if (bias) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = v[j] + bias[(i * 4 + j) / T];
+    for (int j = 0; j < 4; ++j) v[j] = v[j] + bias[(i * 4 + j) % E];
   }
   p[0] = v;
 }
 
-// Sum nchunk partial planes in ascending order (+ bias), then top-k. Element (t, e) of a plane
-// sits at t + e T (expert-major, the split router's planes) or t E + e (token-major: caller-
-// supplied logits, with nchunk = 1 and no bias); the tile loads walk the contiguous index.
+// Sum nchunk partial planes ([t][e], token-major) in ascending order (+ bias), then top-k; with
+// nchunk = 1 and no bias the plane is caller-supplied logits. The tile loads walk the contiguous
+// index.
 template <int KMAX>
 __global__ __launch_bounds__(1024) void router_topk_kernel(
-    const float* __restrict__ partials, int nchunk, bool expert_major,
-    const float* __restrict__ bias, int64_t T, int E, int k, int score_fn,
+    const float* __restrict__ partials, int nchunk, const float* __restrict__ bias, int64_t T,
+    int E, int k, int score_fn,
     float* __restrict__ logits, int32_t* __restrict__ topk_ids, float* __restrict__ topk_w,
     float* __restrict__ prob_partial, float* __restrict__ z_partial) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -338,11 +489,9 @@ __global__ __launch_bounds__(1024) void router_topk_kernel(
   // not a chain of dependent memory round trips.
   const int64_t plane = T * E;
   // Tile index idx -> (token row r, expert e), contiguous in memory along idx.
-  // (Plain selects, not assignments through references: the latter made the compiler keep r
-  // and e in scratch memory with a dynamic index.)
-  auto row_of = [&](int idx) { return expert_major ? idx % kRouteBlock : idx / E; };
-  auto col_of = [&](int idx) { return expert_major ? idx / kRouteBlock : idx % E; };
-  auto at = [&](int64_t t, int e) { return expert_major ? t + e * T : t * E + e; };
+  auto row_of = [&](int idx) { return idx / E; };
+  auto col_of = [&](int idx) { return idx % E; };
+  auto at = [&](int64_t t, int e) { return t * E + e; };
   if (nchunk == 1) {
     // One plane (the split router's planes are summed by router_sum_planes_kernel): eight loads
     // per thread go out together, so a block does not wait on one round trip per element.
@@ -396,15 +545,25 @@ __global__ __launch_bounds__(1024) void router_topk_kernel(
                         z_partial);
 }
 
-int experts_per_wave(int E) {
-  int need = (E + 3) / 4, epw = 1;
-  while (epw < need) epw <<= 1;
-  return epw;
-}
-
 int kmax_for(int k) { return k <= 2 ? 2 : (k <= 4 ? 4 : 8); }
 
-// NT_MOE_ROUTER_MODE=fused|split overrides the size heuristic (for tuning runs).
+// Expert blocks of 32 (a power of two: the fused kernel's waves per token row set the top-k's
+// lanes per token).
+int expert_blocks(int E) {
+  int eb = 1;
+  while (eb * 32 < E) eb <<= 1;
+  return eb;
+}
+
+// Feature ranges per output block of the fused kernel: two when there is one expert block and
+// at most 8 chunks (the second range keeps up to 4 chunk sums in registers), else one.
+int router_ranges(int d, int E) {
+  const int nchunk = ceil_div(d, kRouterChunk);
+  return expert_blocks(E) == 1 && nchunk >= 2 && nchunk <= 8 ? 2 : 1;
+}
+
+// NT_MOE_ROUTER_MODE=fused|split overrides the size heuristic (for tuning runs): fused = no
+// chunk planes, split = chunk planes.
 int router_mode_override() {
   static int mode = [] {
     const char* s = getenv("NT_MOE_ROUTER_MODE");
@@ -417,125 +576,150 @@ int router_mode_override() {
 }
 
 template <int KMAX>
-hipError_t launch_topk_k(const float* partials, int nchunk, bool expert_major, const float* bias,
-                         int64_t T, int E, int k, int score_fn, float* logits, int32_t* ids,
-                         float* w, float* pp, float* zp, hipStream_t stream) {
+hipError_t launch_topk_k(const float* partials, int nchunk, const float* bias, int64_t T, int E,
+                         int k, int score_fn, float* logits, int32_t* ids, float* w, float* pp,
+                         float* zp, hipStream_t stream) {
   dim3 grid(ceil_div(T, kRouteBlock));
   hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(router_topk_kernel<KMAX>),
                                      router_lds_bytes(E));
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL((router_topk_kernel<KMAX>), grid, dim3(1024), router_lds_bytes(E), stream,
-                     partials, nchunk, expert_major, bias, T, E, k, score_fn, logits, ids, w, pp,
-                     zp);
+                     partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp);
   return hipGetLastError();
 }
 
-hipError_t launch_topk_any(const float* partials, int nchunk, bool expert_major,
-                           const float* bias, int64_t T, int E, int k, int score_fn,
-                           float* logits, int32_t* ids, float* w, float* pp, float* zp,
-                           hipStream_t stream) {
+hipError_t launch_topk_any(const float* partials, int nchunk, const float* bias, int64_t T,
+                           int E, int k, int score_fn, float* logits, int32_t* ids, float* w,
+                           float* pp, float* zp, hipStream_t stream) {
   switch (kmax_for(k)) {
-    case 2: return launch_topk_k<2>(partials, nchunk, expert_major, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
-    case 4: return launch_topk_k<4>(partials, nchunk, expert_major, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
-    default: return launch_topk_k<8>(partials, nchunk, expert_major, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    case 2: return launch_topk_k<2>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    case 4: return launch_topk_k<4>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    default: return launch_topk_k<8>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
   }
 }
 
-template <int EPW, int KMAX>
-hipError_t launch_fused_k(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
-                          int64_t T, int d, int E, int k, int score_fn, float* logits,
-                          int32_t* ids, float* w, float* pp, float* zp, hipStream_t stream) {
-  dim3 grid(ceil_div(T, kRouteBlock));
-  hipError_t err = allow_dynamic_lds(
-      reinterpret_cast<const void*>(router_fused_kernel<EPW, KMAX>), router_lds_bytes(E));
+template <int EB, int R, int KMAX>
+hipError_t launch_mfma_k(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
+                         int64_t T, int d, int E, int k, int score_fn, float* logits,
+                         int32_t* ids, float* w, float* pp, float* zp, hipStream_t stream) {
+  auto kern = router_mfma_kernel<EB, R, KMAX>;
+  const size_t lds = router_mfma_lds_bytes(EB, R, E);
+  hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL((router_fused_kernel<EPW, KMAX>), grid, dim3(256), router_lds_bytes(E),
-                     stream, x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp);
+  hipLaunchKernelGGL(kern, dim3(ceil_div(T, kRouteBlock)), dim3(128 * EB * R), lds, stream, x,
+                     ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp);
   return hipGetLastError();
 }
 
-template <int EPW>
-hipError_t launch_fused_e(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
-                          int64_t T, int d, int E, int k, int score_fn, float* logits,
-                          int32_t* ids, float* w, float* pp, float* zp, hipStream_t stream) {
+template <int EB, int R>
+hipError_t launch_mfma_r(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
+                         int64_t T, int d, int E, int k, int score_fn, float* logits,
+                         int32_t* ids, float* w, float* pp, float* zp, hipStream_t stream) {
   switch (kmax_for(k)) {
-    case 2: return launch_fused_k<EPW, 2>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
-    case 4: return launch_fused_k<EPW, 4>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
-    default: return launch_fused_k<EPW, 8>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    case 2: return launch_mfma_k<EB, R, 2>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    case 4: return launch_mfma_k<EB, R, 4>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    default: return launch_mfma_k<EB, R, 8>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
   }
 }
 
-template <int EPW>
-hipError_t launch_partial_e(const uint16_t* x, int64_t ld_x, const float* wt, int64_t T, int d,
-                            int E, float* partials, hipStream_t stream) {
-  dim3 grid(ceil_div(T, kRouteBlock), ceil_div(d, kRouterChunk), ceil_div(E, 4 * EPW));
-  hipLaunchKernelGGL((router_partial_kernel<EPW>), grid, dim3(256), 0, stream, x, ld_x, wt, T,
-                     d, E, partials);
-  return hipGetLastError();
+// Feature ranges of the logits kernel: up to 4, each at most 4 chunks (so d <= 2048).
+int logit_ranges(int d) {
+  const int nchunk = ceil_div(d, kRouterChunk);
+  return nchunk >= 4 ? 4 : (nchunk >= 2 ? 2 : 1);
+}
+
+enum RouterPath { kFused = 0, kLogits = 1, kPlanes = 2 };
+
+// Path for this shape. Fused (top-k in the block, no workspace) when every CU gets a 64-token
+// block and E <= 128; else the logits kernel (one workgroup per 64 tokens x 32 experts, up to
+// 16 chunks) when that gives two waves per CU; else chunk planes (small T), whose planes are
+// capped at 512 MB. Measured at T = 16384 / 8192 / 32768 (E = 32 / 128 / 64): fused 28 us,
+// logits + top-k 94 us (fused: 115, half the CUs idle), fused 180 us.
+int router_path(int64_t T, int d, int E) {
+  const int mode = router_mode_override();
+  const int nchunk = ceil_div(d, kRouterChunk);
+  const int64_t blocks = ceil_div(T, kRouteBlock);
+  const int64_t logit_waves = blocks * (int64_t)ceil_div(E, 32) * 2 * logit_ranges(d);
+  const int64_t plane_bytes = (int64_t)nchunk * T * E * (int64_t)sizeof(float);
+  if (mode == 2) return kPlanes;
+  if (mode == 1) return E <= 128 ? kFused : kLogits;
+  if (E <= 128 && blocks >= num_cus()) return kFused;
+  if (nchunk <= 16 && logit_waves >= 2LL * num_cus()) return kLogits;
+  if (plane_bytes <= (512LL << 20)) return kPlanes;
+  return nchunk <= 16 ? kLogits : kFused;
 }
 
 }  // namespace
 
-// Chunks of the split variant when it is used for this shape, else 0 (fused). The fused kernel
-// has one 4-wave block per 64 tokens, too few waves per CU to hide its scalar weight loads until
-// there are several blocks per CU (measured: at T = 32768, d = 2048, E = 64 the split variant is
-// 24 % faster); the split variant's partial planes are capped at 512 MB of workspace.
-int router_split_chunks(int64_t T, int d, int E) {
-  int mode = router_mode_override();
-  if (mode == 1) return 0;
-  const int nchunk = ceil_div(d, kRouterChunk);
-  const int64_t blocks = ceil_div(T, kRouteBlock);
-  const int64_t plane_bytes = (int64_t)nchunk * T * E * (int64_t)sizeof(float);
-  if (mode == 2 || (blocks < 8LL * num_cus() && plane_bytes <= (512LL << 20))) return nchunk;
-  return 0;
+// Workspace the router uses for this shape: the chunk planes, one T x E logits plane, or none.
+size_t router_workspace_need(int64_t T, int d, int E) {
+  const int path = router_path(T, d, E);
+  const size_t plane = (size_t)T * (size_t)E * sizeof(float);
+  return path == kPlanes ? plane * ceil_div(d, kRouterChunk) : (path == kLogits ? plane : 0);
 }
 
+// Runs the path for the shape when its buffers are there; without enough workspace the fused
+// kernel (up to 128 experts).
 hipError_t launch_router(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
                          int64_t T, int d, int E, int k, int score_fn, float* logits,
                          int32_t* topk_ids, float* topk_w, float* prob_partial,
-                         float* z_partial, float* partials, bool split, hipStream_t stream) {
-  int epw = experts_per_wave(E);
-  if (!split) {
-    switch (epw) {
-#define NT_FUSED(N) case N: return launch_fused_e<N>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, topk_ids, topk_w, prob_partial, z_partial, stream);
-      NT_FUSED(1) NT_FUSED(2) NT_FUSED(4) NT_FUSED(8) NT_FUSED(16) NT_FUSED(32) NT_FUSED(64)
-#undef NT_FUSED
-      default: return hipErrorInvalidValue;
-    }
-  }
-  // Split: smaller expert groups give more blocks when T is small (aim for >= 4 per CU: each
-  // block is a single wave whose weight loads nothing else on the CU would hide).
-  int epw_split = epw < 16 ? epw : 16;
-  const int64_t row_chunks = (int64_t)ceil_div(T, kRouteBlock) * ceil_div(d, kRouterChunk);
-  while (epw_split > 1 && row_chunks * ceil_div(E, 4 * epw_split) < 4LL * num_cus()) epw_split /= 2;
-  hipError_t err;
-  switch (epw_split) {
-    case 1: err = launch_partial_e<1>(x, ld_x, wt, T, d, E, partials, stream); break;
-    case 2: err = launch_partial_e<2>(x, ld_x, wt, T, d, E, partials, stream); break;
-    case 4: err = launch_partial_e<4>(x, ld_x, wt, T, d, E, partials, stream); break;
-    case 8: err = launch_partial_e<8>(x, ld_x, wt, T, d, E, partials, stream); break;
-    default: err = launch_partial_e<16>(x, ld_x, wt, T, d, E, partials, stream); break;
-  }
-  if (err != hipSuccess) return err;
+                         float* z_partial, float* workspace, size_t workspace_bytes,
+                         hipStream_t stream) {
   const int nchunk = ceil_div(d, kRouterChunk);
-  if (E % 4 == 0) {
-    const int64_t n4 = T * E / 4;
-    router_sum_planes_kernel<<<dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream>>>(
-        partials, nchunk, bias, n4, T);
+  const int path = router_path(T, d, E);
+  const size_t plane = (size_t)T * (size_t)E * sizeof(float);
+  hipError_t err;
+  if (path == kPlanes && workspace && workspace_bytes >= plane * nchunk) {
+    hipLaunchKernelGGL(router_mfma_partial_kernel,
+                       dim3((unsigned)ceil_div(T, kRouteBlock), (unsigned)nchunk,
+                            (unsigned)ceil_div(E, 32)),
+                       dim3(128), 0, stream, x, ld_x, wt, T, d, E, workspace);
     err = hipGetLastError();
     if (err != hipSuccess) return err;
-    return launch_topk_any(partials, 1, true, nullptr, T, E, k, score_fn, logits, topk_ids,
-                           topk_w, prob_partial, z_partial, stream);
+    if (E % 4 == 0) {
+      const int64_t n4 = T * E / 4;
+      router_sum_planes_kernel<<<dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream>>>(
+          workspace, nchunk, bias, n4, E);
+      err = hipGetLastError();
+      if (err != hipSuccess) return err;
+      return launch_topk_any(workspace, 1, nullptr, T, E, k, score_fn, logits, topk_ids, topk_w,
+                             prob_partial, z_partial, stream);
+    }
+    return launch_topk_any(workspace, nchunk, bias, T, E, k, score_fn, logits, topk_ids, topk_w,
+                           prob_partial, z_partial, stream);
   }
-  return launch_topk_any(partials, nchunk, true, bias, T, E, k, score_fn, logits, topk_ids,
-                         topk_w, prob_partial, z_partial, stream);
+  float* lbuf = logits ? logits : (workspace && workspace_bytes >= plane ? workspace : nullptr);
+  if ((path != kFused || E > 128) && lbuf && nchunk <= 16) {
+    const int ranges = logit_ranges(d);
+    const dim3 grid((unsigned)ceil_div(T, kRouteBlock), (unsigned)ceil_div(E, 32));
+#define NT_LOGITS(R)                                                                       \
+  if (ranges == R) {                                                                       \
+    auto kern = router_logits_kernel<R>;                                                   \
+    err = allow_dynamic_lds(reinterpret_cast<const void*>(kern), router_logits_lds_bytes(R)); \
+    if (err != hipSuccess) return err;                                                     \
+    hipLaunchKernelGGL(kern, grid, dim3(128 * R), router_logits_lds_bytes(R), stream, x, ld_x, \
+                       wt, bias, T, d, E, lbuf);                                           \
+  }
+    NT_LOGITS(1) NT_LOGITS(2) NT_LOGITS(4)
+#undef NT_LOGITS
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    return launch_topk_any(lbuf, 1, nullptr, T, E, k, score_fn, nullptr, topk_ids, topk_w,
+                           prob_partial, z_partial, stream);
+  }
+  const int eb = expert_blocks(E), ranges = router_ranges(d, E);
+#define NT_MFMA(EB, R) \
+  if (eb == EB && ranges == R) return launch_mfma_r<EB, R>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, topk_ids, topk_w, prob_partial, z_partial, stream);
+  NT_MFMA(1, 1) NT_MFMA(1, 2) NT_MFMA(2, 1) NT_MFMA(4, 1)
+#undef NT_MFMA
+  return hipErrorInvalidValue;  // more than 128 experts need the workspace
 }
 
 hipError_t launch_topk_from_logits(const float* logits, int64_t T, int E, int k,
                                    int score_fn, int32_t* topk_ids, float* topk_w,
                                    float* prob_partial, float* z_partial, hipStream_t stream) {
-  return launch_topk_any(logits, 1, false, nullptr, T, E, k, score_fn, nullptr, topk_ids,
-                         topk_w, prob_partial, z_partial, stream);
+  return launch_topk_any(logits, 1, nullptr, T, E, k, score_fn, nullptr, topk_ids, topk_w,
+                         prob_partial, z_partial, stream);
 }
 
 }  // namespace ntmoe
