@@ -559,7 +559,8 @@ int expert_blocks(int E) {
 // at most 8 chunks (the second range keeps up to 4 chunk sums in registers), else one.
 int router_ranges(int d, int E) {
   const int nchunk = ceil_div(d, kRouterChunk);
-  return expert_blocks(E) == 1 && nchunk >= 2 && nchunk <= 8 ? 2 : 1;
+  if (expert_blocks(E) != 1 || nchunk < 2) return 1;
+  return nchunk >= 4 && nchunk <= 16 ? 4 : (nchunk <= 8 ? 2 : 1);
 }
 
 // NT_MOE_ROUTER_MODE=fused|split overrides the size heuristic (for tuning runs): fused = no
@@ -710,7 +711,7 @@ hipError_t launch_router(const uint16_t* x, int64_t ld_x, const float* wt, const
   const int eb = expert_blocks(E), ranges = router_ranges(d, E);
 #define NT_MFMA(EB, R) \
   if (eb == EB && ranges == R) return launch_mfma_r<EB, R>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, topk_ids, topk_w, prob_partial, z_partial, stream);
-  NT_MFMA(1, 1) NT_MFMA(1, 2) NT_MFMA(2, 1) NT_MFMA(4, 1)
+  NT_MFMA(1, 1) NT_MFMA(1, 2) NT_MFMA(1, 4) NT_MFMA(2, 1) NT_MFMA(4, 1)
 #undef NT_MFMA
   return hipErrorInvalidValue;  // more than 128 experts need the workspace
 }
