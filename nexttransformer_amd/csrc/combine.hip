@@ -20,14 +20,14 @@ namespace {
 // vectors (VPC = 2: 1024 bf16 per chunk) so k * VPC vectors are in flight per lane.
 constexpr int VPC = 2;
 
-__global__ __launch_bounds__(256) void combine_kernel(
+__device__ __forceinline__ void combine_rows(
     const uint16_t* __restrict__ y, const int32_t* __restrict__ combine_dest,
     const float* __restrict__ combine_w, int64_t T, int d, int k,
     const uint16_t* __restrict__ shared_y, int64_t ld_shared, uint16_t* __restrict__ out,
-    int64_t ld_out) {
+    int64_t ld_out, int blocks) {
   const int lane = lane_id();
   const int vecs = d >> 3;
-  const int64_t waves = (int64_t)gridDim.x * 4;
+  const int64_t waves = (int64_t)blocks * 4;
   for (int64_t t = (int64_t)blockIdx.x * 4 + wave_id(); t < T; t += waves) {
     int dest = 0;
     float w = 0.f;
@@ -99,15 +99,15 @@ __global__ __launch_bounds__(256) void combine_kernel(
   }
 }
 
-// One workgroup of 1024 threads. Thread (e, p), p < P = 1024 / E (a power of two), sums
-// block partials b = p, p + P, ... of expert e; a fixed-shape tree then combines the P values
-// and the E experts, so the result does not depend on scheduling.
-constexpr int kAuxThreads = 1024;
+// The auxiliary losses, by one 256-thread workgroup. Thread (e, p), p < P = 256 / E rounded
+// down to a power of two, sums block partials b = p, p + P, ... of expert e in order; fixed-shape
+// trees then combine the P values and the E experts, so the result does not depend on timing.
+constexpr int kAuxThreads = 256;
 
-__global__ __launch_bounds__(kAuxThreads) void aux_kernel(
-    const float* __restrict__ prob_partial, const float* __restrict__ z_partial, int nblk,
-    const int32_t* __restrict__ counts, int E, int P, int k, int64_t T, float aux_coeff,
-    float z_coeff, float* __restrict__ aux_out) {
+__device__ void aux_block(const float* __restrict__ prob_partial,
+                          const float* __restrict__ z_partial, int nblk,
+                          const int32_t* __restrict__ counts, int E, int P, int k, int64_t T,
+                          float aux_coeff, float z_coeff, float* __restrict__ aux_out) {
   __shared__ double red[kAuxThreads];
   __shared__ double zred[kAuxThreads];
   const int tid = threadIdx.x;
@@ -148,6 +148,32 @@ __global__ __launch_bounds__(kAuxThreads) void aux_kernel(
   }
 }
 
+struct AuxArgs {
+  const float* prob_partial;
+  const float* z_partial;
+  const int32_t* counts;
+  int nblk, E, P;
+  float aux_coeff, z_coeff;
+  float* aux_out;  // null: no aux workgroup
+};
+
+// The combine grid plus, when aux.aux_out is set, one last workgroup that computes the losses
+// (they depend only on the router's partials and the counts, so they run beside the combine).
+__global__ __launch_bounds__(256) void combine_aux_kernel(
+    const uint16_t* __restrict__ y, const int32_t* __restrict__ combine_dest,
+    const float* __restrict__ combine_w, int64_t T, int d, int k,
+    const uint16_t* __restrict__ shared_y, int64_t ld_shared, uint16_t* __restrict__ out,
+    int64_t ld_out, AuxArgs aux) {
+  const int combine_blocks = (int)gridDim.x - (aux.aux_out ? 1 : 0);
+  if ((int)blockIdx.x == combine_blocks) {
+    aux_block(aux.prob_partial, aux.z_partial, aux.nblk, aux.counts, aux.E, aux.P, k, T,
+              aux.aux_coeff, aux.z_coeff, aux.aux_out);
+    return;
+  }
+  combine_rows(y, combine_dest, combine_w, T, d, k, shared_y, ld_shared, out, ld_out,
+               combine_blocks);
+}
+
 }  // namespace
 
 hipError_t launch_combine_aux(const uint16_t* y, const int32_t* combine_dest,
@@ -156,24 +182,17 @@ hipError_t launch_combine_aux(const uint16_t* y, const int32_t* combine_dest,
                               int64_t ld_out, const float* prob_partial, const float* z_partial,
                               const int32_t* counts, int E, float aux_coeff, float z_coeff,
                               float* aux_out, hipStream_t stream) {
-  hipError_t err = hipSuccess;
-  if (T > 0) {
-    int64_t blocks = (T + 3) / 4;
-    int64_t cap = (int64_t)num_cus() * 32;
-    if (blocks > cap) blocks = cap;
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, y,
-                       combine_dest, combine_w, T, d, k, shared_y, ld_shared, out, ld_out);
-    err = hipGetLastError();
-    if (err != hipSuccess) return err;
-  }
-  if (aux_out) {
-    const int nblk = ceil_div(T, kRouteBlock);
-    int P = 1;
-    while (P * 2 * E <= kAuxThreads) P *= 2;
-    hipLaunchKernelGGL(aux_kernel, dim3(1), dim3(kAuxThreads), 0, stream, prob_partial, z_partial,
-                       nblk, counts, E, P, k, T, aux_coeff, z_coeff, aux_out);
-    err = hipGetLastError();
-  }
+  AuxArgs aux{prob_partial, z_partial, counts, ceil_div(T, kRouteBlock), E, 1, aux_coeff,
+              z_coeff, aux_out};
+  while (aux.P * 2 * E <= kAuxThreads) aux.P *= 2;
+  int64_t blocks = (T + 3) / 4;
+  const int64_t cap = (int64_t)num_cus() * 32;
+  if (blocks > cap) blocks = cap;
+  if (aux_out) ++blocks;
+  if (blocks == 0) return hipSuccess;
+  hipLaunchKernelGGL(combine_aux_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, y,
+                     combine_dest, combine_w, T, d, k, shared_y, ld_shared, out, ld_out, aux);
+  hipError_t err = hipGetLastError();
   return err;
 }
 
