@@ -73,16 +73,20 @@ def test_router_logits_and_topk_bit_exact(case):
     torch.testing.assert_close(zp.cpu().double().sum(), lse2, rtol=1e-5, atol=1e-5)
 
 
-@pytest.mark.parametrize("with_workspace", [False, True], ids=["fused", "split"])
-def test_router_variants_bit_exact_via_abi(with_workspace):
-    """Raw C-ABI call. Without a workspace the router runs fused; with one (and T below the
-    size threshold) it runs split-K. Both follow the same order: identical bits."""
+@pytest.mark.parametrize("T", [512, 4096])
+@pytest.mark.parametrize("E", [32, 64, 128])
+@pytest.mark.parametrize("variant", ["no-buffers", "workspace", "logits-buffer"])
+def test_router_variants_bit_exact_via_abi(variant, E, T):
+    """Raw C-ABI calls that reach each router kernel (on a 256-CU part): with neither workspace
+    nor a logits buffer the fused kernel (top-k in the block; one, two and four expert blocks);
+    with the workspace the chunk planes (T = 512) or the logits kernel + top-k (T = 4096); with
+    only a logits buffer the logits kernel. All follow the same order: identical bits."""
     import ctypes
     from nexttransformer_amd import _native as nat
-    case = Case("variant", 4096, 1024, 32, 4, 64, seed=11)
+    case = Case("variant", T, 1024, E, 4, 64, seed=11)
     cpu, g = gpu_inputs(case)
     lib = nat.load()
-    T, d, E, k = case.T, case.d, case.E, case.k
+    d, k = case.d, case.k
     nblk = (T + 63) // 64
     logits = torch.empty(T, E, device="cuda")
     ids = torch.empty(T, k, device="cuda", dtype=torch.int32)
@@ -91,16 +95,23 @@ def test_router_variants_bit_exact_via_abi(with_workspace):
     zp = torch.empty(nblk, device="cuda")
     need = lib.nt_moe_router_workspace_bytes(T, d, E, k)
     ws = torch.empty(max(need, 1), device="cuda", dtype=torch.uint8)
+    use_ws = variant == "workspace"
+    use_logits = variant != "no-buffers"
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     st = lib.nt_moe_router_fwd(nat.ptr(g["x"]), d, nat.ptr(g["wt"]), None, T, d, E, k, 0,
-                               nat.ptr(logits), nat.ptr(ids), nat.ptr(w), nat.ptr(pp), nat.ptr(zp),
-                               nat.ptr(ws) if with_workspace else None,
-                               need if with_workspace else 0, stream)
+                               nat.ptr(logits) if use_logits else None, nat.ptr(ids), nat.ptr(w),
+                               nat.ptr(pp), nat.ptr(zp), nat.ptr(ws) if use_ws else None,
+                               need if use_ws else 0, stream)
     nat.check(st, "router")
     torch.cuda.synchronize()
     ref_logits = orc.router_logits_fixed(cpu["x"], cpu["router"])
-    assert torch.equal(logits.cpu().view(torch.int32), ref_logits.view(torch.int32))
-    assert torch.equal(ids.cpu(), orc.topk(ref_logits, k)[0])
+    if use_logits:
+        assert torch.equal(logits.cpu().view(torch.int32), ref_logits.view(torch.int32))
+    ref_ids, ref_w = orc.topk(ref_logits, k)
+    assert torch.equal(ids.cpu(), ref_ids)
+    torch.testing.assert_close(w.cpu(), ref_w, rtol=2e-6, atol=2e-7)
+    s_ = orc.full_scores(ref_logits, 0)
+    torch.testing.assert_close(pp.cpu().double().sum(0), s_.sum(0), rtol=1e-5, atol=1e-5)
 
 
 def test_topk_on_reference_logits_and_ties():
