@@ -111,6 +111,30 @@ def test_module_forward_matches_oracle(kw):
     assert aux.item() == pytest.approx(ref["aux"], rel=AUX_RTOL)
 
 
+def test_module_forward_at_t3_expert_cell_shape():
+    """The reference's registered recipe cell moe-T3-L20 (width 1280, 256 experts, top-8, ReLU^2
+    experts of width 320, one shared expert of width 320; megatron_moe.py:23-24,41,51), one
+    layer on 200 tokens, against the oracle."""
+    from pathlib import Path
+    from nexttransformer_amd.moe import MoELayer
+    from nexttransformer_amd.moe_recipe import load_t3_recipe
+    root = Path(__file__).resolve().parents[1]
+    r = load_t3_recipe("moe-T3-L20", root / "tests" / "golden" / "t3_expert_cells.json")
+    assert (r.width, r.routed_experts, r.top_k, r.expert_width, r.activation) == \
+        (1280, 256, 8, 320, "relu2")
+    m = MoELayer(r, 2)
+    _randomise_fc2(m, 3)
+    g = torch.Generator().manual_seed(4)
+    hidden = torch.randn(2, 100, r.width, generator=g).to(torch.bfloat16).cuda()
+    with torch.no_grad():
+        out, aux = m(hidden)
+    torch.cuda.synchronize()
+    ref = _oracle_for(m, hidden)
+    assert rel_l2(out.float().reshape(-1, r.width), ref["out"]) <= BF16_TOL
+    assert torch.equal(m.last_load.cpu(), ref["counts"].long())
+    assert aux.item() == pytest.approx(ref["aux"], rel=AUX_RTOL)
+
+
 @pytest.mark.parametrize("kw", [
     dict(activation="swiglu", width=512, heads=4, expert_width=256, allow_any_expert_width=True),
     dict(width=96, heads=2, expert_width=24),  # ReLU^2 + shared, padded to 128
