@@ -58,15 +58,17 @@ __device__ __forceinline__ int acc_row(int i, int lane) { return 8 * (i >> 2) + 
 
 template <int KMAX>
 __device__ __forceinline__ void list_insert(float v, int e, float* lv, int* li) {
-  if (!rank_before(v, e, lv[KMAX - 1], li[KMAX - 1])) return;
-  lv[KMAX - 1] = v;
-  li[KMAX - 1] = e;
+  // Branch-free: the new entry moves down the list, each slot keeps the better of it and the
+  // carried entry.
 #pragma unroll
-  for (int j = KMAX - 1; j > 0; --j) {
-    if (rank_before(lv[j], li[j], lv[j - 1], li[j - 1])) {
-      float tv = lv[j]; lv[j] = lv[j - 1]; lv[j - 1] = tv;
-      int ti = li[j]; li[j] = li[j - 1]; li[j - 1] = ti;
-    }
+  for (int j = 0; j < KMAX; ++j) {
+    const bool c = rank_before(v, e, lv[j], li[j]);
+    const float tv = lv[j];
+    const int ti = li[j];
+    lv[j] = c ? v : tv;
+    li[j] = c ? e : ti;
+    v = c ? tv : v;
+    e = c ? ti : e;
   }
 }
 
@@ -74,7 +76,7 @@ __device__ __forceinline__ void list_insert(float v, int e, float* lv, int* li) 
 // LDS tile lg[64][E+1]; overwrites lg with the full scores s_te. Called by all 64 * LPT threads
 // of the block: LPT lanes per token, each scanning every LPT-th expert.
 template <int KMAX, int LPT = 4>
-__device__ void topk_and_scores(float* lg, float* zt, int64_t t0, int64_t T, int E, int k,
+__device__ __forceinline__ void topk_and_scores(float* lg, float* zt, int64_t t0, int64_t T, int E, int k,
                                 int score_fn, int32_t* __restrict__ topk_ids,
                                 float* __restrict__ topk_w, float* __restrict__ prob_partial,
                                 float* __restrict__ z_partial) {
@@ -135,10 +137,20 @@ __device__ void topk_and_scores(float* lg, float* zt, int64_t t0, int64_t T, int
   }
 
   // Full scores s_te for the load-balance loss, logsumexp for the z-loss.
+  // The first pass leaves expf(l - top) (softmax) or 1 + expf(-l) (sigmoid) in row, so the
+  // second only scales.
   float part = 0.f, spart = 0.f;
   for (int e = sub; e < E; e += LPT) {
-    part += expf(row[e] - top);
-    if (score_fn == NT_MOE_SCORE_SIGMOID) spart += 1.f / (1.f + expf(-row[e]));
+    const float l = row[e];
+    const float ex = expf(l - top);
+    part += ex;
+    if (score_fn == NT_MOE_SCORE_SIGMOID) {
+      const float den = 1.f + expf(-l);
+      spart += 1.f / den;
+      row[e] = den;
+    } else {
+      row[e] = ex;
+    }
   }
 #pragma unroll
   for (int m = 1; m < LPT; m <<= 1) {
@@ -148,10 +160,10 @@ __device__ void topk_and_scores(float* lg, float* zt, int64_t t0, int64_t T, int
   const float lse = top + logf(part);
   if (score_fn == NT_MOE_SCORE_SOFTMAX) {
     const float inv = 1.f / part;
-    for (int e = sub; e < E; e += LPT) row[e] = expf(row[e] - top) * inv;
+    for (int e = sub; e < E; e += LPT) row[e] = row[e] * inv;
   } else {
     const float inv = 1.f / spart;
-    for (int e = sub; e < E; e += LPT) row[e] = inv / (1.f + expf(-row[e]));
+    for (int e = sub; e < E; e += LPT) row[e] = inv / row[e];
   }
   if (sub == 0) zt[tt] = lse * lse;
   __syncthreads();
