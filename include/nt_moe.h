@@ -135,6 +135,19 @@ int nt_moe_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
                    nt_moe_stream_t stream);
 
 /*
+ * Route plan in one call: the outputs of nt_moe_histogram_scan followed by nt_moe_permute with
+ * the same arguments (megatron_moe.py:142-145,149), the workspace sized by
+ * nt_moe_route_workspace_bytes(T, k, E). With x_perm NULL and ceil(T/256) * E <= 16384 the
+ * offset scan runs inside the permutation kernel (two launches instead of three); otherwise it
+ * makes exactly those two calls.
+ */
+int nt_moe_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
+                      const float* topk_w, int64_t T, int32_t d, int32_t k, int32_t E,
+                      int32_t* counts, int32_t* offsets, void* workspace, size_t workspace_bytes,
+                      int32_t* src_row, float* perm_w, int32_t* combine_dest, float* combine_w,
+                      uint16_t* x_perm, nt_moe_stream_t stream);
+
+/*
  * Grouped expert FFN over ragged segments, bf16 MFMA with fp32 accumulation:
  *   h[r] = act(a_r . W1_s^T)  (bf16 [rows, H]),   y[r] = h[r] . W2_s^T  (bf16 [rows, d])
  * for every row r of segment s, rows [seg_offsets[s], seg_offsets[s+1]).

@@ -208,6 +208,33 @@ int nt_moe_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
   return launched(err, "permute");
 }
 
+int nt_moe_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
+                      const float* topk_w, int64_t T, int32_t d, int32_t k, int32_t E,
+                      int32_t* counts, int32_t* offsets, void* workspace, size_t workspace_bytes,
+                      int32_t* src_row, float* perm_w, int32_t* combine_dest, float* combine_w,
+                      uint16_t* x_perm, nt_moe_stream_t stream) {
+  int rc = check_route_shape(T, k, E);
+  if (rc) return rc;
+  NT_REQUIRE(counts && offsets && workspace, "route_plan: null buffer");
+  NT_REQUIRE(T == 0 || (topk_ids && topk_w && src_row && combine_dest && combine_w),
+             "route_plan: null buffer");
+  if (workspace_bytes < route_ws_bytes(T, k, E))
+    return fail(NT_MOE_ENOSPC, "route_plan: workspace %zu < %zu bytes", workspace_bytes,
+                route_ws_bytes(T, k, E));
+  if (x_perm && T > 0) {
+    NT_REQUIRE(x, "route_plan: x_perm requested without x");
+    NT_REQUIRE(d > 0 && d % 8 == 0, "route_plan: d must be a positive multiple of 8, got %d", d);
+    NT_REQUIRE(ld_x >= d && ld_x % 8 == 0, "route_plan: ld_x must be >= d and a multiple of 8");
+    NT_REQUIRE(aligned16(x) && aligned16(x_perm),
+               "route_plan: x and x_perm must be 16-byte aligned");
+  }
+  RouteWorkspace ws = route_ws(workspace, T, k);
+  hipError_t err = launch_route_plan(x, ld_x, topk_ids, topk_w, T, d, k, E, counts, offsets,
+                                     ws.ranks, ws.block_counts, src_row, perm_w, combine_dest,
+                                     combine_w, x_perm, reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "route_plan");
+}
+
 size_t nt_moe_grouped_gemm_workspace_bytes(void) { return kGemmWorkspaceBytes; }
 
 int nt_moe_grouped_ffn_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows, const int32_t* src_row,

@@ -66,6 +66,11 @@ hipError_t launch_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_i
                           const int32_t* ranks, const int32_t* block_base,
                           int32_t* src_row, float* perm_w, int32_t* combine_dest,
                           float* combine_w, uint16_t* x_perm, hipStream_t stream);
+hipError_t launch_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
+                             const float* topk_w, int64_t T, int d, int k, int E, int32_t* counts,
+                             int32_t* offsets, int32_t* ranks, int32_t* block_counts,
+                             int32_t* src_row, float* perm_w, int32_t* combine_dest,
+                             float* combine_w, uint16_t* x_perm, hipStream_t stream);
 
 hipError_t launch_grouped_ffn_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                                    const int32_t* src_row,

@@ -179,6 +179,112 @@ __global__ __launch_bounds__(256) void permute_kernel(
   }
 }
 
+// Largest counts table (blocks x experts) that plan_kernel reads in every workgroup; larger
+// shapes take scan_kernel + permute_kernel.
+constexpr int64_t kPlanTableMax = 16384;
+
+// scan_kernel and permute_kernel (without the row move) in one launch, one workgroup per
+// histogram block: the block's expert bases from the counts table -- each column summed over
+// the earlier blocks, plus the exclusive scan over experts of the column totals -- then the
+// permutation of its 256 tokens, one thread per token. Workgroup 0 writes counts and offsets.
+// Every workgroup sums the table in the same fixed shape; all integer, so the bases equal
+// scan_kernel's block_base exactly.
+__global__ __launch_bounds__(256) void plan_kernel(
+    const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int64_t T, int k,
+    int E, int nblk, const int32_t* __restrict__ ranks, const int32_t* __restrict__ block_counts,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ src_row,
+    float* __restrict__ perm_w, int32_t* __restrict__ combine_dest,
+    float* __restrict__ combine_w) {
+  __shared__ int32_t pre_s[256], tot_s[256];  // [G][E] partial column sums, G * E <= 256
+  __shared__ int32_t base_s[NT_MOE_MAX_EXPERTS];
+  __shared__ int32_t wave_tot[4];
+  const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
+  const int blk = blockIdx.x;
+  // The token's ids, weights and ranks are loaded first; their latency overlaps the table's.
+  const int64_t t = (int64_t)blk * kHistBlock + tid;
+  const bool live = t < T;
+  int ev[NT_MOE_MAX_TOPK], rv[NT_MOE_MAX_TOPK];
+  float wv[NT_MOE_MAX_TOPK];
+#pragma unroll
+  for (int j = 0; j < NT_MOE_MAX_TOPK; ++j) {
+    ev[j] = 0x7fffffff;
+    rv[j] = 0;
+    wv[j] = 0.f;
+    if (live && j < k) {
+      ev[j] = topk_ids[t * k + j];
+      wv[j] = topk_w[t * k + j];
+      rv[j] = ranks[t * k + j];  // in bounds; used only for valid ids
+    }
+  }
+  const int G = 256 / E;  // groups of E threads; group g sums blocks g, g + G, ...
+  const int g = tid / E, e = tid - g * E;
+  if (g < G) {
+    int pre = 0, tot = 0;
+#pragma unroll 8
+    for (int b = g; b < nblk; b += G) {
+      const int c = block_counts[(int64_t)b * E + e];
+      tot += c;
+      pre += b < blk ? c : 0;
+    }
+    pre_s[tid] = pre;
+    tot_s[tid] = tot;
+  }
+  __syncthreads();
+  int before = 0, total = 0;  // thread tid owns expert tid
+  if (tid < E) {
+    for (int q = 0; q < G; ++q) {
+      before += pre_s[q * E + tid];
+      total += tot_s[q * E + tid];
+    }
+  }
+  const int incl = group_inclusive_scan(total, 64);
+  if (lane == 63) wave_tot[w] = incl;
+  __syncthreads();
+  int carry = 0;
+  for (int q = 0; q < w; ++q) carry += wave_tot[q];
+  const int excl = carry + incl - total;  // offsets[tid]
+  if (tid < E) {
+    base_s[tid] = excl + before;
+    if (blk == 0) {
+      counts[tid] = total;
+      offsets[tid] = excl;
+    }
+  }
+  if (blk == 0 && tid == 0) offsets[E] = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
+  __syncthreads();
+
+  if (!live) return;
+  const int64_t A = T * k;
+  int dv[NT_MOE_MAX_TOPK];
+#pragma unroll
+  for (int j = 0; j < NT_MOE_MAX_TOPK; ++j) {
+    dv[j] = 0;
+    if (j < k) {
+      if ((unsigned)ev[j] < (unsigned)E) {
+        int dest = base_s[ev[j]] + rv[j];
+        dest = dest < 0 ? 0 : (dest >= A ? (int)(A - 1) : dest);
+        src_row[dest] = (int32_t)t;
+        if (perm_w) perm_w[dest] = wv[j];
+        dv[j] = dest;
+      } else {
+        ev[j] = 0x7ffffffe;  // ignored id: sorts last, row 0 as a harmless target
+      }
+    }
+  }
+  // Ascending expert order; equal keys (only ignored ids) keep their slot order.
+#pragma unroll
+  for (int j = 0; j < NT_MOE_MAX_TOPK; ++j) {
+    if (j < k) {
+      int pos = 0;
+#pragma unroll
+      for (int i = 0; i < NT_MOE_MAX_TOPK; ++i)
+        pos += (ev[i] < ev[j] || (ev[i] == ev[j] && i < j)) ? 1 : 0;
+      combine_dest[t * k + pos] = dv[j];
+      combine_w[t * k + pos] = wv[j];
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_histogram_scan(const int32_t* topk_ids, int64_t T, int k, int E,
@@ -211,6 +317,30 @@ hipError_t launch_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_i
   hipLaunchKernelGGL(permute_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, x, ld_x,
                      topk_ids, topk_w, T, d, k, E, ranks, block_base, src_row, perm_w,
                      combine_dest, combine_w, x_perm);
+  return hipGetLastError();
+}
+
+hipError_t launch_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
+                             const float* topk_w, int64_t T, int d, int k, int E, int32_t* counts,
+                             int32_t* offsets, int32_t* ranks, int32_t* block_counts,
+                             int32_t* src_row, float* perm_w, int32_t* combine_dest,
+                             float* combine_w, uint16_t* x_perm, hipStream_t stream) {
+  const int64_t nblk = ceil_div(T, kHistBlock);
+  if (T == 0 || x_perm || nblk * E > kPlanTableMax) {
+    hipError_t err = launch_histogram_scan(topk_ids, T, k, E, counts, offsets, ranks,
+                                           block_counts, stream);
+    if (err != hipSuccess) return err;
+    return launch_permute(x, ld_x, topk_ids, topk_w, T, d, k, E, ranks, block_counts, src_row,
+                          perm_w, combine_dest, combine_w, x_perm, stream);
+  }
+  size_t lds = (size_t)4 * E * (sizeof(uint64_t) + sizeof(int32_t));
+  hipLaunchKernelGGL(histogram_kernel, dim3((unsigned)nblk), dim3(256), lds, stream, topk_ids, T,
+                     k, E, ranks, block_counts);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(plan_kernel, dim3((unsigned)nblk), dim3(256), 0, stream, topk_ids, topk_w, T,
+                     k, E, (int)nblk, ranks, block_counts, counts, offsets, src_row, perm_w,
+                     combine_dest, combine_w);
   return hipGetLastError();
 }
 

@@ -137,13 +137,12 @@ def route_plan(ids: Tensor, weights: Tensor, num_experts: int, x: Optional[Tenso
     ws_bytes = lib.nt_moe_route_workspace_bytes(T, k, E)
     ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
     stream = _stream(dev)
-    nat.check(lib.nt_moe_histogram_scan(ptr(ids), T, k, E, ptr(counts), ptr(offsets), ptr(ws),
-                                        ws_bytes, stream), "ntmoe::route_plan histogram")
-    nat.check(lib.nt_moe_permute(ptr(x) if want_x_perm else None,
-                                 x.stride(0) if want_x_perm else 0, ptr(ids), ptr(weights), T, d,
-                                 k, E, ptr(ws), ws_bytes, ptr(src), ptr(perm_w), ptr(cdest),
-                                 ptr(cw), ptr(x_perm) if want_x_perm else None, stream),
-              "ntmoe::route_plan permute")
+    nat.check(lib.nt_moe_route_plan(ptr(x) if want_x_perm else None,
+                                    x.stride(0) if want_x_perm else 0, ptr(ids), ptr(weights), T,
+                                    d, k, E, ptr(counts), ptr(offsets), ptr(ws), ws_bytes,
+                                    ptr(src), ptr(perm_w), ptr(cdest), ptr(cw),
+                                    ptr(x_perm) if want_x_perm else None, stream),
+              "ntmoe::route_plan")
     return counts, offsets, src, perm_w, cdest, cw, x_perm
 
 

@@ -156,6 +156,54 @@ def test_route_plan_bit_exact(case):
     assert torch.equal(x_perm.cpu(), cpu["x"][r_src.long()])
 
 
+# (T, E, k, skew): the one-launch scan + permutation (counts table of ceil(T/256) x E entries up
+# to 16384: the benchmark shapes, E not dividing 256, E = 256, a ragged last block) and the
+# three-launch path beyond that table size (T = 40000, E = 128).
+PLAN_SHAPES = [(1, 4, 1, 0.0), (1000, 32, 4, 0.0), (16384, 32, 4, 0.0), (32768, 64, 8, 1.2),
+               (8192, 128, 8, 0.0), (300, 256, 8, 0.0), (777, 96, 3, 1.2), (16411, 24, 3, 0.0),
+               (40000, 128, 2, 1.2)]
+
+
+@pytest.mark.parametrize("T,E,k,skew", PLAN_SHAPES)
+def test_route_plan_one_call_matches_oracle_and_two_calls(T, E, k, skew):
+    """nt_moe_route_plan (the module's path) against the oracle, the reference's
+    mapping.T.nonzero() order, and nt_moe_histogram_scan + nt_moe_permute, bit for bit."""
+    import ctypes
+    from nexttransformer_amd import _native as nat, ops
+    g = torch.Generator().manual_seed(T * 7 + E)
+    scores = torch.rand(T, E, generator=g) - skew * torch.log1p(torch.arange(E).float())
+    ids_c = scores.topk(k, dim=1).indices.int()
+    w_c = torch.rand(T, k, generator=g)
+    ids, w = ids_c.cuda(), w_c.cuda()
+    counts, offsets, src, perm_w, cdest, cw, _ = ops.route_plan(ids, w, E, None, False)
+    r_counts, r_offsets, r_src, r_dest = orc.route_plan(ids_c, E)
+    assert torch.equal(counts.cpu(), r_counts)
+    assert torch.equal(offsets.cpu(), r_offsets)
+    assert torch.equal(src.cpu(), r_src)
+    mapping = torch.zeros(T, E, dtype=torch.bool)
+    mapping[torch.arange(T)[:, None], ids_c.long()] = True
+    assert torch.equal(src.cpu().long(), mapping.T.nonzero()[:, 1])
+    order = ids_c.long().argsort(-1)
+    assert torch.equal(cdest.cpu(), r_dest.gather(1, order))
+    assert torch.equal(cw.cpu(), w_c.gather(1, order))
+    assert torch.equal(perm_w.cpu()[r_dest.long()], w_c)
+    # the same outputs from the two separate entry points
+    lib = nat.load()
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    ws_bytes = lib.nt_moe_route_workspace_bytes(T, k, E)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    c2, o2 = torch.empty_like(counts), torch.empty_like(offsets)
+    s2, p2, d2, w2 = (torch.empty_like(src), torch.empty_like(perm_w), torch.empty_like(cdest),
+                      torch.empty_like(cw))
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.nt_moe_histogram_scan(P(ids), T, k, E, P(c2), P(o2), P(ws), ws_bytes, stream) == 0
+    assert lib.nt_moe_permute(None, 0, P(ids), P(w), T, 0, k, E, P(ws), ws_bytes, P(s2), P(p2),
+                              P(d2), P(w2), None, stream) == 0
+    torch.cuda.synchronize()
+    for a, b in ((counts, c2), (offsets, o2), (src, s2), (perm_w, p2), (cdest, d2), (cw, w2)):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("case", SMALL, ids=lambda c: c.name)
 @pytest.mark.parametrize("permute_rows", [False, True])
 def test_layer_forward_matches_fp32_reference(case, permute_rows):
