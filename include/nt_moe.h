@@ -293,6 +293,43 @@ int nt_moe_combine_aux(const uint16_t* y, const int32_t* combine_dest, const flo
                        const int32_t* counts, int32_t E, float aux_coeff, float z_coeff,
                        float* aux_out, nt_moe_stream_t stream);
 
+/*
+ * Backward of the layer (autograd through megatron_moe.py:137-150 and the MCore router and
+ * aux losses, megatron_moe.py:43-45,95-100; the reference trains through it, e.g.
+ * tests/test_megatron_moe.py:183-197). The grouped dgrad GEMMs use the forward entry points
+ * with transposed weights; these three cover the rest. All reductions have a fixed shape.
+ *
+ * Combine transpose: for token t and its k assignments (combine_dest / combine_w from
+ * nt_moe_permute, ascending expert order)
+ *   grad_y[dest]   = w * grad_out[t]                 bf16 [T*k, d] (expert-major rows)
+ *   grad_w[t, j]   = <grad_out[t], y[dest of slot j]> fp32 [T, k], top-k slot order of topk_ids
+ * y is the forward's expert output (bf16 [T*k, d]); d % 8 == 0, ld_grad % 8 == 0.
+ */
+int nt_moe_combine_bwd(const uint16_t* grad_out, int64_t ld_grad, const uint16_t* y,
+                       const int32_t* topk_ids, const int32_t* combine_dest,
+                       const float* combine_w, int64_t T, int32_t d, int32_t k,
+                       uint16_t* grad_y, float* grad_w, nt_moe_stream_t stream);
+
+/*
+ * Activation backward (megatron_moe.py:23-24, lm.py:29-35): grad_fc1 from grad_h [rows, H] and
+ * the fc1 pre-activations [rows, F] (F = 2H for SwiGLU, gate then value; H for ReLU^2), bf16.
+ * H % 8 == 0.
+ */
+int nt_moe_act_bwd(const uint16_t* fc1, const uint16_t* grad_h, int64_t rows, int32_t H,
+                   int32_t activation, uint16_t* grad_fc1, nt_moe_stream_t stream);
+
+/*
+ * Router backward: grad_logits fp32 [T, E] from grad_w (the routing weights' gradient, top-k
+ * slot order) through the k-selected normalisation of score_fn, plus the load-balance and
+ * z-loss terms when grad_aux (device fp32 [3], the gradient of nt_moe_combine_aux's
+ * {lb + z, lb, z}) is given. logits are the forward's (bias included); counts its counts.
+ * Then grad Wr = grad_logits^T x and grad x += grad_logits Wr are plain GEMMs.
+ */
+int nt_moe_router_bwd(const float* logits, const int32_t* topk_ids, const float* topk_w,
+                      const float* grad_w, const int32_t* counts, int64_t T, int32_t E,
+                      int32_t k, int32_t score_fn, const float* grad_aux, float aux_coeff,
+                      float z_coeff, float* grad_logits, nt_moe_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

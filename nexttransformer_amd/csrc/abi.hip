@@ -208,6 +208,57 @@ int nt_moe_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
   return launched(err, "permute");
 }
 
+int nt_moe_combine_bwd(const uint16_t* grad_out, int64_t ld_grad, const uint16_t* y,
+                       const int32_t* topk_ids, const int32_t* combine_dest,
+                       const float* combine_w, int64_t T, int32_t d, int32_t k,
+                       uint16_t* grad_y, float* grad_w, nt_moe_stream_t stream) {
+  NT_REQUIRE(T >= 0 && T * (int64_t)k < ((int64_t)1 << 31), "combine_bwd: T * k must fit int32");
+  NT_REQUIRE(k >= 1 && k <= NT_MOE_MAX_TOPK, "combine_bwd: top-k must be in [1, %d], got %d",
+             NT_MOE_MAX_TOPK, k);
+  NT_REQUIRE(d > 0 && d % 8 == 0, "combine_bwd: d must be a positive multiple of 8, got %d", d);
+  NT_REQUIRE(ld_grad >= d && ld_grad % 8 == 0, "combine_bwd: ld_grad must be >= d and a multiple of 8");
+  if (T == 0) return ok();
+  NT_REQUIRE(grad_out && y && topk_ids && combine_dest && combine_w && grad_y && grad_w,
+             "combine_bwd: null buffer");
+  NT_REQUIRE(aligned16(grad_out) && aligned16(y) && aligned16(grad_y),
+             "combine_bwd: grad_out, y and grad_y must be 16-byte aligned");
+  return launched(launch_combine_bwd(grad_out, ld_grad, y, topk_ids, combine_dest, combine_w, T,
+                                     d, k, grad_y, grad_w, reinterpret_cast<hipStream_t>(stream)),
+                  "combine_bwd");
+}
+
+int nt_moe_act_bwd(const uint16_t* fc1, const uint16_t* grad_h, int64_t rows, int32_t H,
+                   int32_t activation, uint16_t* grad_fc1, nt_moe_stream_t stream) {
+  NT_REQUIRE(rows >= 0, "act_bwd: rows must be >= 0");
+  NT_REQUIRE(H > 0 && H % 8 == 0, "act_bwd: H must be a positive multiple of 8, got %d", H);
+  NT_REQUIRE(activation == NT_MOE_ACT_SWIGLU || activation == NT_MOE_ACT_RELU2,
+             "act_bwd: unknown activation %d", activation);
+  if (rows == 0) return ok();
+  NT_REQUIRE(fc1 && grad_h && grad_fc1, "act_bwd: null buffer");
+  NT_REQUIRE(aligned16(fc1) && aligned16(grad_h) && aligned16(grad_fc1),
+             "act_bwd: buffers must be 16-byte aligned");
+  return launched(launch_act_bwd(fc1, grad_h, rows, H, activation, grad_fc1,
+                                 reinterpret_cast<hipStream_t>(stream)),
+                  "act_bwd");
+}
+
+int nt_moe_router_bwd(const float* logits, const int32_t* topk_ids, const float* topk_w,
+                      const float* grad_w, const int32_t* counts, int64_t T, int32_t E,
+                      int32_t k, int32_t score_fn, const float* grad_aux, float aux_coeff,
+                      float z_coeff, float* grad_logits, nt_moe_stream_t stream) {
+  int rc = check_route_shape(T, k, E);
+  if (rc) return rc;
+  NT_REQUIRE(score_fn == NT_MOE_SCORE_SOFTMAX || score_fn == NT_MOE_SCORE_SIGMOID,
+             "router_bwd: unknown score_fn %d", score_fn);
+  if (T == 0) return ok();
+  NT_REQUIRE(logits && topk_ids && topk_w && grad_w && counts && grad_logits,
+             "router_bwd: null buffer");
+  return launched(launch_router_bwd(logits, topk_ids, topk_w, grad_w, counts, T, E, k, score_fn,
+                                    grad_aux, aux_coeff, z_coeff, grad_logits,
+                                    reinterpret_cast<hipStream_t>(stream)),
+                  "router_bwd");
+}
+
 int nt_moe_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
                       const float* topk_w, int64_t T, int32_t d, int32_t k, int32_t E,
                       int32_t* counts, int32_t* offsets, void* workspace, size_t workspace_bytes,

@@ -66,6 +66,16 @@ hipError_t launch_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_i
                           const int32_t* ranks, const int32_t* block_base,
                           int32_t* src_row, float* perm_w, int32_t* combine_dest,
                           float* combine_w, uint16_t* x_perm, hipStream_t stream);
+hipError_t launch_combine_bwd(const uint16_t* g, int64_t ld_g, const uint16_t* y,
+                              const int32_t* topk_ids, const int32_t* combine_dest,
+                              const float* combine_w, int64_t T, int d, int k, uint16_t* dy,
+                              float* dw, hipStream_t stream);
+hipError_t launch_act_bwd(const uint16_t* fc1, const uint16_t* dh, int64_t rows, int H,
+                          int activation, uint16_t* dfc1, hipStream_t stream);
+hipError_t launch_router_bwd(const float* logits, const int32_t* topk_ids, const float* topk_w,
+                             const float* dw, const int32_t* counts, int64_t T, int E, int k,
+                             int score_fn, const float* grad_aux, float aux_coeff, float z_coeff,
+                             float* dlogits, hipStream_t stream);
 hipError_t launch_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
                              const float* topk_w, int64_t T, int d, int k, int E, int32_t* counts,
                              int32_t* offsets, int32_t* ranks, int32_t* block_counts,

@@ -90,6 +90,57 @@ def _ep_size(pg_collection):
     return int(size)
 
 
+class _MoETrain(torch.autograd.Function):
+    """The layer with gradients (bf16 experts): ops.moe_forward, then ops.moe_backward. Its
+    inputs are the fp32 masters (the experts' stacked), so gradients reach the parameters; the
+    bf16 copies the GEMMs read are made here, as MasterLinear casts its master per call
+    (megatron_moe.py:58-78)."""
+
+    @staticmethod
+    def forward(ctx, x, router_w, w1, w2, sw1, sw2, cfg):
+        bf = torch.bfloat16
+        wr_t = router_w.detach().t().contiguous()
+        w1b = w1.detach().to(bf).contiguous()
+        w2b = w2.detach().to(bf).contiguous()
+        sw1b = sw1.detach().to(bf).contiguous() if sw1 is not None else None
+        sw2b = sw2.detach().to(bf).contiguous() if sw2 is not None else None
+        up = nat.EPI_SWIGLU if cfg["activation"] == nat.ACT_SWIGLU else nat.EPI_RELU2
+        H = w2b.shape[2]
+        widths = [(H, w2b.shape[1])] + ([(sw2b.shape[2], sw2b.shape[1])] if sw1b is not None else [])
+        packed = all(ops.packable(d, h, up) and ops.packable(h, d, nat.EPI_NONE)
+                     for h, d in widths)
+        fw = (lambda w, e: ops.pack_expert_weights(w, e)) if packed else (lambda w, e: w)
+        out, aux, state = ops.moe_forward(
+            x, wr_t, fw(w1b, up), fw(w2b, nat.EPI_NONE), top_k=cfg["top_k"],
+            score_fn=cfg["score_fn"], activation=cfg["activation"], aux_coeff=cfg["aux_coeff"],
+            z_coeff=cfg["z_coeff"],
+            shared_w1=fw(sw1b, up) if sw1b is not None else None,
+            shared_w2=fw(sw2b, nat.EPI_NONE) if sw2b is not None else None,
+            want_logits=True, packed=packed, keep=True)
+        cfg["counts"] = state["counts"]
+        ctx.cfg = cfg
+        ctx.state = state
+        ctx.tensors = (x, wr_t, w1b, w2b, sw1b, sw2b)
+        return out, aux
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_aux):
+        x, wr_t, w1b, w2b, sw1b, sw2b = ctx.tensors
+        cfg = ctx.cfg
+        if x.shape[0] == 0:
+            z = lambda t: None if t is None else torch.zeros(t.shape, device=t.device)
+            return (torch.zeros_like(x), z(wr_t.t()), z(w1b), z(w2b), z(sw1b), z(sw2b), None)
+        bw = ops.backward_weights(w1b, w2b, sw1b, sw2b)
+        g = ops.moe_backward(grad_out, None if grad_aux is None else grad_aux.contiguous(), x,
+                             wr_t, bw, ctx.state, top_k=cfg["top_k"], score_fn=cfg["score_fn"],
+                             activation=cfg["activation"], aux_coeff=cfg["aux_coeff"],
+                             z_coeff=cfg["z_coeff"])
+        ctx.state = ctx.tensors = None
+        f = lambda t: None if t is None else t.float()
+        return (g["x"], g["router"], f(g["w1"]), f(g["w2"]), f(g["shared_w1"]),
+                f(g["shared_w2"]), None)
+
+
 class MoELayer(nn.Module):
     """MoE layer forward on one MI355X: router -> route plan -> grouped GEMMs -> combine + aux.
 
@@ -244,13 +295,12 @@ class MoELayer(nn.Module):
             raise ValueError(f"hidden width {hidden.shape[-1]} != recipe width {r.width}")
         if not hidden.is_cuda:
             raise ValueError("the MoE layer runs on the GPU only (no CPU path)")
-        if torch.is_grad_enabled() and (hidden.requires_grad or
-                                        any(p.requires_grad for p in self.parameters())):
-            raise RuntimeError("the HIP MoE layer is forward-only: call it under torch.no_grad() "
-                               "or torch.inference_mode()")
         if self.router.weight.device != hidden.device:
             raise ValueError(f"parameters are on {self.router.weight.device}, hidden on "
                              f"{hidden.device}")
+        if torch.is_grad_enabled() and (hidden.requires_grad or
+                                        any(p.requires_grad for p in self.parameters())):
+            return self._forward_train(hidden)
         w = self.packed_weights()
         x = hidden.reshape(-1, r.width)
         dp = w["router_t"].shape[0]
@@ -274,6 +324,32 @@ class MoELayer(nn.Module):
         self.last_aux = aux[0]
         out = out.reshape(hidden.shape).to(hidden.dtype)
         return out, self.last_aux
+
+
+    def _forward_train(self, hidden):
+        """Forward with gradients to hidden and every master (bf16 experts)."""
+        r = self.recipe
+        widths = [r.width, r.expert_width] + (
+            [r.shared_expert_width] if self.shared_experts is not None else [])
+        if r.expert_dtype == "fp8" or any(w % 64 for w in widths):
+            raise RuntimeError("the MoE backward covers bf16 experts whose widths are multiples "
+                               "of 64; run this configuration under torch.no_grad()")
+        x = hidden.reshape(-1, r.width).to(torch.bfloat16).contiguous()
+        experts = list(self.experts.local_experts)
+        w1 = torch.stack([e.linear_fc1.weight for e in experts])
+        w2 = torch.stack([e.linear_fc2.weight for e in experts])
+        sw1 = sw2 = None
+        if self.shared_experts is not None:
+            sw1 = self.shared_experts.linear_fc1.weight.unsqueeze(0)
+            sw2 = self.shared_experts.linear_fc2.weight.unsqueeze(0)
+        cfg = dict(top_k=r.top_k, score_fn=_SCORE[r.score_function],
+                   activation=_ACT[r.activation], aux_coeff=r.aux_loss_coeff,
+                   z_coeff=r.z_loss_coeff)
+        out, aux = _MoETrain.apply(x, self.router.weight, w1, w2, sw1, sw2, cfg)
+        self.last_load = cfg["counts"].to(torch.int64)
+        self.last_aux_parts = aux.detach()
+        self.last_aux = aux[0]
+        return out.reshape(hidden.shape).to(hidden.dtype), self.last_aux
 
 
 class MoEFFN(nn.Module):

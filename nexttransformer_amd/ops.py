@@ -456,7 +456,7 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
                 activation=nat.ACT_SWIGLU, aux_coeff=0.01, z_coeff=0.001, logit_bias=None,
                 shared_w1=None, shared_w2=None, want_logits=False, permute_rows=False,
                 w1_scale=None, w2_scale=None, shared_w1_scale=None, shared_w2_scale=None,
-                packed=False, mark=None):
+                packed=False, mark=None, keep=False):
     """The MoE layer forward on the GPU: router -> route plan -> grouped GEMMs -> combine + aux.
 
     x bf16 [T, d]; w_router_t fp32 [d, E]; w1 bf16 [E, F, d] (F = 2H for SwiGLU, H for ReLU^2);
@@ -471,7 +471,8 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
     block scales (w*_scale, from quantize_fp8_blockwise); the token rows and the intermediate
     h are then quantised per row and both projections run on the fp8 grouped GEMM.
     `mark(name)`, when given, is called after each stage is enqueued (used to place timing
-    events on the stream).
+    events on the stream). keep (bf16 experts): the state also holds what moe_backward reads
+    (h, y, the shared expert's h, the router's aux partials).
     """
     T = x.shape[0]
     E = w_router_t.shape[1]
@@ -526,7 +527,7 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
     mark("gemm_up")
     y = gemm(h, None, offsets, w2, nat.EPI_NONE, A)
     mark("gemm_down")
-    shared_y = None
+    shared_y = hs = None
     if shared_w1 is not None:
         seg = _whole_batch_segment(T, x.device)
         hs = gemm(x, None, seg, shared_w1, up_epi, T)
@@ -536,4 +537,181 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
     mark("combine")
     state = dict(logits=logits, ids=ids, weights=w, counts=counts, offsets=offsets, src_row=src,
                  perm_w=perm_w, combine_dest=cdest, combine_w=cw)
+    if keep:
+        state.update(h=h, y=y, shared_h=hs, prob_partial=pp, z_partial=zp)
     return out, aux, state
+
+
+# ---------------------------------------------------------------------------------------------
+# backward (bf16 experts)
+
+@torch.library.custom_op("ntmoe::combine_bwd", mutates_args=())
+def combine_bwd(grad_out: Tensor, y: Tensor, ids: Tensor, combine_dest: Tensor,
+                combine_w: Tensor) -> tuple[Tensor, Tensor]:
+    """(grad_y bf16 [T*k, d] expert-major, grad_w fp32 [T, k] in top-k slot order)."""
+    _on_gpu(grad_out, y, ids, combine_dest, combine_w)
+    T, k = ids.shape
+    _require(grad_out.dtype == torch.bfloat16 and grad_out.dim() == 2 and grad_out.shape[0] == T
+             and grad_out.stride(1) == 1, "combine_bwd: grad_out must be bf16 [T, d]")
+    d = grad_out.shape[1]
+    _require(y.dtype == torch.bfloat16 and y.shape == (T * k, d) and y.is_contiguous(),
+             "combine_bwd: y must be contiguous bf16 [T*k, d]")
+    _require(ids.dtype == torch.int32 and ids.is_contiguous() and combine_dest.dtype == torch.int32
+             and combine_dest.shape == (T, k) and combine_dest.is_contiguous()
+             and combine_w.dtype == torch.float32 and combine_w.shape == (T, k)
+             and combine_w.is_contiguous(), "combine_bwd: bad ids / combine_dest / combine_w")
+    dev = y.device
+    gy = torch.empty(T * k, d, device=dev, dtype=torch.bfloat16)
+    gw = torch.empty(T, k, device=dev, dtype=torch.float32)
+    st = nat.load().nt_moe_combine_bwd(ptr(grad_out), grad_out.stride(0), ptr(y), ptr(ids),
+                                       ptr(combine_dest), ptr(combine_w), T, d, k, ptr(gy),
+                                       ptr(gw), _stream(dev))
+    nat.check(st, "ntmoe::combine_bwd")
+    return gy, gw
+
+
+@combine_bwd.register_fake
+def _(grad_out, y, ids, combine_dest, combine_w):
+    T, k = ids.shape
+    return (y.new_empty(T * k, grad_out.shape[1]),
+            y.new_empty((T, k), dtype=torch.float32))
+
+
+@torch.library.custom_op("ntmoe::act_bwd", mutates_args=())
+def act_bwd(fc1: Tensor, grad_h: Tensor, activation: int) -> Tensor:
+    """grad of the fc1 pre-activations [rows, F] from grad_h [rows, H]."""
+    _on_gpu(fc1, grad_h)
+    _require(fc1.dtype == torch.bfloat16 and grad_h.dtype == torch.bfloat16 and fc1.is_contiguous()
+             and grad_h.is_contiguous() and fc1.dim() == 2 and grad_h.dim() == 2,
+             "act_bwd: fc1 and grad_h must be contiguous bf16 matrices")
+    rows, H = grad_h.shape
+    F = 2 * H if activation == nat.ACT_SWIGLU else H
+    _require(fc1.shape == (rows, F), "act_bwd: fc1 must be [rows, 2H] (SwiGLU) or [rows, H]")
+    out = torch.empty_like(fc1)
+    st = nat.load().nt_moe_act_bwd(ptr(fc1), ptr(grad_h), rows, H, activation, ptr(out),
+                                   _stream(fc1.device))
+    nat.check(st, "ntmoe::act_bwd")
+    return out
+
+
+@act_bwd.register_fake
+def _(fc1, grad_h, activation):
+    return torch.empty_like(fc1)
+
+
+@torch.library.custom_op("ntmoe::router_bwd", mutates_args=())
+def router_bwd(logits: Tensor, ids: Tensor, weights: Tensor, grad_w: Tensor, counts: Tensor,
+               score_fn: int, grad_aux: Optional[Tensor], aux_coeff: float,
+               z_coeff: float) -> Tensor:
+    """grad_logits fp32 [T, E] (routing-weight and aux/z-loss terms)."""
+    _on_gpu(logits, ids, weights, grad_w, counts, grad_aux)
+    T, E = logits.shape
+    k = ids.shape[1]
+    _require(logits.dtype == torch.float32 and logits.is_contiguous(),
+             "router_bwd: logits must be contiguous fp32 [T, E]")
+    _require(ids.dtype == torch.int32 and ids.shape == (T, k) and ids.is_contiguous()
+             and weights.dtype == torch.float32 and weights.shape == (T, k)
+             and weights.is_contiguous() and grad_w.dtype == torch.float32
+             and grad_w.shape == (T, k) and grad_w.is_contiguous(),
+             "router_bwd: bad ids / weights / grad_w")
+    _require(counts.dtype == torch.int32 and counts.shape == (E,), "router_bwd: bad counts")
+    if grad_aux is not None:
+        _require(grad_aux.dtype == torch.float32 and grad_aux.shape == (3,)
+                 and grad_aux.is_contiguous(), "router_bwd: grad_aux must be fp32 [3]")
+    out = torch.empty_like(logits)
+    st = nat.load().nt_moe_router_bwd(ptr(logits), ptr(ids), ptr(weights), ptr(grad_w),
+                                      ptr(counts), T, E, k, score_fn, ptr(grad_aux),
+                                      float(aux_coeff), float(z_coeff), ptr(out),
+                                      _stream(logits.device))
+    nat.check(st, "ntmoe::router_bwd")
+    return out
+
+
+@router_bwd.register_fake
+def _(logits, ids, weights, grad_w, counts, score_fn, grad_aux, aux_coeff, z_coeff):
+    return torch.empty_like(logits)
+
+
+class Projection:
+    """One dgrad / recompute GEMM's weights, c[r] = a_r . W_s^T with W [S, n, K] bf16: packed for
+    the packed GEMM when the shape qualifies, else the plain grouped GEMM's operand."""
+
+    def __init__(self, w):
+        S, n, K = w.shape
+        self.packed = packable(K, n, nat.EPI_NONE)
+        self.w = pack_expert_weights(w.contiguous(), nat.EPI_NONE) if self.packed else w.contiguous()
+
+    def __call__(self, a, src_row, seg_offsets, total_rows):
+        gemm = grouped_gemm_packed if self.packed else grouped_gemm
+        return gemm(a, src_row, seg_offsets, self.w, nat.EPI_NONE, total_rows)
+
+
+def backward_weights(w1, w2, shared_w1=None, shared_w2=None):
+    """The backward's GEMM operands from the bf16 weights the forward used (plain layout):
+    W1 (recompute of the fc1 pre-activations), W1^T and W2^T (dgrad), and the shared expert's."""
+    t = lambda w: w.transpose(1, 2).contiguous()
+    bw = dict(w1=Projection(w1), w1t=Projection(t(w1)), w2t=Projection(t(w2)), w1_plain=w1,
+              w2_plain=w2, shared=None)
+    if shared_w1 is not None:
+        bw["shared"] = dict(w1=Projection(shared_w1), w1t=Projection(t(shared_w1)),
+                            w2t=Projection(t(shared_w2)))
+    return bw
+
+
+def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
+                 score_fn=nat.SCORE_SOFTMAX, activation=nat.ACT_SWIGLU, aux_coeff=0.01,
+                 z_coeff=0.001):
+    """Gradients of moe_forward (bf16 experts) for grad_out [T, d] and grad_aux [3] (or None).
+
+    state: moe_forward's state from a call with want_logits=True and keep=True; bw: from
+    backward_weights. Returns dict(x bf16 [T, d], router fp32 [E, d] (the router weight's, i.e.
+    of w_router_t^T), w1 [E, F, d], w2 [E, d, H], shared_w1, shared_w2 (bf16)).
+
+    On the GPU kernels: fc1 recompute, dgrad of both projections (grouped GEMMs), the combine
+    transpose and routing-weight gradient, the activation backward, the token-side sum of the
+    k gradient rows (the forward's combine kernel with unit weights, shared expert first) and
+    the router backward. The router's two fp32 products and the expert weight gradients
+    (per-expert dy^T h and d_fc1^T x products) are plain library GEMMs.
+    """
+    T, d = x.shape
+    E = w_router_t.shape[1]
+    k = top_k
+    A = T * k
+    src, offsets = state["src_row"], state["offsets"]
+    cdest, ids = state["combine_dest"], state["ids"]
+    g = grad_out.to(torch.bfloat16).contiguous()
+    fc1 = bw["w1"](x, src, offsets, A)
+    gy, gw = combine_bwd(g, state["y"], ids, cdest, state["combine_w"])
+    dh = bw["w2t"](gy, None, offsets, A)
+    dfc1 = act_bwd(fc1, dh, activation)
+    dxp = bw["w1t"](dfc1, None, offsets, A)
+    dxs = None
+    res = dict(shared_w1=None, shared_w2=None)
+    if bw["shared"] is not None:
+        sb = bw["shared"]
+        seg = _whole_batch_segment(T, x.device)
+        fc1s = sb["w1"](x, None, seg, T)
+        dhs = sb["w2t"](g, None, seg, T)
+        dfc1s = act_bwd(fc1s, dhs, activation)
+        dxs = sb["w1t"](dfc1s, None, seg, T)
+        res["shared_w1"] = (dfc1s.t() @ x).unsqueeze(0)
+        res["shared_w2"] = (g.t() @ state["shared_h"]).unsqueeze(0)
+    ones = torch.ones(T, k, device=x.device, dtype=torch.float32)
+    dx_e, _ = combine_aux(dxp, cdest, ones, dxs, state["prob_partial"], state["z_partial"],
+                          state["counts"], 0.0, 0.0)
+    dlogits = router_bwd(state["logits"], ids, state["weights"], gw, state["counts"], score_fn,
+                         grad_aux, aux_coeff, z_coeff)
+    res["router"] = dlogits.t() @ x.float()
+    res["x"] = (dx_e.float() + dlogits @ w_router_t.t()).to(torch.bfloat16)
+    # expert weight gradients over each expert's rows (offsets read on the host)
+    F, H = bw["w1_plain"].shape[1], bw["w2_plain"].shape[2]
+    gw1 = torch.zeros(E, F, d, device=x.device, dtype=torch.bfloat16)
+    gw2 = torch.zeros(E, d, H, device=x.device, dtype=torch.bfloat16)
+    xp = x.index_select(0, src.long())
+    h = state["h"]
+    for e, (lo, hi) in enumerate(zip(offsets[:-1].tolist(), offsets[1:].tolist())):
+        if hi > lo:
+            gw1[e] = dfc1[lo:hi].t() @ xp[lo:hi]
+            gw2[e] = gy[lo:hi].t() @ h[lo:hi]
+    res["w1"], res["w2"] = gw1, gw2
+    return res

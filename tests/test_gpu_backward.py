@@ -1,0 +1,158 @@
+"""GPU parity of the layer backward against fp32 autograd.
+
+The reference is the layer written in plain PyTorch fp32 on the CPU (router GEMM, softmax or
+sigmoid over the k selected, per-expert SwiGLU / ReLU^2 FFNs with the bf16-rounded weights the
+forward uses, the shared expert, the MCore load-balance and z losses: megatron_moe.py:43-45,
+137-150, reference_blocks.py:35-45), differentiated by autograd for
+loss = <out, G> + g_aux * aux with a random G. The expert selection is the forward's (ids), so
+ties cannot differ. Bar: relative L2 <= 2e-2 for every gradient (the GPU path keeps bf16
+intermediates: the combine transpose, the recomputed fc1 pre-activations, dh, d fc1 and the
+weight-gradient products are bf16 with fp32 accumulation).
+"""
+import pytest
+import torch
+
+from tests.moe_cases import Case, make_inputs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+CASES = [
+    Case("bwd-T512-d256-E8-k2-swiglu", 512, 256, 8, 2, 128, seed=21),
+    Case("bwd-T300-d512-E16-k4-sigmoid-shared", 300, 512, 16, 4, 256, score_fn=1, shared_H=256,
+         seed=22),
+    Case("bwd-T700-d256-E32-k8-relu2-zipf", 700, 256, 32, 8, 128, activation=1, zipf_bias=1.2,
+         seed=23),
+    Case("bwd-T1024-d1024-E32-k4-swiglu", 1024, 1024, 32, 4, 512, seed=24),
+]
+
+
+def ffn(x, w1, w2, activation):
+    f = x @ w1.t()
+    if activation == 0:
+        H = w2.shape[1]
+        h = torch.nn.functional.silu(f[:, :H]) * f[:, H:]
+    else:
+        h = torch.relu(f).square()
+    return h @ w2.t()
+
+
+def reference_grads(x, wr, bias, w1, w2, sw1, sw2, ids, G, g_aux, case, aux_coeff, z_coeff):
+    x = x.float().clone().requires_grad_()
+    wr = wr.float().clone().requires_grad_()
+    w1 = w1.to(torch.bfloat16).float().requires_grad_()
+    w2 = w2.to(torch.bfloat16).float().requires_grad_()
+    params = [x, wr, w1, w2]
+    if sw1 is not None:
+        sw1 = sw1.to(torch.bfloat16).float().requires_grad_()
+        sw2 = sw2.to(torch.bfloat16).float().requires_grad_()
+        params += [sw1, sw2]
+    T, E, k = case.T, case.E, case.k
+    logits = x @ wr.t()
+    if bias is not None:
+        logits = logits + bias
+    ids = ids.long()
+    sel = logits.gather(1, ids)
+    if case.score_fn == 0:
+        w = sel.softmax(-1)
+    else:
+        s = torch.sigmoid(sel)
+        w = s / s.sum(-1, keepdim=True)
+    out = torch.zeros(T, x.shape[1])
+    for e in range(E):
+        tok, slot = torch.where(ids == e)
+        if tok.numel():
+            out = out.index_add(0, tok, ffn(x[tok], w1[e], w2[e], case.activation) * w[tok, slot, None])
+    if sw1 is not None:
+        out = out + ffn(x, sw1[0], sw2[0], case.activation)
+    counts = torch.bincount(ids.flatten(), minlength=E).float()
+    if case.score_fn == 0:
+        p = logits.softmax(-1)
+    else:
+        s = torch.sigmoid(logits)
+        p = s / s.sum(-1, keepdim=True)
+    lb = aux_coeff * E / (k * T * T) * (p.sum(0) * counts).sum()
+    z = z_coeff * torch.logsumexp(logits, -1).square().mean()
+    loss = (out * G).sum() + g_aux * (lb + z)
+    loss.backward()
+    return [t.grad for t in params]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: c.name)
+def test_backward_matches_fp32_autograd(case):
+    from nexttransformer_amd import _native as nat, ops
+    cpu = make_inputs(case)
+    dev = torch.device("cuda")
+    aux_coeff, z_coeff, g_aux = 0.01, 0.001, 3.0
+    x = cpu["x"].to(dev)
+    wr = cpu["router"]  # fp32 [E, d]
+    wr_t = wr.t().contiguous().to(dev)
+    bias = None if cpu["bias"] is None else cpu["bias"].to(dev)
+    bf = torch.bfloat16
+    w1b, w2b = cpu["w1"].to(bf).to(dev), cpu["w2"].to(bf).to(dev)
+    sw1b = sw2b = None
+    if cpu["shared_w1"] is not None:
+        sw1b, sw2b = cpu["shared_w1"].to(bf).to(dev), cpu["shared_w2"].to(bf).to(dev)
+    out, aux, state = ops.moe_forward(x, wr_t, w1b, w2b, top_k=case.k, score_fn=case.score_fn,
+                                      activation=case.activation, aux_coeff=aux_coeff,
+                                      z_coeff=z_coeff, logit_bias=bias, shared_w1=sw1b,
+                                      shared_w2=sw2b, want_logits=True, keep=True)
+    gen = torch.Generator().manual_seed(case.seed + 7)
+    G = torch.randn(case.T, case.d, generator=gen)
+    grad_aux = torch.tensor([g_aux, 0.0, 0.0], device=dev)
+    bw = ops.backward_weights(w1b, w2b, sw1b, sw2b)
+    g = ops.moe_backward(G.to(bf).to(dev), grad_aux, x, wr_t, bw, state, top_k=case.k,
+                         score_fn=case.score_fn, activation=case.activation,
+                         aux_coeff=aux_coeff, z_coeff=z_coeff)
+    torch.cuda.synchronize()
+    ref = reference_grads(cpu["x"], wr, cpu["bias"], cpu["w1"], cpu["w2"], cpu["shared_w1"],
+                          cpu["shared_w2"], state["ids"].cpu(), G.to(bf).float(), g_aux, case,
+                          aux_coeff, z_coeff)
+    names = ["x", "router", "w1", "w2"] + (["shared_w1", "shared_w2"] if sw1b is not None else [])
+    for name, r in zip(names, ref):
+        got = g[name].float().cpu()
+        assert got.shape == r.shape, name
+        err = rel_l2(got, r)
+        assert err <= TOL, f"{name}: relative L2 {err:.3e}"
+
+
+@pytest.mark.parametrize("activation", [0, 1])
+def test_activation_backward_matches_autograd(activation):
+    from nexttransformer_amd import ops
+    rows, H = 333, 136
+    gen = torch.Generator().manual_seed(5 + activation)
+    F = 2 * H if activation == 0 else H
+    fc1 = torch.randn(rows, F, generator=gen).to(torch.bfloat16)
+    dh = torch.randn(rows, H, generator=gen).to(torch.bfloat16)
+    got = ops.act_bwd(fc1.cuda(), dh.cuda(), activation).float().cpu()
+    f = fc1.float().requires_grad_()
+    if activation == 0:
+        h = torch.nn.functional.silu(f[:, :H]) * f[:, H:]
+    else:
+        h = torch.relu(f).square()
+    h.backward(dh.float())
+    torch.testing.assert_close(got, f.grad.to(torch.bfloat16).float(), rtol=1.6e-2, atol=1e-5)
+
+
+def test_combine_backward_is_exact_transpose():
+    """grad_y rows are w * grad_out in bf16 and grad_w the fp32 dots (checked in float64)."""
+    from nexttransformer_amd import ops
+    T, d, E, k = 257, 264, 12, 3
+    gen = torch.Generator().manual_seed(9)
+    ids = torch.rand(T, E, generator=gen).topk(k, dim=1).indices.int()
+    w = torch.rand(T, k, generator=gen)
+    counts, offsets, src, perm_w, cdest, cw, _ = ops.route_plan(ids.cuda(), w.cuda(), E, None,
+                                                                False)
+    y = torch.randn(T * k, d, generator=gen).to(torch.bfloat16)
+    g = torch.randn(T, d, generator=gen).to(torch.bfloat16)
+    gy, gw = ops.combine_bwd(g.cuda(), y.cuda(), ids.cuda(), cdest, cw)
+    torch.cuda.synchronize()
+    src_c, pw = src.cpu().long(), perm_w.cpu()
+    want = (pw[:, None] * g.float()[src_c]).to(torch.bfloat16)
+    assert torch.equal(gy.cpu(), want)
+    order = ids.long().argsort(-1)
+    dest_topk = torch.empty(T, k, dtype=torch.long)
+    dest_topk.scatter_(1, order, cdest.cpu().long())
+    ref = (g.double()[:, None, :] * y.double()[dest_topk]).sum(-1)
+    torch.testing.assert_close(gw.cpu().double(), ref, rtol=1e-5, atol=1e-4)

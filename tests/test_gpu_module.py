@@ -215,8 +215,12 @@ def test_module_repacks_after_in_place_update_and_casts_inputs():
         m.shared_experts.linear_fc2.weight.mul_(2.0)
         c = ffn(hidden.to(torch.bfloat16))
     assert rel_l2(c.float(), 2 * b.float()) <= 1e-2
-    with pytest.raises(RuntimeError, match="forward-only"):
-        ffn(hidden)  # gradients enabled and parameters require grad
+    # gradients enabled: the training path gives the same output and fills every .grad
+    d = ffn(hidden.to(torch.bfloat16))
+    assert torch.equal(d, c)
+    (d.float().square().sum() + ffn.last_aux).backward()
+    for name, p in m.named_parameters():
+        assert p.grad is not None and torch.isfinite(p.grad).all(), name
 
 
 def test_module_empty_batch():
