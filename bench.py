@@ -48,6 +48,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--permute-rows", action="store_true",
                    help="move token rows with the permute kernel instead of gathering in the GEMM")
+    p.add_argument("--train", action="store_true",
+                   help="time forward + backward (bf16 configs) instead of the forward")
     p.add_argument("--cpu-budget-s", type=float, default=20.0)
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy (known HBM bytes), used to "
@@ -73,6 +75,74 @@ def calibrate_copy(reps=20, nbytes=1 << 30):
     print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes,
                       "avg_launch_ms": round(ms, 5),
                       "GB_per_s": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
+
+
+def train_bench(args, case, cpu, g):
+    """Forward + backward steps (bf16 experts): the forward keeps what the backward reads, the
+    backward gets a fixed random output gradient and a unit aux-loss gradient. Prints one JSON
+    line; the per-stage split of the backward comes from a separate instrumented pass."""
+    import torch
+    from nexttransformer_amd import ops
+    if g["w1_scale"] is not None:
+        log("bench.py --train: the backward covers bf16 experts (configs 1-4)")
+        sys.exit(2)
+    dev = torch.device("cuda")
+    bf = torch.bfloat16
+    w1b, w2b = cpu["w1"].to(bf).to(dev), cpu["w2"].to(bf).to(dev)
+    sw1b = sw2b = None
+    if cpu["shared_w1"] is not None:
+        sw1b, sw2b = cpu["shared_w1"].to(bf).to(dev), cpu["shared_w2"].to(bf).to(dev)
+    bw = ops.backward_weights(w1b, w2b, sw1b, sw2b)
+    grad_out = (torch.randn(case.T, case.d, generator=torch.Generator().manual_seed(1))
+                .to(bf).to(dev))
+    grad_aux = torch.tensor([1.0, 0.0, 0.0], device=dev)
+    stream = torch.cuda.current_stream()
+
+    def step(mark_f=None, mark_b=None):
+        _, _, st = ops.moe_forward(g["x"], g["wt"], g["w1"], g["w2"], top_k=case.k,
+                                   score_fn=case.score_fn, activation=case.activation,
+                                   logit_bias=g["bias"], shared_w1=g["shared_w1"],
+                                   shared_w2=g["shared_w2"], packed=g["packed"],
+                                   want_logits=True, keep=True, mark=mark_f)
+        return ops.moe_backward(grad_out, grad_aux, g["x"], g["wt"], bw, st, top_k=case.k,
+                                score_fn=case.score_fn, activation=case.activation,
+                                mark=mark_b)
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    reps = 5
+    stage = {}
+    for _ in range(reps):
+        evs = [("start", torch.cuda.Event(enable_timing=True))]
+        evs[0][1].record(stream)
+
+        def mark(name):
+            e = torch.cuda.Event(enable_timing=True)
+            e.record(stream)
+            evs.append((name, e))
+        step(lambda n: mark("fwd_" + n), lambda n: mark("bwd_" + n))
+        torch.cuda.synchronize()
+        for (_, a), (n, b) in zip(evs, evs[1:]):
+            stage[n] = stage.get(n, 0.0) + a.elapsed_time(b) / reps
+    A = case.T * case.k
+    F = 2 * case.H if case.activation == 0 else case.H
+    up, down = 2.0 * A * case.d * F, 2.0 * A * case.H * case.d
+    # forward: up + down; backward: fc1 recompute + dgrad of both + wgrad of both
+    flops = 4 * up + 3 * down + 3 * 2.0 * case.T * case.d * case.E
+    result = {"metric": "MoE layer forward+backward tokens/s", "value": round(case.T / (ms * 1e-3), 1),
+              "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+              "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+              "vs_baseline": None, "dtype": "bf16", "data": "synthetic, seed 0",
+              "config": describe(case, args.config, False, False),
+              "layer_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+              "stages_ms": {n: round(v, 5) for n, v in stage.items()}}
+    print(json.dumps(result), flush=True)
 
 
 def gpu_inputs(case, fp8):
@@ -205,6 +275,10 @@ def main():
                                w2_scale=g["w2_scale"], shared_w1_scale=g["shared_w1_scale"],
                                shared_w2_scale=g["shared_w2_scale"],
                                permute_rows=args.permute_rows, packed=g["packed"], mark=mark)
+
+    if args.train:
+        train_bench(args, case, cpu, g)
+        return
 
     state = None
     for _ in range(max(1, args.warmup)):

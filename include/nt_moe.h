@@ -325,6 +325,20 @@ int nt_moe_act_bwd(const uint16_t* fc1, const uint16_t* grad_h, int64_t rows, in
  * {lb + z, lb, z}) is given. logits are the forward's (bias included); counts its counts.
  * Then grad Wr = grad_logits^T x and grad x += grad_logits Wr are plain GEMMs.
  */
+/*
+ * Grouped weight gradient (the expert weight gradients of the grouped FFN: autograd of the
+ * per-expert MasterLinear products, megatron_moe.py:58-78,145), bf16 MFMA, fp32 accumulation:
+ *   c[s, n, m] = sum over rows r of segment s of a[r, n] * b[row(r), m]   (bf16 [S, N, M])
+ * row(r) = b_src_row[r] when given (e.g. the gathered token rows), else r. With a = grad_y,
+ * b = h this is dW2; with a = grad_fc1, b = x and b_src_row = src_row, dW1. An empty segment's
+ * matrix is zero. N and M multiples of 128; lda, ldb multiples of 8.
+ */
+int nt_moe_grouped_wgrad_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                              int64_t b_rows, const int32_t* b_src_row,
+                              const int32_t* seg_offsets, int32_t num_segments,
+                              int64_t total_rows, int32_t N, int32_t M, uint16_t* c,
+                              nt_moe_stream_t stream);
+
 int nt_moe_router_bwd(const float* logits, const int32_t* topk_ids, const float* topk_w,
                       const float* grad_w, const int32_t* counts, int64_t T, int32_t E,
                       int32_t k, int32_t score_fn, const float* grad_aux, float aux_coeff,

@@ -242,6 +242,29 @@ int nt_moe_act_bwd(const uint16_t* fc1, const uint16_t* grad_h, int64_t rows, in
                   "act_bwd");
 }
 
+int nt_moe_grouped_wgrad_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                              int64_t b_rows, const int32_t* b_src_row,
+                              const int32_t* seg_offsets, int32_t num_segments,
+                              int64_t total_rows, int32_t N, int32_t M, uint16_t* c,
+                              nt_moe_stream_t stream) {
+  NT_REQUIRE(N > 0 && N % 128 == 0 && M > 0 && M % 128 == 0,
+             "grouped_wgrad: N and M must be positive multiples of 128, got %d, %d", N, M);
+  NT_REQUIRE(num_segments >= 1 && num_segments <= NT_MOE_MAX_SEGMENTS,
+             "grouped_wgrad: num_segments must be in [1, %d]", NT_MOE_MAX_SEGMENTS);
+  NT_REQUIRE(total_rows >= 0 && total_rows < ((int64_t)1 << 31), "grouped_wgrad: bad total_rows");
+  NT_REQUIRE(lda >= N && lda % 8 == 0 && ldb >= M && ldb % 8 == 0,
+             "grouped_wgrad: lda >= N, ldb >= M, both multiples of 8");
+  NT_REQUIRE(b_src_row ? b_rows >= 1 : b_rows >= total_rows,
+             "grouped_wgrad: b needs total_rows rows without b_src_row");
+  NT_REQUIRE(a && b && seg_offsets && c, "grouped_wgrad: null buffer");
+  NT_REQUIRE(aligned16(a) && aligned16(b) && aligned16(c),
+             "grouped_wgrad: buffers must be 16-byte aligned");
+  return launched(launch_grouped_wgrad(a, lda, b, ldb, b_rows, b_src_row, seg_offsets,
+                                       num_segments, total_rows, N, M, c,
+                                       reinterpret_cast<hipStream_t>(stream)),
+                  "grouped_wgrad");
+}
+
 int nt_moe_router_bwd(const float* logits, const int32_t* topk_ids, const float* topk_w,
                       const float* grad_w, const int32_t* counts, int64_t T, int32_t E,
                       int32_t k, int32_t score_fn, const float* grad_aux, float aux_coeff,

@@ -66,6 +66,10 @@ hipError_t launch_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_i
                           const int32_t* ranks, const int32_t* block_base,
                           int32_t* src_row, float* perm_w, int32_t* combine_dest,
                           float* combine_w, uint16_t* x_perm, hipStream_t stream);
+hipError_t launch_grouped_wgrad(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                                int64_t b_rows, const int32_t* b_src_row,
+                                const int32_t* seg_offsets, int num_segments, int64_t total_rows,
+                                int N, int M, uint16_t* c, hipStream_t stream);
 hipError_t launch_combine_bwd(const uint16_t* g, int64_t ld_g, const uint16_t* y,
                               const int32_t* topk_ids, const int32_t* combine_dest,
                               const float* combine_w, int64_t T, int d, int k, uint16_t* dy,

@@ -632,6 +632,34 @@ def _(logits, ids, weights, grad_w, counts, score_fn, grad_aux, aux_coeff, z_coe
     return torch.empty_like(logits)
 
 
+@torch.library.custom_op("ntmoe::grouped_wgrad", mutates_args=())
+def grouped_wgrad(a: Tensor, b: Tensor, b_src_row: Optional[Tensor], seg_offsets: Tensor,
+                  total_rows: int) -> Tensor:
+    """c [S, N, M] bf16: c[s] = sum over segment s's rows r of a[r]^T b[row(r)]."""
+    _on_gpu(a, b, b_src_row, seg_offsets)
+    _require(a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16 and a.dim() == 2
+             and b.dim() == 2 and a.stride(1) == 1 and b.stride(1) == 1,
+             "grouped_wgrad: a and b must be bf16 matrices with contiguous rows")
+    _require(seg_offsets.dtype == torch.int32 and seg_offsets.dim() == 1
+             and seg_offsets.is_contiguous(), "grouped_wgrad: seg_offsets must be int32 [S+1]")
+    if b_src_row is not None:
+        _require(b_src_row.dtype == torch.int32 and b_src_row.is_contiguous(),
+                 "grouped_wgrad: b_src_row must be contiguous int32")
+    S = seg_offsets.shape[0] - 1
+    N, M = a.shape[1], b.shape[1]
+    c = torch.empty(S, N, M, device=a.device, dtype=torch.bfloat16)
+    st = nat.load().nt_moe_grouped_wgrad_bf16(ptr(a), a.stride(0), ptr(b), b.stride(0),
+                                              b.shape[0], ptr(b_src_row), ptr(seg_offsets), S,
+                                              total_rows, N, M, ptr(c), _stream(a.device))
+    nat.check(st, "ntmoe::grouped_wgrad")
+    return c
+
+
+@grouped_wgrad.register_fake
+def _(a, b, b_src_row, seg_offsets, total_rows):
+    return a.new_empty(seg_offsets.shape[0] - 1, a.shape[1], b.shape[1])
+
+
 class Projection:
     """One dgrad / recompute GEMM's weights, c[r] = a_r . W_s^T with W [S, n, K] bf16: packed for
     the packed GEMM when the shape qualifies, else the plain grouped GEMM's operand."""
@@ -660,7 +688,7 @@ def backward_weights(w1, w2, shared_w1=None, shared_w2=None):
 
 def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
                  score_fn=nat.SCORE_SOFTMAX, activation=nat.ACT_SWIGLU, aux_coeff=0.01,
-                 z_coeff=0.001):
+                 z_coeff=0.001, mark=None):
     """Gradients of moe_forward (bf16 experts) for grad_out [T, d] and grad_aux [3] (or None).
 
     state: moe_forward's state from a call with want_logits=True and keep=True; bw: from
@@ -670,9 +698,12 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
     On the GPU kernels: fc1 recompute, dgrad of both projections (grouped GEMMs), the combine
     transpose and routing-weight gradient, the activation backward, the token-side sum of the
     k gradient rows (the forward's combine kernel with unit weights, shared expert first) and
-    the router backward. The router's two fp32 products and the expert weight gradients
-    (per-expert dy^T h and d_fc1^T x products) are plain library GEMMs.
+    the router backward, the expert weight gradients (grouped_wgrad: dy^T h and d_fc1^T x over
+    each expert's rows, x gathered through src_row). The router's two fp32 products are plain
+    library GEMMs, as are the weight gradients of widths that are not multiples of 128. `mark(name)` as in
+    moe_forward.
     """
+    mark = mark or (lambda name: None)
     T, d = x.shape
     E = w_router_t.shape[1]
     k = top_k
@@ -681,10 +712,15 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
     cdest, ids = state["combine_dest"], state["ids"]
     g = grad_out.to(torch.bfloat16).contiguous()
     fc1 = bw["w1"](x, src, offsets, A)
+    mark("fc1_recompute")
     gy, gw = combine_bwd(g, state["y"], ids, cdest, state["combine_w"])
+    mark("combine_bwd")
     dh = bw["w2t"](gy, None, offsets, A)
+    mark("dgrad_down")
     dfc1 = act_bwd(fc1, dh, activation)
+    mark("act_bwd")
     dxp = bw["w1t"](dfc1, None, offsets, A)
+    mark("dgrad_up")
     dxs = None
     res = dict(shared_w1=None, shared_w2=None)
     if bw["shared"] is not None:
@@ -694,24 +730,34 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
         dhs = sb["w2t"](g, None, seg, T)
         dfc1s = act_bwd(fc1s, dhs, activation)
         dxs = sb["w1t"](dfc1s, None, seg, T)
+        # one segment over all T rows: a plain library product (a single long reduction, which
+        # the grouped kernel would give to too few workgroups)
         res["shared_w1"] = (dfc1s.t() @ x).unsqueeze(0)
         res["shared_w2"] = (g.t() @ state["shared_h"]).unsqueeze(0)
+        mark("shared")
     ones = torch.ones(T, k, device=x.device, dtype=torch.float32)
     dx_e, _ = combine_aux(dxp, cdest, ones, dxs, state["prob_partial"], state["z_partial"],
                           state["counts"], 0.0, 0.0)
+    mark("dx_sum")
     dlogits = router_bwd(state["logits"], ids, state["weights"], gw, state["counts"], score_fn,
                          grad_aux, aux_coeff, z_coeff)
     res["router"] = dlogits.t() @ x.float()
     res["x"] = (dx_e.float() + dlogits @ w_router_t.t()).to(torch.bfloat16)
-    # expert weight gradients over each expert's rows (offsets read on the host)
+    mark("router_bwd")
+    # expert weight gradients over each expert's rows
     F, H = bw["w1_plain"].shape[1], bw["w2_plain"].shape[2]
-    gw1 = torch.zeros(E, F, d, device=x.device, dtype=torch.bfloat16)
-    gw2 = torch.zeros(E, d, H, device=x.device, dtype=torch.bfloat16)
-    xp = x.index_select(0, src.long())
     h = state["h"]
-    for e, (lo, hi) in enumerate(zip(offsets[:-1].tolist(), offsets[1:].tolist())):
-        if hi > lo:
-            gw1[e] = dfc1[lo:hi].t() @ xp[lo:hi]
-            gw2[e] = gy[lo:hi].t() @ h[lo:hi]
-    res["w1"], res["w2"] = gw1, gw2
+    if F % 128 == 0 and H % 128 == 0 and d % 128 == 0:
+        res["w1"] = grouped_wgrad(dfc1, x, src, offsets, A)
+        res["w2"] = grouped_wgrad(gy, h, None, offsets, A)
+    else:  # widths the grouped kernel does not tile: per-expert library products
+        gw1 = torch.zeros(E, F, d, device=x.device, dtype=torch.bfloat16)
+        gw2 = torch.zeros(E, d, H, device=x.device, dtype=torch.bfloat16)
+        xp = x.index_select(0, src.long())
+        for e, (lo, hi) in enumerate(zip(offsets[:-1].tolist(), offsets[1:].tolist())):
+            if hi > lo:
+                gw1[e] = dfc1[lo:hi].t() @ xp[lo:hi]
+                gw2[e] = gy[lo:hi].t() @ h[lo:hi]
+        res["w1"], res["w2"] = gw1, gw2
+    mark("wgrad")
     return res

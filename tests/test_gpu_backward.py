@@ -156,3 +156,28 @@ def test_combine_backward_is_exact_transpose():
     dest_topk.scatter_(1, order, cdest.cpu().long())
     ref = (g.double()[:, None, :] * y.double()[dest_topk]).sum(-1)
     torch.testing.assert_close(gw.cpu().double(), ref, rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("gather", [False, True])
+def test_grouped_wgrad_matches_float64(gather):
+    """Ragged segments (empty, shorter than one 32-row step, not a multiple of it, long)."""
+    from nexttransformer_amd import ops
+    gen = torch.Generator().manual_seed(31 + gather)
+    sizes = [0, 5, 32, 77, 300, 0, 1]
+    N, M = 256, 128
+    total = sum(sizes)
+    offsets = torch.tensor([0] + list(torch.tensor(sizes).cumsum(0)), dtype=torch.int32)
+    a = torch.randn(total, N, generator=gen).to(torch.bfloat16)
+    b_rows = 50 if gather else total
+    b = torch.randn(b_rows, M, generator=gen).to(torch.bfloat16)
+    src = torch.randint(0, b_rows, (total,), generator=gen, dtype=torch.int32) if gather else None
+    got = ops.grouped_wgrad(a.cuda(), b.cuda(), None if src is None else src.cuda(),
+                            offsets.cuda(), total).float().cpu()
+    bb = b[src.long()] if gather else b
+    for s in range(len(sizes)):
+        lo, hi = int(offsets[s]), int(offsets[s + 1])
+        ref = a[lo:hi].double().t() @ bb[lo:hi].double()
+        if hi == lo:
+            assert torch.equal(got[s], torch.zeros(N, M))
+        else:
+            torch.testing.assert_close(got[s].double(), ref, rtol=8e-3, atol=1e-2)
