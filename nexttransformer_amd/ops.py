@@ -697,7 +697,8 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
 
     On the GPU kernels: fc1 recompute, dgrad of both projections (grouped GEMMs), the combine
     transpose and routing-weight gradient, the activation backward, the token-side sum of the
-    k gradient rows (the forward's combine kernel with unit weights, shared expert first) and
+    k gradient rows (the forward's combine kernel with unit weights, the router's and the
+    shared expert's input gradients first, rounded to bf16) and
     the router backward, the expert weight gradients (grouped_wgrad: dy^T h and d_fc1^T x over
     each expert's rows, x gathered through src_row). The router's two fp32 products are plain
     library GEMMs, as are the weight gradients of widths that are not multiples of 128. `mark(name)` as in
@@ -735,15 +736,19 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
         res["shared_w1"] = (dfc1s.t() @ x).unsqueeze(0)
         res["shared_w2"] = (g.t() @ state["shared_h"]).unsqueeze(0)
         mark("shared")
-    ones = torch.ones(T, k, device=x.device, dtype=torch.float32)
-    dx_e, _ = combine_aux(dxp, cdest, ones, dxs, state["prob_partial"], state["z_partial"],
-                          state["counts"], 0.0, 0.0)
-    mark("dx_sum")
     dlogits = router_bwd(state["logits"], ids, state["weights"], gw, state["counts"], score_fn,
                          grad_aux, aux_coeff, z_coeff)
-    res["router"] = dlogits.t() @ x.float()
-    res["x"] = (dx_e.float() + dlogits @ w_router_t.t()).to(torch.bfloat16)
+    res["router"] = torch.mm(dlogits.t(), x.float())
+    # the router's and the shared expert's input gradients enter the token-side sum as its
+    # first term (the combine kernel's shared row), in bf16
+    first = torch.mm(dlogits, w_router_t.t())
+    if dxs is not None:
+        first += dxs.float()
     mark("router_bwd")
+    ones = torch.ones(T, k, device=x.device, dtype=torch.float32)
+    res["x"], _ = combine_aux(dxp, cdest, ones, first.to(torch.bfloat16), state["prob_partial"],
+                              state["z_partial"], state["counts"], 0.0, 0.0)
+    mark("dx_sum")
     # expert weight gradients over each expert's rows
     F, H = bw["w1_plain"].shape[1], bw["w2_plain"].shape[2]
     h = state["h"]
