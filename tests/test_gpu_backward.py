@@ -25,6 +25,11 @@ CASES = [
     Case("bwd-T700-d256-E32-k8-relu2-zipf", 700, 256, 32, 8, 128, activation=1, zipf_bias=1.2,
          seed=23),
     Case("bwd-T1024-d1024-E32-k4-swiglu", 1024, 1024, 32, 4, 512, seed=24),
+    # the registered T3 expert cell's widths (d 1280, ReLU^2 width 320, shared expert): widths
+    # the packed GEMM and the grouped weight-gradient kernel do not tile take the plain grouped
+    # GEMM and the per-expert library products
+    Case("bwd-T200-d1280-E16-k4-relu2-H320-shared", 200, 1280, 16, 4, 320, activation=1,
+         shared_H=320, seed=25),
 ]
 
 
