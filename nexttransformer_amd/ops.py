@@ -682,7 +682,8 @@ def backward_weights(w1, w2, shared_w1=None, shared_w2=None):
               w2_plain=w2, shared=None)
     if shared_w1 is not None:
         bw["shared"] = dict(w1=Projection(shared_w1), w1t=Projection(t(shared_w1)),
-                            w2t=Projection(t(shared_w2)))
+                            w2t=Projection(t(shared_w2)), w1_plain=shared_w1,
+                            w2_plain=shared_w2)
     return bw
 
 
@@ -709,6 +710,13 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
     E = w_router_t.shape[1]
     k = top_k
     A = T * k
+    if T == 0:
+        z = lambda t: None if t is None else torch.zeros_like(t)
+        sh = bw["shared"]
+        return dict(x=torch.zeros_like(x), router=torch.zeros(E, d, device=x.device),
+                    w1=z(bw["w1_plain"]), w2=z(bw["w2_plain"]),
+                    shared_w1=None if sh is None else z(sh["w1_plain"]),
+                    shared_w2=None if sh is None else z(sh["w2_plain"]))
     src, offsets = state["src_row"], state["offsets"]
     cdest, ids = state["combine_dest"], state["ids"]
     g = grad_out.to(torch.bfloat16).contiguous()
