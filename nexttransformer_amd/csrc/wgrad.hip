@@ -62,28 +62,31 @@ __global__ __launch_bounds__(256) void grouped_wgrad_kernel(
     // Loader: threads 0-127 move A, 128-255 move B; thread -> (8-row group rg, 8-column group cg)
     const int op = tid >> 7;
     const int lt = tid & 127;
-    const int rg = lt >> 4;        // 0..7: rows 8 rg .. 8 rg + 7 of the slab
-    const int cg = lt & 15;        // 0..15: columns 8 cg .. 8 cg + 7 of the tile
+    // rg varies fastest so a wave's eight 16-byte LDS stores per column land in eight different
+    // 16-byte bank groups (columns 8 apart map to the same group)
+    const int rg = lt & 7;         // 0..7: rows 8 rg .. 8 rg + 7 of the slab
+    const int cg = lt >> 3;        // 0..15: columns 8 cg .. 8 cg + 7 of the tile
     const uint16_t* base = op == 0 ? a + n0 + 8 * cg : b + m0 + 8 * cg;
     const int64_t ld = op == 0 ? lda : ldb;
-    auto load = [&](int64_t r0, u32x4 (&v)[8]) {
-      int64_t rows[8];
+    // Gathered B rows: the row indices of a slab are loaded one slab ahead of its data (idx), so
+    // the data loads do not wait on an index load.
+    const bool gather = op == 1 && b_src_row != nullptr;
+    int32_t idx[8];
+    auto load_idx = [&](int64_t r0) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int64_t r = r0 + 8 * rg + i;
-        rows[i] = r < hi ? r : lo;
+        idx[i] = b_src_row[r < hi ? r : lo];
       }
-      if (op == 1 && b_src_row) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          int64_t row = b_src_row[rows[i]];
-          rows[i] = row < 0 ? 0 : (row >= b_rows ? b_rows - 1 : row);
-        }
-      }
+    };
+    auto load = [&](int64_t r0, u32x4 (&v)[8]) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        v[i] = *reinterpret_cast<const u32x4*>(base + rows[i] * ld);
-        if (r0 + 8 * rg + i >= hi) v[i] = u32x4{0u, 0u, 0u, 0u};
+        const int64_t r = r0 + 8 * rg + i;
+        int64_t row = r < hi ? r : lo;
+        if (gather) row = idx[i] < 0 ? 0 : (idx[i] >= b_rows ? b_rows - 1 : idx[i]);
+        v[i] = *reinterpret_cast<const u32x4*>(base + row * ld);
+        if (r >= hi) v[i] = u32x4{0u, 0u, 0u, 0u};
       }
     };
     auto store = [&](int buf, const u32x4 (&v)[8]) {
@@ -103,13 +106,16 @@ __global__ __launch_bounds__(256) void grouped_wgrad_kernel(
     };
 
     u32x4 v[8];
+    if (gather) load_idx(lo);
     load(lo, v);
+    if (gather && lo + kWK < hi) load_idx(lo + kWK);
     store(0, v);
     __syncthreads();
     int buf = 0;
     for (int64_t r0 = lo; r0 < hi; r0 += kWK) {
       const bool more = r0 + kWK < hi;
       if (more) load(r0 + kWK, v);
+      if (gather && r0 + 2 * kWK < hi) load_idx(r0 + 2 * kWK);
       const uint16_t* sa = lds[buf][0];
       const uint16_t* sb = lds[buf][1];
 #pragma unroll
