@@ -746,7 +746,12 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
         mark("shared")
     dlogits = router_bwd(state["logits"], ids, state["weights"], gw, state["counts"], score_fn,
                          grad_aux, aux_coeff, z_coeff)
-    res["router"] = torch.mm(dlogits.t(), x.float())
+    # dWr = dlogits^T x in fp32: a long reduction (K = T) over a thin output, which the library
+    # tiles poorly as one product; 16 batched partial products summed in a fixed order are ~4x
+    # faster (T split into equal chunks; fewer when T is not a multiple of 16)
+    chunks = next(c for c in (16, 8, 4, 2, 1) if T % c == 0)
+    res["router"] = torch.bmm(dlogits.view(chunks, T // chunks, E).transpose(1, 2).contiguous(),
+                              x.float().view(chunks, T // chunks, d)).sum(0)
     # the router's and the shared expert's input gradients enter the token-side sum as its
     # first term (the combine kernel's shared row), in bf16
     first = torch.mm(dlogits, w_router_t.t())
