@@ -214,6 +214,20 @@ int nt_moe_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int64_t a_r
                                     int32_t epilogue, uint16_t* c, nt_moe_stream_t stream);
 
 /*
+ * nt_moe_grouped_gemm_bf16_packed with the SWIGLU or RELU2 epilogue that also stores the
+ * epilogue's input, the fc1 pre-activations, to pre: bf16 [total_rows, 2 n_out] (SwiGLU: gate
+ * then value) or [total_rows, n_out] (ReLU^2), rounded from the same fp32 accumulators. For a
+ * training forward whose backward needs them (nt_moe_act_bwd); otherwise the backward
+ * recomputes them with an EPI_NONE launch. 16-byte aligned; total_rows * width * 2 < 2^31.
+ */
+int nt_moe_grouped_gemm_bf16_packed_keep(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                         const int32_t* src_row, const int32_t* seg_offsets,
+                                         int32_t num_segments, int64_t total_rows,
+                                         const uint16_t* w_packed, int32_t K, int32_t n_out,
+                                         int32_t epilogue, uint16_t* c, uint16_t* pre,
+                                         nt_moe_stream_t stream);
+
+/*
  * FP8 path (OCP E4M3FN, the format of gfx950's matrix cores). The reference has no fp8
  * experts -- its MasterLinear runs bf16/fp32 matmuls (megatron_moe.py:58-78) -- so these entry
  * points are the fp8 variant of the same expert computation (megatron_moe.py:145) for the

@@ -36,6 +36,8 @@ SIGNATURES = {
                               _p, _p]),
     "nt_moe_route_plan": (_i32, [_p, _i64, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _sz, _p,
                                  _p, _p, _p, _p, _p]),
+    "nt_moe_grouped_gemm_bf16_packed_keep": (_i32, [_p, _i64, _i64, _p, _p, _i32, _i64, _p, _i32,
+                                                    _i32, _i32, _p, _p, _p]),
     "nt_moe_grouped_wgrad_bf16": (_i32, [_p, _i64, _p, _i64, _i64, _p, _p, _i32, _i64, _i32, _i32,
                                          _p, _p]),
     "nt_moe_combine_bwd": (_i32, [_p, _i64, _p, _p, _p, _p, _i64, _i32, _i32, _p, _p, _p]),

@@ -397,11 +397,10 @@ int nt_moe_pack_expert_weights_bf16(const uint16_t* w, int64_t num_segments, int
   return launched(err, "pack_expert_weights_bf16");
 }
 
-int nt_moe_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows,
-                                    const int32_t* src_row, const int32_t* seg_offsets,
-                                    int32_t num_segments, int64_t total_rows,
-                                    const uint16_t* w_packed, int32_t K, int32_t n_out,
-                                    int32_t epilogue, uint16_t* c, nt_moe_stream_t stream) {
+static int check_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows, const int32_t* src_row,
+                        const int32_t* seg_offsets, int32_t num_segments, int64_t total_rows,
+                        const uint16_t* w_packed, int32_t K, int32_t n_out, int32_t epilogue,
+                        uint16_t* c) {
   NT_REQUIRE(K >= packed_gemm_min_k() && K % 128 == 0,
              "grouped_gemm_packed: K must be a multiple of 128 and >= %d, got %d",
              packed_gemm_min_k(), K);
@@ -423,12 +422,46 @@ int nt_moe_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int64_t a_r
              "grouped_gemm_packed: a, w_packed and c must be 16-byte aligned");
   int rc = check_gemm_extent(a_rows, ld_a, 0, 0);
   if (rc) return rc;
+  return 0;
+}
+
+int nt_moe_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                    const int32_t* src_row, const int32_t* seg_offsets,
+                                    int32_t num_segments, int64_t total_rows,
+                                    const uint16_t* w_packed, int32_t K, int32_t n_out,
+                                    int32_t epilogue, uint16_t* c, nt_moe_stream_t stream) {
+  int rc = check_packed(a, ld_a, a_rows, src_row, seg_offsets, num_segments, total_rows,
+                        w_packed, K, n_out, epilogue, c);
+  if (rc) return rc;
   if (total_rows == 0) return ok();
   hipError_t err = launch_grouped_gemm_bf16_packed(a, ld_a, a_rows, src_row, seg_offsets,
                                                    num_segments, total_rows, w_packed, K, n_out,
                                                    epilogue, c,
                                                    reinterpret_cast<hipStream_t>(stream));
   return launched(err, "grouped_gemm_bf16_packed");
+}
+
+int nt_moe_grouped_gemm_bf16_packed_keep(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                         const int32_t* src_row, const int32_t* seg_offsets,
+                                         int32_t num_segments, int64_t total_rows,
+                                         const uint16_t* w_packed, int32_t K, int32_t n_out,
+                                         int32_t epilogue, uint16_t* c, uint16_t* pre,
+                                         nt_moe_stream_t stream) {
+  NT_REQUIRE(epilogue == NT_MOE_EPI_SWIGLU || epilogue == NT_MOE_EPI_RELU2,
+             "grouped_gemm_packed_keep: the epilogue must be SWIGLU or RELU2, got %d", epilogue);
+  int rc = check_packed(a, ld_a, a_rows, src_row, seg_offsets, num_segments, total_rows,
+                        w_packed, K, n_out, epilogue, c);
+  if (rc) return rc;
+  const int64_t pw = epilogue == NT_MOE_EPI_SWIGLU ? 2 * (int64_t)n_out : n_out;
+  NT_REQUIRE(total_rows * pw * 2 < ((int64_t)1 << 31),
+             "grouped_gemm_packed_keep: the pre-activations must stay below 2 GiB");
+  NT_REQUIRE(pre && aligned16(pre), "grouped_gemm_packed_keep: pre must be a 16-byte aligned buffer");
+  if (total_rows == 0) return ok();
+  return launched(launch_grouped_gemm_bf16_packed_keep(a, ld_a, a_rows, src_row, seg_offsets,
+                                                       num_segments, total_rows, w_packed, K,
+                                                       n_out, epilogue, c, pre,
+                                                       reinterpret_cast<hipStream_t>(stream)),
+                  "grouped_gemm_packed_keep");
 }
 
 int nt_moe_quantize_fp8_rowwise(const uint16_t* x, int64_t ld_x, int64_t rows, int32_t d,

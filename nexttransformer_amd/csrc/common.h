@@ -66,6 +66,12 @@ hipError_t launch_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_i
                           const int32_t* ranks, const int32_t* block_base,
                           int32_t* src_row, float* perm_w, int32_t* combine_dest,
                           float* combine_w, uint16_t* x_perm, hipStream_t stream);
+hipError_t launch_grouped_gemm_bf16_packed_keep(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                                const int32_t* src_row,
+                                                const int32_t* seg_offsets, int num_segments,
+                                                int64_t total_rows, const uint16_t* wp, int K,
+                                                int n_out, int epilogue, uint16_t* c,
+                                                uint16_t* pre, hipStream_t stream);
 hipError_t launch_grouped_wgrad(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                                 int64_t b_rows, const int32_t* b_src_row,
                                 const int32_t* seg_offsets, int num_segments, int64_t total_rows,

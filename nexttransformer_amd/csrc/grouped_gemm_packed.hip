@@ -117,11 +117,14 @@ struct Tile {
   int s, nt, m0, seg_end;
 };
 
-template <int EPI, bool GATHER, int WAVES>
+// KEEP: also store the epilogue's input (the fc1 pre-activations: SwiGLU gate then value, 2 n_out
+// wide, or the ReLU^2 input, n_out wide) to Pre, for a backward pass.
+template <int EPI, bool GATHER, int WAVES, bool KEEP = false>
 __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
     const uint16_t* __restrict__ A, int64_t ld_a, const int32_t* __restrict__ src_row,
     const int32_t* __restrict__ seg_offsets, int S, int total_rows, int64_t a_rows,
-    const uint16_t* __restrict__ Wp, int K, int n_out, uint16_t* __restrict__ Cout) {
+    const uint16_t* __restrict__ Wp, int K, int n_out, uint16_t* __restrict__ Cout,
+    uint16_t* __restrict__ Pre) {
   using Gm = Geo<WAVES>;
   constexpr int kBM = Gm::kBM, kWaves = Gm::kWaves, kAQ = Gm::kAQ, kStage = Gm::kStage;
   constexpr int kWB = Gm::kWB, kNJ = Gm::kNJ, kIdxWaves = Gm::kIdxWaves;
@@ -380,6 +383,11 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
 
   const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       Cout, 0, (int)((int64_t)total_rows * n_out * 2), kBufferWord3);
+  constexpr int kPreW = EPI == NT_MOE_EPI_SWIGLU ? 2 : 1;  // pre-activation width / n_out
+  __amdgpu_buffer_rsrc_t pre_rsrc = out_rsrc;
+  if constexpr (KEEP)
+    pre_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        Pre, 0, (int)((int64_t)total_rows * kPreW * n_out * 2), kBufferWord3);
 
   // ---- consumer ---------------------------------------------------------------------------
   Tile ct = pt;
@@ -524,6 +532,20 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
                                     ? (uint32_t)(((int64_t)m * n_out + col) * 2)
                                     : 0x80000000u;
           __builtin_amdgcn_raw_buffer_store_b128(packed, out_rsrc, voff, 0, 0);
+          if constexpr (KEEP) {
+            const bool ok = row_ok && nb < NB && col < n_out;
+            const int64_t prow = (int64_t)m * kPreW * n_out;
+#pragma unroll
+            for (int h = 0; h < (EPI == NT_MOE_EPI_SWIGLU ? 2 : 1); ++h) {
+              const int e0 = EPI == NT_MOE_EPI_SWIGLU ? 8 * h : 8 * st;
+              const u32x4 pv = {pack_bf16x2(acc[rb][j][e0], acc[rb][j][e0 + 1]),
+                                pack_bf16x2(acc[rb][j][e0 + 2], acc[rb][j][e0 + 3]),
+                                pack_bf16x2(acc[rb][j][e0 + 4], acc[rb][j][e0 + 5]),
+                                pack_bf16x2(acc[rb][j][e0 + 6], acc[rb][j][e0 + 7])};
+              const uint32_t poff = ok ? (uint32_t)((prow + h * n_out + col) * 2) : 0x80000000u;
+              __builtin_amdgcn_raw_buffer_store_b128(pv, pre_rsrc, poff, 0, 0);
+            }
+          }
         }
       }
     }
@@ -559,10 +581,11 @@ __global__ __launch_bounds__(256) void pack_weights_kernel(const uint16_t* __res
       *reinterpret_cast<const u32x4*>(w + (s * R + row) * (int64_t)K + k0);
 }
 
-template <int EPI, bool GATHER, int WAVES>
+template <int EPI, bool GATHER, int WAVES, bool KEEP = false>
 hipError_t launch_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows, const int32_t* src_row,
                          const int32_t* seg_offsets, int S, int64_t total_rows,
-                         const uint16_t* wp, int K, int n_out, uint16_t* c, hipStream_t stream) {
+                         const uint16_t* wp, int K, int n_out, uint16_t* c, hipStream_t stream,
+                         uint16_t* pre = nullptr) {
   using Gm = Geo<WAVES>;
   const int NB = (EPI == NT_MOE_EPI_SWIGLU ? 2 * n_out : n_out) / 32;
   const int64_t n_tiles = (NB + kTileBlocks - 1) / kTileBlocks;
@@ -571,11 +594,11 @@ hipError_t launch_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows, const 
   if (upper < grid) grid = upper;
   grid = ((grid + 7) / 8) * 8;
   const size_t lds = Gm::lds(S);
-  auto kern = grouped_gemm_packed_kernel<EPI, GATHER, WAVES>;
+  auto kern = grouped_gemm_packed_kernel<EPI, GATHER, WAVES, KEEP>;
   hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(Gm::kThreads), lds, stream, a, ld_a,
-                     src_row, seg_offsets, S, (int)total_rows, a_rows, wp, K, n_out, c);
+                     src_row, seg_offsets, S, (int)total_rows, a_rows, wp, K, n_out, c, pre);
   return hipGetLastError();
 }
 
@@ -628,6 +651,27 @@ hipError_t launch_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int6
   }
 #undef NT_P
 #undef NT_PW
+}
+
+hipError_t launch_grouped_gemm_bf16_packed_keep(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                                const int32_t* src_row,
+                                                const int32_t* seg_offsets, int num_segments,
+                                                int64_t total_rows, const uint16_t* wp, int K,
+                                                int n_out, int epilogue, uint16_t* c,
+                                                uint16_t* pre, hipStream_t stream) {
+  if (total_rows == 0) return hipSuccess;
+#define NT_PK(EPI)                                                                          \
+  return src_row ? launch_packed<EPI, true, 4, true>(a, ld_a, a_rows, src_row, seg_offsets, \
+                                                     num_segments, total_rows, wp, K, n_out, \
+                                                     c, stream, pre)                         \
+                 : launch_packed<EPI, false, 4, true>(a, ld_a, a_rows, src_row, seg_offsets, \
+                                                      num_segments, total_rows, wp, K, n_out, \
+                                                      c, stream, pre)
+  if (epilogue == NT_MOE_EPI_SWIGLU) {
+    NT_PK(NT_MOE_EPI_SWIGLU);
+  }
+  NT_PK(NT_MOE_EPI_RELU2);
+#undef NT_PK
 }
 
 }  // namespace ntmoe

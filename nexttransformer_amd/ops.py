@@ -289,6 +289,44 @@ def _(a, src_row, seg_offsets, w_packed, epilogue, total_rows):
     return a.new_empty((total_rows, rows // 2 if epilogue == nat.EPI_SWIGLU else rows))
 
 
+@torch.library.custom_op("ntmoe::grouped_gemm_packed_keep", mutates_args=())
+def grouped_gemm_packed_keep(a: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor,
+                             w_packed: Tensor, epilogue: int,
+                             total_rows: int) -> tuple[Tensor, Tensor]:
+    """(c, pre): grouped_gemm_packed with the SwiGLU / ReLU^2 epilogue, plus the epilogue's input
+    (the fc1 pre-activations, [rows, 2 n_out] or [rows, n_out]) for the backward."""
+    _on_gpu(a, src_row, seg_offsets, w_packed)
+    _require(epilogue in (nat.EPI_SWIGLU, nat.EPI_RELU2),
+             "grouped_gemm_packed_keep: the epilogue must be SWIGLU or RELU2")
+    _require(a.dtype == torch.bfloat16 and a.dim() == 2 and a.stride(1) == 1,
+             "grouped_gemm_packed_keep: a must be bf16 [*, K] with contiguous rows")
+    _require(w_packed.dtype == torch.bfloat16 and w_packed.dim() == 3 and w_packed.is_contiguous(),
+             "grouped_gemm_packed_keep: w_packed must be contiguous bf16 [S, rows, K]")
+    S, rows, K = w_packed.shape
+    n_out = rows // 2 if epilogue == nat.EPI_SWIGLU else rows
+    _require(a.shape[1] == K, "grouped_gemm_packed_keep: a and w disagree on K")
+    _require(seg_offsets.dtype == torch.int32 and seg_offsets.shape == (S + 1,)
+             and seg_offsets.is_contiguous(),
+             "grouped_gemm_packed_keep: seg_offsets must be int32 [S+1]")
+    if src_row is not None:
+        _require(src_row.dtype == torch.int32 and src_row.is_contiguous(),
+                 "grouped_gemm_packed_keep: src_row must be contiguous int32")
+    c = torch.empty(total_rows, n_out, device=a.device, dtype=torch.bfloat16)
+    pre = torch.empty(total_rows, rows, device=a.device, dtype=torch.bfloat16)
+    st = nat.load().nt_moe_grouped_gemm_bf16_packed_keep(
+        ptr(a), a.stride(0), a.shape[0], ptr(src_row), ptr(seg_offsets), S, total_rows,
+        ptr(w_packed), K, n_out, epilogue, ptr(c), ptr(pre), _stream(a.device))
+    nat.check(st, "ntmoe::grouped_gemm_packed_keep")
+    return c, pre
+
+
+@grouped_gemm_packed_keep.register_fake
+def _(a, src_row, seg_offsets, w_packed, epilogue, total_rows):
+    S, rows, K = w_packed.shape
+    n_out = rows // 2 if epilogue == nat.EPI_SWIGLU else rows
+    return (a.new_empty(total_rows, n_out), a.new_empty(total_rows, rows))
+
+
 # ---------------------------------------------------------------------------------------------
 # fp8 (OCP e4m3fn bytes held in uint8 tensors)
 
@@ -472,7 +510,8 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
     h are then quantised per row and both projections run on the fp8 grouped GEMM.
     `mark(name)`, when given, is called after each stage is enqueued (used to place timing
     events on the stream). keep (bf16 experts): the state also holds what moe_backward reads
-    (h, y, the shared expert's h, the router's aux partials).
+    (h, y, the shared expert's h, the router's aux partials and, with packed weights, the fc1
+    pre-activations from the up projection's launch).
     """
     T = x.shape[0]
     E = w_router_t.shape[1]
@@ -520,8 +559,11 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
                      x_scale=xs)
         return out, aux, state
     gemm = grouped_gemm_packed if packed else grouped_gemm
+    fc1 = None
     if permute_rows:
         h = gemm(x_perm, None, offsets, w1, up_epi, A)
+    elif packed and keep:  # the backward's fc1 pre-activations from the same launch
+        h, fc1 = grouped_gemm_packed_keep(x, src, offsets, w1, up_epi, A)
     else:
         h = gemm(x, src, offsets, w1, up_epi, A)
     mark("gemm_up")
@@ -538,7 +580,7 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
     state = dict(logits=logits, ids=ids, weights=w, counts=counts, offsets=offsets, src_row=src,
                  perm_w=perm_w, combine_dest=cdest, combine_w=cw)
     if keep:
-        state.update(h=h, y=y, shared_h=hs, prob_partial=pp, z_partial=zp)
+        state.update(h=h, y=y, shared_h=hs, prob_partial=pp, z_partial=zp, fc1=fc1)
     return out, aux, state
 
 
@@ -720,7 +762,9 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
     src, offsets = state["src_row"], state["offsets"]
     cdest, ids = state["combine_dest"], state["ids"]
     g = grad_out.to(torch.bfloat16).contiguous()
-    fc1 = bw["w1"](x, src, offsets, A)
+    fc1 = state.get("fc1")
+    if fc1 is None:  # not kept by the forward: recompute the pre-activations
+        fc1 = bw["w1"](x, src, offsets, A)
     mark("fc1_recompute")
     gy, gw = combine_bwd(g, state["y"], ids, cdest, state["combine_w"])
     mark("combine_bwd")

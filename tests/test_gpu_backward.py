@@ -84,8 +84,11 @@ def reference_grads(x, wr, bias, w1, w2, sw1, sw2, ids, G, g_aux, case, aux_coef
     return [t.grad for t in params]
 
 
+@pytest.mark.parametrize("packed", [False, True], ids=["plain", "packed"])
 @pytest.mark.parametrize("case", CASES, ids=lambda c: c.name)
-def test_backward_matches_fp32_autograd(case):
+def test_backward_matches_fp32_autograd(case, packed):
+    """packed: the forward runs the packed GEMMs and keeps the fc1 pre-activations from the up
+    projection's launch (the module's training path); plain: the backward recomputes them."""
     from nexttransformer_amd import _native as nat, ops
     cpu = make_inputs(case)
     dev = torch.device("cuda")
@@ -99,10 +102,22 @@ def test_backward_matches_fp32_autograd(case):
     sw1b = sw2b = None
     if cpu["shared_w1"] is not None:
         sw1b, sw2b = cpu["shared_w1"].to(bf).to(dev), cpu["shared_w2"].to(bf).to(dev)
-    out, aux, state = ops.moe_forward(x, wr_t, w1b, w2b, top_k=case.k, score_fn=case.score_fn,
-                                      activation=case.activation, aux_coeff=aux_coeff,
-                                      z_coeff=z_coeff, logit_bias=bias, shared_w1=sw1b,
-                                      shared_w2=sw2b, want_logits=True, keep=True)
+    fw = dict(w1=w1b, w2=w2b, shared_w1=sw1b, shared_w2=sw2b)
+    if packed:
+        up = nat.EPI_SWIGLU if case.activation == 0 else nat.EPI_RELU2
+        F = w1b.shape[1]
+        if not (ops.packable(case.d, F // (2 if case.activation == 0 else 1), up)
+                and ops.packable(case.H, case.d, nat.EPI_NONE)
+                and (sw1b is None or ops.packable(case.shared_H, case.d, nat.EPI_NONE))):
+            pytest.skip("widths the packed GEMM does not take")
+        fw = {n: None if w is None else ops.pack_expert_weights(w, up if "1" in n else nat.EPI_NONE)
+              for n, w in fw.items()}
+    out, aux, state = ops.moe_forward(x, wr_t, fw["w1"], fw["w2"], top_k=case.k,
+                                      score_fn=case.score_fn, activation=case.activation,
+                                      aux_coeff=aux_coeff, z_coeff=z_coeff, logit_bias=bias,
+                                      shared_w1=fw["shared_w1"], shared_w2=fw["shared_w2"],
+                                      want_logits=True, keep=True, packed=packed)
+    assert (state["fc1"] is not None) == packed
     gen = torch.Generator().manual_seed(case.seed + 7)
     G = torch.randn(case.T, case.d, generator=gen)
     grad_aux = torch.tensor([g_aux, 0.0, 0.0], device=dev)
@@ -186,3 +201,27 @@ def test_grouped_wgrad_matches_float64(gather):
             assert torch.equal(got[s], torch.zeros(N, M))
         else:
             torch.testing.assert_close(got[s].double(), ref, rtol=8e-3, atol=1e-2)
+
+
+@pytest.mark.parametrize("activation", [0, 1])
+def test_kept_pre_activations_equal_a_recompute(activation):
+    """The keep launch's h equals the plain packed launch's, and its pre-activations equal an
+    EPI_NONE launch over the same rows, bit for bit (same fp32 accumulators, one rounding)."""
+    from nexttransformer_amd import _native as nat, ops
+    gen = torch.Generator().manual_seed(41 + activation)
+    E, d, H, T = 8, 512, 256, 700
+    F = 2 * H if activation == 0 else H
+    up = nat.EPI_SWIGLU if activation == 0 else nat.EPI_RELU2
+    w1 = (torch.randn(E, F, d, generator=gen) * 0.05).to(torch.bfloat16).cuda()
+    x = torch.randn(T, d, generator=gen).to(torch.bfloat16).cuda()
+    sizes = torch.tensor([0, 130, 1, 512, 77, 0, 300, 380])
+    offsets = torch.cat([torch.zeros(1), sizes.cumsum(0)]).int().cuda()
+    A = int(sizes.sum())
+    src = torch.randint(0, T, (A,), generator=gen, dtype=torch.int32).cuda()
+    h, pre = ops.grouped_gemm_packed_keep(x, src, offsets, ops.pack_expert_weights(w1, up), up, A)
+    h_ref = ops.grouped_gemm_packed(x, src, offsets, ops.pack_expert_weights(w1, up), up, A)
+    pre_ref = ops.grouped_gemm_packed(x, src, offsets, ops.pack_expert_weights(w1, nat.EPI_NONE),
+                                      nat.EPI_NONE, A)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h_ref)
+    assert torch.equal(pre, pre_ref)
