@@ -97,6 +97,28 @@ def test_gemm_argument_errors_are_einval(lib):
     assert st == nat.NT_MOE_EINVAL and "H must be" in lib.nt_moe_last_error().decode()
 
 
+def test_backward_argument_errors_are_einval(lib):
+    """The backward entry points validate shapes before touching any buffer."""
+    from nexttransformer_amd import _native as nat
+    st = lib.nt_moe_combine_bwd(None, 100, None, None, None, None, 4, 100, 2, None, None, None)
+    assert st == nat.NT_MOE_EINVAL and "d must be" in lib.nt_moe_last_error().decode()
+    st = lib.nt_moe_combine_bwd(None, 64, None, None, None, None, 4, 64, 9, None, None, None)
+    assert st == nat.NT_MOE_EINVAL and "top-k" in lib.nt_moe_last_error().decode()
+    st = lib.nt_moe_act_bwd(None, None, 4, 12, nat.ACT_SWIGLU, None, None)
+    assert st == nat.NT_MOE_EINVAL and "H must be" in lib.nt_moe_last_error().decode()
+    st = lib.nt_moe_act_bwd(None, None, 4, 16, 7, None, None)
+    assert st == nat.NT_MOE_EINVAL and "activation" in lib.nt_moe_last_error().decode()
+    st = lib.nt_moe_router_bwd(None, None, None, None, None, 4, 300, 2, 0, None, 0.01, 0.001,
+                               None, None)
+    assert st == nat.NT_MOE_EINVAL and "E must be" in lib.nt_moe_last_error().decode()
+    st = lib.nt_moe_grouped_wgrad_bf16(None, 256, None, 256, 8, None, None, 1, 8, 256, 96, None,
+                                       None)
+    assert st == nat.NT_MOE_EINVAL and "multiples of 128" in lib.nt_moe_last_error().decode()
+    st = lib.nt_moe_grouped_gemm_bf16_packed_keep(None, 256, 8, None, None, 1, 8, None, 256, 64,
+                                                  nat.EPI_NONE, None, None, None)
+    assert st == nat.NT_MOE_EINVAL and "SWIGLU or RELU2" in lib.nt_moe_last_error().decode()
+
+
 def test_ops_reject_cpu_tensors():
     from nexttransformer_amd import ops
     x = torch.zeros(4, 64, dtype=torch.bfloat16)
@@ -104,6 +126,10 @@ def test_ops_reject_cpu_tensors():
         ops.router(x, torch.zeros(64, 4), None, 2, 0, False)
     with pytest.raises(ValueError, match="GPU only"):
         ops.route_plan(torch.zeros(4, 2, dtype=torch.int32), torch.zeros(4, 2), 4, None, False)
+    with pytest.raises(ValueError, match="GPU only"):
+        ops.act_bwd(torch.zeros(4, 32, dtype=torch.bfloat16), torch.zeros(4, 16, dtype=torch.bfloat16), 0)
+    with pytest.raises(ValueError, match="GPU only"):
+        ops.grouped_wgrad(x, x, None, torch.zeros(2, dtype=torch.int32), 4)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
