@@ -135,13 +135,22 @@ def train_bench(args, case, cpu, g):
     up, down = 2.0 * A * case.d * F, 2.0 * A * case.H * case.d
     # forward: up + down; backward: fc1 recompute + dgrad of both + wgrad of both
     flops = 4 * up + 3 * down + 3 * 2.0 * case.T * case.d * case.E
+    # the backward's dominant kernel: the two expert weight gradients (dW1: up-sized, dW2:
+    # down-sized), timed by the instrumented pass's events around them
+    wg_ms = stage.get("bwd_wgrad", 0.0)
+    wg_tflops = (up + down) / (wg_ms * 1e-3) / 1e12 if wg_ms > 0 else None
     result = {"metric": "MoE layer forward+backward tokens/s", "value": round(case.T / (ms * 1e-3), 1),
               "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
               "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
               "vs_baseline": None, "dtype": "bf16", "data": "synthetic, seed 0",
               "config": describe(case, args.config, False, False),
               "layer_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
-              "stages_ms": {n: round(v, 5) for n, v in stage.items()}}
+              "stages_ms": {n: round(v, 5) for n, v in stage.items()},
+              "roofline": None if wg_tflops is None else {
+                  "kernel": "grouped_wgrad_kernel (dW1 + dW2)", "bound": "mfma",
+                  "achieved": round(wg_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                  "frac": round(wg_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                  "flop_per_step": up + down, "ms_per_step": round(wg_ms, 5)}}
     print(json.dumps(result), flush=True)
 
 
