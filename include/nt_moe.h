@@ -1,5 +1,5 @@
 /*
- * nt_moe.h -- C ABI of the MI355X (gfx950) mixture-of-experts layer forward.
+ * nt_moe.h -- C ABI of the MI355X (gfx950) mixture-of-experts layer (forward and backward).
  *
  * One shared library, libnt_moe.so, exports these entry points. Every entry point
  *   - returns an int status: NT_MOE_OK (0) or a negative NT_MOE_E* code;

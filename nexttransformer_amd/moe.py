@@ -20,8 +20,10 @@ block scales and per-row quantised activations), repacked into [E, rows, cols] s
 a master changes (tracked by the tensors' version counters, which in-place optimizer updates
 bump).
 
-The HIP path is forward-only: a call that would need gradients raises RuntimeError instead of
-returning a result without a graph. There is no CPU path.
+Under autograd the layer runs its training path (_MoETrain: the forward keeps what the HIP
+backward reads, and the gradients reach hidden and every fp32 master) for bf16 experts whose
+widths are multiples of 64; other configurations raise RuntimeError there instead of returning a
+result without a graph. There is no CPU path.
 """
 import math
 
