@@ -216,9 +216,10 @@ int nt_moe_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int64_t a_r
 /*
  * nt_moe_grouped_gemm_bf16_packed with the SWIGLU or RELU2 epilogue that also stores the
  * epilogue's input, the fc1 pre-activations, to pre: bf16 [total_rows, 2 n_out] (SwiGLU: gate
- * then value) or [total_rows, n_out] (ReLU^2), rounded from the same fp32 accumulators. For a
- * training forward whose backward needs them (nt_moe_act_bwd); otherwise the backward
- * recomputes them with an EPI_NONE launch. 16-byte aligned; total_rows * width * 2 < 2^31.
+ * then value) or [total_rows, n_out] (ReLU^2), rounded from the same fp32 accumulators: what
+ * autograd saves from the fc1 product and activation for the backward (megatron_moe.py:23-24,
+ * 58-78; lm.py:29-35), read by nt_moe_act_bwd; otherwise the backward recomputes them with an
+ * EPI_NONE launch. 16-byte aligned; total_rows * width * 2 < 2^31.
  */
 int nt_moe_grouped_gemm_bf16_packed_keep(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                                          const int32_t* src_row, const int32_t* seg_offsets,
