@@ -17,8 +17,9 @@ written. The average launch duration is measured with HIP events recorded on the
 around every launch inside the timed region. `traffic` (HBM bytes per launch) comes from the
 rocprofv3 FETCH_SIZE / WRITE_SIZE summary in profiles/traffic.json, when present.
 
-cpu_baseline: the CPU oracle (a restatement of the reference's eager per-expert PyTorch loop,
-fp32) timed on this host's cores on the same workload, on rank 0 only.
+cpu_baseline: the reference's eager CPU layer restated with torch's own ops (oracle/, the
+RoutedFFN loop of reference_blocks.py:35-45 in fp32) timed on this host on the same workload,
+with every core of the affinity mask and with one thread.
 """
 import argparse
 import json
@@ -50,7 +51,7 @@ def parse():
                    help="move token rows with the permute kernel instead of gathering in the GEMM")
     p.add_argument("--train", action="store_true",
                    help="time forward + backward (bf16 configs) instead of the forward")
-    p.add_argument("--cpu-budget-s", type=float, default=20.0)
+    p.add_argument("--cpu-budget-s", type=float, default=30.0)
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy (known HBM bytes), used to "
                         "scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
@@ -196,8 +197,13 @@ def gpu_inputs(case, fp8):
 
 
 def layer_flops(case):
-    from oracle.moe_oracle import tflops
-    return tflops(case.T, case.d, case.E, case.k, case.H, case.shared_H)
+    """Algorithmic FLOP of one forward: router 2 T d E + routed experts 2 (T k) d F + 2 (T k) H d
+    (F = 2H for SwiGLU, H for ReLU^2) + the shared expert's 2 T d Fs + 2 T Hs d."""
+    F = 2 * case.H if case.activation == 0 else case.H
+    Fs = 2 * case.shared_H if case.activation == 0 else case.shared_H
+    A = case.T * case.k
+    return (2 * case.T * case.d * case.E + 2 * A * case.d * (F + case.H)
+            + 2 * case.T * case.d * (Fs + case.shared_H))
 
 
 def load_traffic(case_key):
@@ -211,31 +217,58 @@ def load_traffic(case_key):
 
 
 def cpu_baseline(case, cpu, budget_s):
-    """The oracle's eager per-expert fp32 forward (reference semantics) on the host cores."""
+    """The reference's eager CPU layer (torch ops: F.linear router, topk, softmax over the
+    selected, per-expert torch.where / index_add loop, shared expert; fp32) timed on the host:
+    with every core of this process's affinity mask and with one thread (the reference CI's
+    OMP_NUM_THREADS=1). Median of up to 5 runs after 2 warm-ups per thread count. The sample is
+    the full workload when a run fits the budget, else its first T' tokens (scaled to tokens/s)."""
     import torch
     from oracle import moe_oracle as orc
-    threads = min(len(os.sched_getaffinity(0)), 16)
-    torch.set_num_threads(threads)
     weights = orc.Weights(router=cpu["router"], w1=cpu["w1"], w2=cpu["w2"],
                           shared_w1=None if cpu["shared_w1"] is None else cpu["shared_w1"][0],
                           shared_w2=None if cpu["shared_w2"] is None else cpu["shared_w2"][0],
                           bias=cpu["bias"])
-    x = cpu["x"]
+    threads_all = len(os.sched_getaffinity(0))
+    before = torch.get_num_threads()
 
-    def run():
+    def measure(threads, tokens, share):
+        torch.set_num_threads(threads)
+        x = cpu["x"][:tokens]
+
+        def run():
+            t0 = time.perf_counter()
+            orc.reference_eager_forward(x, weights, case.k, score_fn=case.score_fn,
+                                        activation=case.activation)
+            return time.perf_counter() - t0
+        first = run()
+        # the second warm-up, then as many timed runs (<= 5) as this thread count's share allows
+        reps = max(1, min(5, int((share - 2 * first) / max(first, 1e-3))))
+        run()
+        times = sorted(run() for _ in range(reps))
+        med = times[len(times) // 2]
+        return dict(value=round(tokens / med, 1), unit="tokens/s", cores=threads,
+                    ms_per_sample=round(med * 1e3, 3), sample_tokens=tokens, runs=reps)
+    try:
+        multi = measure(threads_all, case.T, budget_s / 3)
+        # one thread: size the sample so that one run takes about 1/8 of its share
+        torch.set_num_threads(1)
+        probe = min(case.T, 1024)
         t0 = time.perf_counter()
-        orc.moe_forward(x, weights, case.k, score_fn=case.score_fn, activation=case.activation,
-                        router="reference")
-        return time.perf_counter() - t0
-
-    first = run()  # warm-up, also sizes the sample
-    reps = max(1, min(5, int(budget_s / max(first, 1e-3))))
-    times = sorted(run() for _ in range(reps))
-    med = times[len(times) // 2]
-    return dict(value=case.T / med, unit="tokens/s", cores=threads, kind="port",
-                sample=f"full workload ({case.T} tokens), oracle eager per-expert fp32 loop with "
-                       f"the reference's F.linear router, median of {reps} after 1 warm-up",
-                ms_per_step=med * 1e3)
+        orc.reference_eager_forward(cpu["x"][:probe], weights, case.k, score_fn=case.score_fn,
+                                    activation=case.activation)
+        per_token_1t = (time.perf_counter() - t0) / probe
+        tokens_1t = int(min(case.T, max(64, (2 * budget_s / 3) / 8 / per_token_1t)))
+        single = measure(1, tokens_1t, 2 * budget_s / 3)
+    finally:
+        torch.set_num_threads(before)
+    out = dict(multi, kind="port",
+               sample=f"reference eager CPU layer (torch ops, fp32) on {multi['sample_tokens']} "
+                      f"tokens of the workload, {threads_all} threads (this process's affinity "
+                      f"mask), median of {multi['runs']} after 2 warm-ups",
+               single_thread=dict(single, sample=f"same path, 1 thread, first "
+                                                 f"{single['sample_tokens']} tokens, median of "
+                                                 f"{single['runs']} after 2 warm-ups"))
+    return out
 
 
 def describe(case, cfg, permute_rows, fp8):

@@ -8,10 +8,20 @@ Reference contract (nexttransformer/scaling/megatron_moe.py):
   * last_load = per-expert token counts                                        :143, 149
   * MegatronFFN(recipe, layer_number, *, pg_collection, cpu_math) wraps the
     engine and returns only the output for a [B, S, d] hidden                  :153-182
-The engine's forward here returns (out, aux_loss) rather than MCore's (out, bias=None): the
-aux loss (load balance + z-loss, closed forms of megatron_moe.py:44-45) is a value, and it is
-also kept as the tensor attribute `last_aux` that the plugin shell sums into the training loss
-(nexttransformer/models/plugins.py:24-25, lm.py:386-388).
+  * build_model(recipe, *, pg_collection, cpu_math): MoE FFNs on every block but the dense
+    first one, model.moe_recipe / model.moe_cpu_math set                       :185-208
+The engine's forward here returns (out, aux_loss) rather than MCore's (out, bias=None); the
+aux loss is the load-balance + z-loss of megatron_moe.py:44-45 in closed form. How its gradient
+reaches the router is the engine's `aux_grad` mode:
+  * "inject" (default; the reference engine's MCore semantics, megatron_moe.py:233-236): the
+    backward adds d(aux)/d(router) scaled by the value last given to set_aux_loss_scale(),
+    whether or not the caller's loss uses aux_loss, which is returned detached (a value to
+    log). Only in training mode (module.train()), as MCore's router applies it.
+  * "loss": aux_loss carries the graph and the caller adds it to its loss; the ffn plugin runs
+    its engine this way because the plugin shell sums every `last_aux` tensor into the
+    training loss (nexttransformer/models/plugins.py:24-25, lm.py:386-388).
+The engine keeps its aux as `last_aux_loss`, never as `last_aux`, so the shell's sum over
+modules counts it once, through the plugin block that owns the engine.
 
 Compute: x is cast to bf16 (the reference's MasterLinear runs matmuls in the activation dtype,
 megatron_moe.py:74-75); the router GEMM runs in fp32 on the bf16 values; expert GEMMs run on
@@ -35,6 +45,31 @@ from nexttransformer_amd import ops
 from nexttransformer_amd.moe_recipe import MoERecipe
 
 SEED_LAYER_STRIDE = 100003  # megatron_moe.py:113-120: seed + 100003 * layer_number + index
+AUX_GRAD_MODES = ("inject", "loss")
+
+# Scale of the injected aux-loss gradient (MCore's MoEAuxLossAutoScaler main-loss scale), set by
+# set_aux_loss_scale() before backward and read when the backward runs.
+_aux_loss_scale = None
+
+
+def set_aux_loss_scale(scale, *, device="cpu"):
+    """Scale of the aux / z-loss gradient that "inject" engines add in their backward; call it
+    before backward with the same 1/accumulation factor the main loss uses
+    (megatron_moe.py:233-236). Stays in force until the next call; 1.0 until the first."""
+    global _aux_loss_scale
+    _aux_loss_scale = torch.tensor(float(scale), dtype=torch.float32, device=device)
+
+
+def _injected_aux_grad(device):
+    """{lb + z, lb, z} gradient [3] on `device` that an "inject" backward adds: (scale, 0, 0)."""
+    g = torch.zeros(3, device=device, dtype=torch.float32)
+    if _aux_loss_scale is None:
+        g[0] = 1.0
+    else:
+        g[0] = _aux_loss_scale.to(device, non_blocking=True)
+    return g
+
+
 _SCORE = {"softmax": nat.SCORE_SOFTMAX, "sigmoid": nat.SCORE_SIGMOID}
 _ACT = {"swiglu": nat.ACT_SWIGLU, "relu2": nat.ACT_RELU2}
 
@@ -132,6 +167,11 @@ class _MoETrain(torch.autograd.Function):
         if x.shape[0] == 0:
             z = lambda t: None if t is None else torch.zeros(t.shape, device=t.device)
             return (torch.zeros_like(x), z(wr_t.t()), z(w1b), z(w2b), z(sw1b), z(sw2b), None)
+        if cfg["inject"]:  # MCore: the aux gradient arrives whatever the caller's loss holds
+            injected = _injected_aux_grad(x.device)
+            grad_aux = injected if grad_aux is None else grad_aux + injected
+        if grad_out is None:
+            grad_out = torch.zeros(x.shape, device=x.device, dtype=torch.bfloat16)
         bw = ops.backward_weights(w1b, w2b, sw1b, sw2b)
         g = ops.moe_backward(grad_out, None if grad_aux is None else grad_aux.contiguous(), x,
                              wr_t, bw, ctx.state, top_k=cfg["top_k"], score_fn=cfg["score_fn"],
@@ -149,10 +189,12 @@ class MoELayer(nn.Module):
     forward(hidden [..., d]) -> (out [..., d] in hidden's dtype, aux_loss fp32 scalar).
     """
 
-    def __init__(self, recipe: MoERecipe, layer_number: int, pg_collection=None, *, device=None):
+    def __init__(self, recipe, layer_number: int, pg_collection=None, *, device=None,
+                 aux_grad="inject"):
         super().__init__()
-        if not isinstance(recipe, MoERecipe):
-            raise ValueError("recipe must be a MoERecipe")
+        recipe = MoERecipe.from_any(recipe)
+        if aux_grad not in AUX_GRAD_MODES:
+            raise ValueError(f"aux_grad must be one of {AUX_GRAD_MODES}")
         if layer_number < 1:
             raise ValueError("layer_number counts from one")
         if _ep_size(pg_collection) != 1:
@@ -166,6 +208,7 @@ class MoELayer(nn.Module):
                       if torch.cuda.is_available() else torch.device("cpu"))
         self.recipe = recipe
         self.layer_number = layer_number
+        self.aux_grad = aux_grad
         gated = recipe.activation == "swiglu"
         self.router = Router(recipe.routed_experts, recipe.width, device)
         self.experts = LocalExperts(recipe.routed_experts, recipe.width, recipe.expert_width,
@@ -173,7 +216,7 @@ class MoELayer(nn.Module):
         self.shared_experts = (ExpertMLP(recipe.width, recipe.shared_expert_width, gated, device)
                                if recipe.shared_experts else None)
         self.last_load = None
-        self.last_aux = None
+        self.last_aux_loss = None
         self.last_aux_parts = None
         self._pack_key = None
         self._packed = None
@@ -323,9 +366,9 @@ class MoELayer(nn.Module):
             out = out[:, :r.width]
         self.last_load = state["counts"].to(torch.int64)
         self.last_aux_parts = aux
-        self.last_aux = aux[0]
+        self.last_aux_loss = aux[0]
         out = out.reshape(hidden.shape).to(hidden.dtype)
-        return out, self.last_aux
+        return out, self.last_aux_loss
 
 
     def _forward_train(self, hidden):
@@ -344,34 +387,94 @@ class MoELayer(nn.Module):
         if self.shared_experts is not None:
             sw1 = self.shared_experts.linear_fc1.weight.unsqueeze(0)
             sw2 = self.shared_experts.linear_fc2.weight.unsqueeze(0)
+        inject = self.aux_grad == "inject"
         cfg = dict(top_k=r.top_k, score_fn=_SCORE[r.score_function],
                    activation=_ACT[r.activation], aux_coeff=r.aux_loss_coeff,
-                   z_coeff=r.z_loss_coeff)
+                   z_coeff=r.z_loss_coeff, inject=inject and self.training)
         out, aux = _MoETrain.apply(x, self.router.weight, w1, w2, sw1, sw2, cfg)
         self.last_load = cfg["counts"].to(torch.int64)
         self.last_aux_parts = aux.detach()
-        self.last_aux = aux[0]
-        return out.reshape(hidden.shape).to(hidden.dtype), self.last_aux
+        # "inject": the gradient comes from the backward itself, so the returned value is
+        # detached and adding it to a loss changes nothing
+        self.last_aux_loss = aux[0].detach() if inject else aux[0]
+        return out.reshape(hidden.shape).to(hidden.dtype), self.last_aux_loss
 
 
 class MoEFFN(nn.Module):
     """The block-level wrapper (megatron_moe.py:153-182): forward(hidden [B, S, d]) -> [B, S, d].
 
-    The engine's per-row computation and its aux loss (sums over all tokens) do not depend on the
-    token order, so no [B, S] <-> [S, B] transpose is needed around it.
+    Accepts this build's MoERecipe or the reference's. Its engine injects the aux-loss gradient
+    as MCore does (set_aux_loss_scale), so, like the reference's MegatronFFN, it exposes no
+    `last_aux` for a trainer to add; the engine's last_aux_loss holds the value for logging.
+    The engine's per-row computation and its aux loss (sums over all tokens) do not depend on
+    the token order, so no [B, S] <-> [S, B] transpose is needed around it.
     """
 
     def __init__(self, recipe, layer_number, *, pg_collection=None, cpu_math=False, device=None):
         super().__init__()
         if cpu_math:
             raise ValueError("this build has no CPU math path: the MoE layer runs on the GPU")
-        self.engine = MoELayer(recipe, layer_number, pg_collection, device=device)
-        self.last_aux = None
+        self.engine = MoELayer(recipe, layer_number, pg_collection, device=device,
+                               aux_grad="inject")
 
     def forward(self, hidden):
-        out, aux = self.engine(hidden)
-        self.last_aux = aux
+        out, _ = self.engine(hidden)
         return out
 
 
 MegatronFFN = MoEFFN
+
+
+def install_moe_ffns(model, recipe, *, pg_collection=None, cpu_math=False, device=None):
+    """Puts MoE FFNs into a native backbone the way the scaling adapter does
+    (megatron_moe.py:203-207): block `index` > 0 of model.transformer.h gets
+    MegatronFFN(recipe, layer_number=index + 1); block 0 keeps its dense FFN. Sets
+    model.moe_recipe (the recipe object as given, so a reference recipe keeps its own counts()
+    for the reference optimizer, megatron_optimizer.py:60-65) and model.moe_cpu_math."""
+    if cpu_math:
+        raise ValueError("this build has no CPU math path: the MoE layer runs on the GPU")
+    blocks = list(model.transformer.h)
+    if len(blocks) < 2:
+        raise ValueError("the backbone needs at least two blocks (the first stays dense)")
+    if device is None:
+        device = next(model.parameters()).device
+    for index, block in enumerate(blocks):
+        if index > 0:
+            block.mlp = MoEFFN(recipe, index + 1, pg_collection=pg_collection, device=device)
+    model.moe_recipe = recipe
+    model.moe_cpu_math = False
+    return model
+
+
+def build_model(recipe, *, pg_collection=None, cpu_math=False, backbone=None):
+    """The scaling adapter's build_model (megatron_moe.py:185-208): the family's native backbone
+    with MoE FFNs on every block but the dense first one.
+
+    backbone(recipe, device) -> model builds the native backbone (an nn.Module whose
+    model.transformer.h lists blocks with an `mlp`). By default it is NextTransformer's own
+    builder, imported from the installed `nexttransformer` package, configured as the adapter
+    configures it (megatron_moe.py:191-202); this package does not ship that backbone."""
+    r = MoERecipe.from_any(recipe)
+    if r.family not in ("moe", "looped"):
+        raise ValueError(f"family {r.family!r} has no native full-attention backbone")
+    if cpu_math:
+        raise ValueError("this build has no CPU math path: the MoE layer runs on the GPU")
+    device = torch.device("cuda", torch.cuda.current_device())
+    model = (backbone or _native_backbone)(recipe, device)
+    return install_moe_ffns(model, recipe, pg_collection=pg_collection, device=device)
+
+
+def _native_backbone(recipe, device):
+    """NextTransformer's native backbone for `recipe` (needs the nexttransformer package):
+    full-MHA, no value embeddings, stored depth unique_layers and executed depth layers, a
+    4 x width dense FFN, window pattern "L" (megatron_moe.py:191-202)."""
+    from dataclasses import replace
+    from nexttransformer.models.config import debug_config
+    from nexttransformer.models.lm import build_model as native_build
+    method = "fixed_recursive" if recipe.family == "looped" else "mha_no_ve"
+    config = replace(debug_config(method, width=recipe.width, sequence_len=recipe.sequence_len),
+                     layers=recipe.unique_layers, heads=recipe.heads, mlp_width=4 * recipe.width,
+                     vocab_size=recipe.vocab_size, window_pattern="L")
+    if config.n_layer != recipe.unique_layers or config.maximum_depth != recipe.layers:
+        raise ValueError("the backbone's stored and executed depths differ from the recipe's")
+    return native_build(config, device=f"cuda:{device.index}", seed=recipe.seed)

@@ -1,36 +1,47 @@
-"""MoE recipe: the reference's MoERecipe config keys plus the keys this MI355X build adds.
+"""The MoE layer's configuration: the reference recipe's keys, plus the few this build adds.
 
-Mirrors nexttransformer/scaling/moe_recipe.py:26-154 (field names, defaults, validation,
-counts/estimate/manifest, load_t3_recipe and
-ValueError behaviour). Added keys, all explicit so no reference recipe changes meaning:
-  score_function         "softmax" (the reference's router, megatron_moe.py:43) or "sigmoid"
-                         (top-k on logits, sigmoid scores normalised over the selected)
-  activation             "relu2" (the reference's two-matrix ReLU^2 expert, megatron_moe.py:23-24)
-                         or "swiglu" (fc1 rows [0, H) gate, [H, 2H) value: silu(g) * u, the
-                         gated_linear_unit order of the MCore config the adapter builds)
-  expert_dtype           "bf16" or "fp8" (e4m3 weights with 128x128 block scales)
-  shared_experts         0 or 1 ungated shared expert (the reference always has 1)
-  shared_expert_width    hidden width of the shared expert (default: expert_width)
-  allow_any_expert_width the reference requires expert_width == width // 4
-                         (moe_recipe.py:63-64); True relaxes exactly that check
+Interface kept from nexttransformer/scaling/moe_recipe.py:26-47 (so a recipe means the same in
+both code bases): the field names and their defaults, expert_width defaulting to width // 4,
+unique_layers defaulting to layers, and ValueError for a configuration that cannot be built.
+Everything else here is this build's own: the checks are grouped by what they protect (shape,
+routing, numerics, build keys), and the reference's cost estimates, manifest and CPU-debug
+shrink are not carried over (the MoE layer does not use them). counts() stays, because the
+reference optimizer reads block_total and embedding_and_head from model.moe_recipe
+(nexttransformer/scaling/megatron_optimizer.py:60-65).
+
+Keys this build adds (all optional; a reference recipe keeps its meaning):
+  score_function   "softmax" (top-k on the logits, softmax over the selected: the reference's
+                   router, megatron_moe.py:43) or "sigmoid" (sigmoid scores of the selected,
+                   normalised over them)
+  activation       "relu2" (the reference's two-matrix expert, megatron_moe.py:23-24) or
+                   "swiglu" (fc1 rows [0, H) are the gate, [H, 2H) the value: silu(g) * u)
+  expert_dtype     "bf16" or "fp8" (e4m3 expert weights with 128 x 128 block scales)
+  shared_experts   0 or 1 always-on ungated expert (the reference always has 1)
+  shared_expert_width       its hidden width (default: expert_width)
+  allow_any_expert_width    the reference fixes expert_width = width // 4; True lifts that
 """
-from dataclasses import asdict, dataclass, replace
+from dataclasses import dataclass, fields
 import json
 import math
 from pathlib import Path
 
-EXPERT_FAMILIES = ("moe", "looped", "kda-dsa")
-FULL_ATTENTION = ("moe", "looped")
 SCORE_FUNCTIONS = ("softmax", "sigmoid")
 ACTIVATIONS = ("relu2", "swiglu")
 EXPERT_DTYPES = ("bf16", "fp8")
-# The feed-forward keys the T3 expert families share (moe_recipe.py:14-17); a manifest whose
-# expert families disagree with them is rejected by load_t3_recipe.
-SHARED_FFN_RECIPE = dict(firstLayerDense=True, ffn="ReLU²", routedExperts=256,
-                         selectedExperts=8, sharedExperts=1, expertWidthDivisor=4)
-ATTENTION_NOTE = {"moe": "native full causal MHA; no VE",
-                  "looped": "native full causal MHA, shared core executed twice; no VE",
-                  "kda-dsa": "three KDA mixers then one DSA mixer; no VE"}
+# Families of the reference's T3 scaling study that put routed experts in their FFNs, and the
+# ones among them whose attention is plain full MHA (parameter counts apply only to those).
+EXPERT_FAMILIES = ("moe", "looped", "kda-dsa")
+MHA_FAMILIES = ("moe", "looped")
+# Parameters of the native backbone outside the blocks and the vocabulary matrices: one
+# residual and one x0 scalar per layer plus 26 fixed gate / mixing scalars.
+_BACKBONE_SCALARS_PER_LAYER = 2
+_BACKBONE_SCALARS_FIXED = 26
+# Manifest spelling of the expert activation -> the recipe's.
+_MANIFEST_FFN = {"ReLU²": "relu2", "SwiGLU": "swiglu"}
+
+
+def _positive(*values):
+    return all(isinstance(v, int) and v > 0 for v in values)
 
 
 @dataclass(frozen=True)
@@ -53,7 +64,7 @@ class MoERecipe:
     family: str = "moe"
     unique_layers: int | None = None
     loops: int = 1
-    # keys added by this build
+    # added by this build
     score_function: str = "softmax"
     activation: str = "relu2"
     expert_dtype: str = "bf16"
@@ -62,44 +73,68 @@ class MoERecipe:
     allow_any_expert_width: bool = False
 
     def __post_init__(self):
-        if self.expert_width is None:
-            object.__setattr__(self, "expert_width", self.width // 4)
-        if self.unique_layers is None:
-            object.__setattr__(self, "unique_layers", self.layers)
+        fill = dict(expert_width=self.width // 4 if isinstance(self.width, int) else None,
+                    unique_layers=self.layers)
+        for name, value in fill.items():
+            if getattr(self, name) is None:
+                object.__setattr__(self, name, value)
         if self.shared_expert_width is None:
             object.__setattr__(self, "shared_expert_width", self.expert_width)
+        problems = [*self._shape_problems(), *self._routing_problems(),
+                    *self._numeric_problems(), *self._build_problems()]
+        if problems:
+            raise ValueError("invalid MoE recipe: " + "; ".join(problems))
+
+    # -- validation, grouped by what each check protects --------------------------------------
+
+    def _shape_problems(self):
         if self.family not in EXPERT_FAMILIES:
-            raise ValueError(f"not a T3 expert family: {self.family}")
-        if not 2 <= self.unique_layers <= self.layers or self.loops < 1:
-            raise ValueError("unique layers must be between two and the executed depth")
-        if min(self.layers, self.width, self.heads, self.vocab_size, self.sequence_len,
-               self.routed_experts, self.expert_width, self.global_batch_tokens,
-               self.training_flops) <= 0:
-            raise ValueError("model dimensions and budgets must be positive")
-        if self.layers < 2 or self.width < 24 or self.width % self.heads or self.width % 4:
-            raise ValueError("MoE needs >=2 layers, width>=24 divisible by heads and four")
-        if (self.width // self.heads) % 2:
-            raise ValueError("even head dimension is required")
+            yield f"family {self.family!r} has no routed experts (expected one of {EXPERT_FAMILIES})"
+        if not _positive(self.layers, self.width, self.heads, self.vocab_size, self.sequence_len,
+                         self.routed_experts, self.expert_width, self.global_batch_tokens,
+                         self.training_flops, self.loops):
+            yield "sizes, budgets and loops must be positive integers"
+            return
+        if self.layers < 2:
+            yield "an MoE stack needs at least two layers (the first stays dense)"
+        if not 2 <= self.unique_layers <= self.layers:
+            yield "stored (unique) layers must lie between two and the executed depth"
+        if self.width < 24 or self.width % 4 or self.width % self.heads:
+            yield "width must be at least 24 and divisible by four and by the head count"
+        elif (self.width // self.heads) % 2:
+            yield "the head dimension must be even"
         if self.expert_width != self.width // 4 and not self.allow_any_expert_width:
-            raise ValueError("expert_width must be width // 4 unless allow_any_expert_width=True")
-        if not 1 <= self.top_k <= self.routed_experts:
-            raise ValueError("top-k must fit the expert count")
+            yield (f"expert_width {self.expert_width} is not width // 4 = {self.width // 4} "
+                   "(set allow_any_expert_width=True to allow it)")
         if self.global_batch_tokens % self.sequence_len:
-            raise ValueError("batch must contain whole sequences")
-        if not all(math.isfinite(x) and x >= 0 for x in (self.aux_loss_coeff, self.z_loss_coeff)):
-            raise ValueError("routing loss coefficients must be finite and nonnegative")
-        if not math.isfinite(self.router_init_std) or self.router_init_std <= 0:
-            raise ValueError("router initialization standard deviation must be positive")
+            yield "global_batch_tokens must be a whole number of sequences"
+
+    def _routing_problems(self):
+        if not (isinstance(self.top_k, int) and isinstance(self.routed_experts, int)
+                and 1 <= self.top_k <= self.routed_experts):
+            yield f"top_k must lie in [1, routed_experts]; got {self.top_k}"
         if self.score_function not in SCORE_FUNCTIONS:
-            raise ValueError(f"score_function must be one of {SCORE_FUNCTIONS}")
+            yield f"score_function must be one of {SCORE_FUNCTIONS}"
+
+    def _numeric_problems(self):
+        for name in ("aux_loss_coeff", "z_loss_coeff"):
+            v = getattr(self, name)
+            if not (math.isfinite(v) and v >= 0):
+                yield f"{name} must be a finite, non-negative coefficient"
+        if not (math.isfinite(self.router_init_std) and self.router_init_std > 0):
+            yield "router_init_std (the router's initial standard deviation) must be positive"
+
+    def _build_problems(self):
         if self.activation not in ACTIVATIONS:
-            raise ValueError(f"activation must be one of {ACTIVATIONS}")
+            yield f"activation must be one of {ACTIVATIONS}"
         if self.expert_dtype not in EXPERT_DTYPES:
-            raise ValueError(f"expert_dtype must be one of {EXPERT_DTYPES}")
+            yield f"expert_dtype must be one of {EXPERT_DTYPES}"
         if self.shared_experts not in (0, 1):
-            raise ValueError("shared_experts must be 0 or 1")
-        if self.shared_expert_width <= 0:
-            raise ValueError("shared_expert_width must be positive")
+            yield "shared_experts must be 0 or 1"
+        if not _positive(self.shared_expert_width):
+            yield "shared_expert_width must be a positive integer"
+
+    # -- sizes ------------------------------------------------------------------------------
 
     @property
     def fc1_rows(self):
@@ -107,99 +142,92 @@ class MoERecipe:
         return 2 * self.expert_width if self.activation == "swiglu" else self.expert_width
 
     def expert_params(self, width=None):
-        """Parameters of one expert of hidden `width` (fc1 + fc2)."""
-        h = self.expert_width if width is None else width
-        rows = 2 * h if self.activation == "swiglu" else h
-        return rows * self.width + self.width * h
-
-    def block_active(self):
-        """Parameters a token activates across the executed depth (reference convention,
-        moe_recipe.py:74-85, generalised to the expert activation and shared width)."""
-        if self.family not in FULL_ATTENTION:
-            raise ValueError(f"{self.family} attention needs its own cost proof")
-        d, e = self.width, self.routed_experts
-        shared = self.shared_experts * self.expert_params(self.shared_expert_width)
-        return (4 * self.layers * d * d + 8 * d * d
-                + (self.layers - 1) * (self.top_k * self.expert_params() + shared)
-                + (self.layers - 1) * d * e)
-
-    def describes_capacity(self):
-        """Whether the parameter counts describe the family: a flat stack of MHA layers."""
-        return self.family in FULL_ATTENTION and self.unique_layers == self.layers
-
-    def counts(self):
-        """Parameter counts (moe_recipe.py:93-106): attention 4Ld^2, a dense first FFN 8d^2,
-        (L-1) MoE layers of E routed + shared experts and a d x E router, embeddings and head
-        padded to 64 rows, and the backbone's 2L + 26 scalars."""
-        if not self.describes_capacity():
-            raise ValueError(f"{self.family} capacity needs its own accounting")
-        d, e = self.width, self.routed_experts
-        shared = self.shared_experts * self.expert_params(self.shared_expert_width)
-        total = (4 * self.layers * d * d + 8 * d * d
-                 + (self.layers - 1) * (e * self.expert_params() + shared)
-                 + (self.layers - 1) * d * e)
-        small = 2 * self.layers + 26
-        io = 2 * d * math.ceil(self.vocab_size / 64) * 64
-        return dict(block_total=total, block_active=self.block_active(), embedding_and_head=io,
-                    native_small_parameters=small, model_total=total + io + small)
-
-    def estimate(self):
-        """Main-term training cost (moe_recipe.py:108-118): 6 x active parameters + attention
-        12 s d L + head 6 d V FLOP per token, and the updates / tokens the budget buys."""
-        if self.family not in FULL_ATTENTION:
-            return dict(flops_per_token_main_term=None, estimated_updates=None,
-                        estimated_tokens=None, cost_proof_complete=False)
-        d, s = self.width, self.sequence_len
-        flops = 6 * self.block_active() + 12 * s * d * self.layers + 6 * d * self.vocab_size
-        updates = round(self.training_flops / (flops * self.global_batch_tokens))
-        return dict(flops_per_token_main_term=flops, estimated_updates=updates,
-                    estimated_tokens=updates * self.global_batch_tokens, cost_proof_complete=False)
-
-    def manifest(self):
-        counts = self.counts() if self.describes_capacity() else None
-        act = {"relu2": "ReLU squared", "swiglu": "SwiGLU"}[self.activation]
-        return dict(protocol="nextt-scale-2k-v1", recipe=asdict(self), counts=counts,
-                    estimate=self.estimate(), attention=ATTENTION_NOTE[self.family],
-                    ffn=f"first dense 4d; then routed top-k plus {self.shared_experts} shared; {act}",
-                    gpu_validated=False, formal_training_ready=False)
+        """Parameters of one expert of hidden width `width` (default expert_width): fc1 + fc2."""
+        hidden = self.expert_width if width is None else width
+        matrices = 3 if self.activation == "swiglu" else 2
+        return matrices * self.width * hidden
 
     def moe_layer_params(self):
-        """Parameters of one MoE layer as built by nexttransformer_amd.moe.MoELayer."""
-        shared = self.shared_experts * self.expert_params(self.shared_expert_width)
-        return self.routed_experts * self.expert_params() + shared + self.width * self.routed_experts
+        """Parameters of one MoE layer as nexttransformer_amd.moe.MoELayer holds them."""
+        return (self.routed_experts * self.expert_params() + self._shared_params()
+                + self.width * self.routed_experts)
 
-    def debug(self, *, routed_experts=8, top_k=2):
-        """The reference's CPU debug shrink (moe_recipe.py:128-133)."""
-        shape = (dict(layers=2 + self.loops, unique_layers=3) if self.loops > 1
-                 else dict(layers=3, unique_layers=3))
-        return replace(self, **shape, width=32, heads=2, vocab_size=64, sequence_len=8,
-                       routed_experts=routed_experts, top_k=top_k, expert_width=8,
-                       shared_expert_width=8, global_batch_tokens=32,
-                       cell_id=self.cell_id + "-cpu-debug")
+    def _shared_params(self):
+        return self.shared_experts * self.expert_params(self.shared_expert_width)
+
+    def counts(self):
+        """Parameter counts of the whole model the scaling adapter builds: full MHA in every
+        layer, a dense 4d ReLU^2 FFN in the first, an MoE layer in each of the others, the
+        embedding and head over the vocabulary padded to 64, and the backbone's scalars.
+        block_active counts what one token uses: top_k routed experts instead of all of them.
+        Only defined for a flat stack of full-attention layers."""
+        if self.family not in MHA_FAMILIES or self.unique_layers != self.layers:
+            raise ValueError(f"parameter counts describe a flat full-attention stack; family "
+                             f"{self.family!r} with {self.unique_layers} stored of {self.layers} "
+                             "executed layers is not one")
+        d = self.width
+        per_layer_attention = 4 * d * d
+        dense_first = 2 * d * (4 * d)
+        router = d * self.routed_experts
+        moe_stored = self.routed_experts * self.expert_params() + self._shared_params() + router
+        moe_used = self.top_k * self.expert_params() + self._shared_params() + router
+        blocks = self.layers * per_layer_attention + dense_first
+        block_total = blocks + (self.layers - 1) * moe_stored
+        block_active = blocks + (self.layers - 1) * moe_used
+        vocab_rows = -(-self.vocab_size // 64) * 64
+        io = 2 * d * vocab_rows
+        scalars = _BACKBONE_SCALARS_PER_LAYER * self.layers + _BACKBONE_SCALARS_FIXED
+        return dict(block_total=block_total, block_active=block_active, embedding_and_head=io,
+                    native_small_parameters=scalars, model_total=block_total + io + scalars)
+
+    # -- conversion from the reference's recipe ---------------------------------------------
+
+    @classmethod
+    def from_any(cls, recipe):
+        """This build's recipe for `recipe`: itself, or -- for the reference's MoERecipe or any
+        object carrying its fields -- a recipe with those field values read by name and the
+        build-only keys at their defaults (ReLU^2, softmax, bf16, one shared expert of the
+        routed experts' width), which is exactly the reference's layer."""
+        if isinstance(recipe, cls):
+            return recipe
+        added = {"score_function", "activation", "expert_dtype", "shared_experts",
+                 "shared_expert_width", "allow_any_expert_width"}
+        names = [f.name for f in fields(cls) if f.name not in added]
+        missing = [n for n in names if not hasattr(recipe, n)]
+        if missing:
+            raise ValueError(f"not an MoE recipe: {type(recipe).__name__} lacks {missing}")
+        return cls(**{n: getattr(recipe, n) for n in names})
 
 
 def load_t3_recipe(cell_id="moe-T3-L20", path=None):
-    """The recipe of a T3 expert cell from a scaling manifest (moe_recipe.py:136-154).
+    """The recipe of one expert cell of a T3 scaling manifest (the JSON the reference keeps at
+    configs/scaling/t3.json; this package ships none, so `path` is required).
 
-    `path` is the manifest JSON (the reference keeps it at configs/scaling/t3.json); this
-    package ships none, so it is required.
-    """
+    The cell gives the depth, width, heads and expert width; its family's recipe gives the
+    routed / selected / shared expert counts and the FFN activation, which are read, not
+    assumed, and must be ones this build runs. Looped families store pre + core + post layers
+    and execute the core `loops` times."""
     if path is None:
         raise ValueError("load_t3_recipe needs the path of a T3 scaling manifest")
     data = json.loads(Path(path).read_text())
-    cell = next((c for c in data["cells"]
-                 if c["id"] == cell_id and c["family"] in EXPERT_FAMILIES), None)
-    if cell is None:
-        raise ValueError(f"unknown T3 expert cell: {cell_id}")
-    rule = next(f["recipe"] for f in data["families"] if f["id"] == cell["family"])
-    if ({k: v for k, v in rule.items() if k in SHARED_FFN_RECIPE} != SHARED_FFN_RECIPE
-            or data["valueEmbeddings"] or data["protocol"] != "nextt-scale-2k-v1"):
-        raise ValueError("the shared T3 expert recipe changed; review the adapter before using it")
-    loops = rule.get("loops", 1)
-    unique = (cell["preLayers"] + cell["coreLayers"] + cell["postLayers"] if loops > 1
+    cells = {c["id"]: c for c in data["cells"] if c.get("family") in EXPERT_FAMILIES}
+    if cell_id not in cells:
+        raise ValueError(f"{cell_id!r} is not an expert-family cell of {path}")
+    cell = cells[cell_id]
+    family = next(f["recipe"] for f in data["families"] if f["id"] == cell["family"])
+    if family.get("ffn") not in _MANIFEST_FFN:
+        raise ValueError(f"family {cell['family']!r}: expert FFN {family.get('ffn')!r} is not "
+                         f"one of {tuple(_MANIFEST_FFN)}")
+    if not family.get("firstLayerDense", False):
+        raise ValueError(f"family {cell['family']!r}: the scaling adapter keeps layer 0 dense")
+    loops = family.get("loops", 1)
+    stored = (cell["preLayers"] + cell["coreLayers"] + cell["postLayers"] if loops > 1
               else cell["layers"])
     return MoERecipe(layers=cell["layers"], width=cell["width"], heads=cell["heads"],
                      vocab_size=data["vocabSize"], sequence_len=data["sequenceLength"],
                      seed=data["seed"], global_batch_tokens=data["globalBatchTokens"],
                      training_flops=data["trainingFlops"], expert_width=cell["expertWidth"],
-                     cell_id=cell_id, family=cell["family"], unique_layers=unique, loops=loops)
+                     routed_experts=family["routedExperts"], top_k=family["selectedExperts"],
+                     shared_experts=family["sharedExperts"],
+                     activation=_MANIFEST_FFN[family["ffn"]], cell_id=cell_id,
+                     family=cell["family"], unique_layers=stored, loops=loops)

@@ -176,6 +176,39 @@ def moe_forward(x, weights, k, *, score_fn=SOFTMAX, activation=SWIGLU, aux_coeff
                 counts=counts, offsets=offsets, src_row=src, dest=dest)
 
 
+def reference_eager_forward(x, weights, k, *, score_fn=SOFTMAX, activation=SWIGLU,
+                            aux_coeff=0.01, z_coeff=0.001):
+    """The reference's eager CPU layer written with torch's own ops, as RoutedFFN runs it
+    (reference_blocks.py:35-45): fp32 rows, router F.linear (+ bias), logits.topk(k), softmax
+    over the selected (sigmoid normalised over them for the sigmoid score), the shared expert
+    first, then per expert torch.where over the top-k indices, the expert's FFN on the gathered
+    rows weighted after fc2, and index_add into the output; the aux / z losses in closed form on
+    the full logits (megatron_moe.py:44-45). Used as the timed CPU baseline; tie order is
+    torch.topk's."""
+    rows = x.detach().cpu().float()
+    logits = F.linear(rows, weights.router.float())
+    if weights.bias is not None:
+        logits = logits + weights.bias.float()
+    top, idx = logits.topk(k)
+    if score_fn == SOFTMAX:
+        w = top.softmax(-1)
+    else:
+        s = torch.sigmoid(top)
+        w = s / s.sum(-1, keepdim=True)
+    if weights.shared_w1 is not None:
+        out = expert_ffn(rows, weights.shared_w1.float(), weights.shared_w2.float(), activation)
+    else:
+        out = torch.zeros_like(rows)
+    for e in range(weights.router.shape[0]):
+        token, slot = torch.where(idx == e)
+        if token.numel():
+            y = expert_ffn(rows[token], weights.w1[e].float(), weights.w2[e].float(), activation)
+            out = out.index_add(0, token, y * w[token, slot, None])
+    counts = torch.bincount(idx.flatten(), minlength=weights.router.shape[0])
+    lb, z = aux_losses(logits, counts, k, aux_coeff, z_coeff, score_fn)
+    return out, lb + z
+
+
 def moe_forward_tokens(x, weights, k, tokens, *, logits, score_fn=SOFTMAX, activation=SWIGLU,
                        dtype=torch.float32):
     """Output rows for a subset of tokens only (every token's output depends on its own row and

@@ -59,6 +59,16 @@ def make_inputs(case, device="cpu"):
     return out
 
 
+def make_router_inputs(case):
+    """x bf16 [T, d], router fp32 [E, d] and the logit bias (or None) of make_inputs(case), drawn
+    without the expert weights: x and the router come first from the same generator, so the
+    values are identical."""
+    g = torch.Generator().manual_seed(case.seed)
+    x = torch.randn(case.T, case.d, generator=g).to(torch.bfloat16)
+    router = torch.randn(case.E, case.d, generator=g) * 0.02
+    return x, router, (zipf_bias(case.E, case.zipf_bias) if case.zipf_bias else None)
+
+
 def rel_l2(a, b):
     a, b = a.double().cpu(), b.double().cpu()
     return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()

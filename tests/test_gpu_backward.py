@@ -25,12 +25,28 @@ CASES = [
     Case("bwd-T700-d256-E32-k8-relu2-zipf", 700, 256, 32, 8, 128, activation=1, zipf_bias=1.2,
          seed=23),
     Case("bwd-T1024-d1024-E32-k4-swiglu", 1024, 1024, 32, 4, 512, seed=24),
-    # the registered T3 expert cell's widths (d 1280, ReLU^2 width 320, shared expert): widths
-    # the packed GEMM and the grouped weight-gradient kernel do not tile take the plain grouped
-    # GEMM and the per-expert library products
+    # the registered T3 expert cell's widths (d 1280, ReLU^2 width 320, shared expert)
     Case("bwd-T200-d1280-E16-k4-relu2-H320-shared", 200, 1280, 16, 4, 320, activation=1,
          shared_H=320, seed=25),
+    # the packed path with the kept pre-activations for ReLU^2 and for skewed routing
+    Case("bwd-T700-d512-E32-k8-relu2-H256-zipf", 700, 512, 32, 8, 256, activation=1,
+         zipf_bias=1.2, seed=26),
+    Case("bwd-T600-d512-E24-k6-relu2-sigmoid-H256-shared", 600, 512, 24, 6, 256, activation=1,
+         score_fn=1, shared_H=256, seed=27),
 ]
+
+
+def _packable(case):
+    """Whether every projection of the case qualifies for the packed GEMM."""
+    from nexttransformer_amd import _native as nat, ops
+    up = nat.EPI_SWIGLU if case.activation == 0 else nat.EPI_RELU2
+    widths = [case.H] + ([case.shared_H] if case.shared_H else [])
+    return all(ops.packable(case.d, h, up) and ops.packable(h, case.d, nat.EPI_NONE)
+               for h in widths)
+
+
+# (case, packed) pairs: every case with plain weights; the packed variant where the widths allow
+RUNS = [(c, False) for c in CASES] + [(c, True) for c in CASES if _packable(c)]
 
 
 def ffn(x, w1, w2, activation):
@@ -84,8 +100,8 @@ def reference_grads(x, wr, bias, w1, w2, sw1, sw2, ids, G, g_aux, case, aux_coef
     return [t.grad for t in params]
 
 
-@pytest.mark.parametrize("packed", [False, True], ids=["plain", "packed"])
-@pytest.mark.parametrize("case", CASES, ids=lambda c: c.name)
+@pytest.mark.parametrize("case,packed", RUNS,
+                         ids=[f"{c.name}-{'packed' if p else 'plain'}" for c, p in RUNS])
 def test_backward_matches_fp32_autograd(case, packed):
     """packed: the forward runs the packed GEMMs and keeps the fc1 pre-activations from the up
     projection's launch (the module's training path); plain: the backward recomputes them."""
@@ -105,11 +121,6 @@ def test_backward_matches_fp32_autograd(case, packed):
     fw = dict(w1=w1b, w2=w2b, shared_w1=sw1b, shared_w2=sw2b)
     if packed:
         up = nat.EPI_SWIGLU if case.activation == 0 else nat.EPI_RELU2
-        F = w1b.shape[1]
-        if not (ops.packable(case.d, F // (2 if case.activation == 0 else 1), up)
-                and ops.packable(case.H, case.d, nat.EPI_NONE)
-                and (sw1b is None or ops.packable(case.shared_H, case.d, nat.EPI_NONE))):
-            pytest.skip("widths the packed GEMM does not take")
         fw = {n: None if w is None else ops.pack_expert_weights(w, up if "1" in n else nat.EPI_NONE)
               for n, w in fw.items()}
     out, aux, state = ops.moe_forward(x, wr_t, fw["w1"], fw["w2"], top_k=case.k,

@@ -68,6 +68,11 @@ def test_full_size_layer(cfg, packed):
     assert bool((key[1:] > key[:-1]).all())
     rows_of = ids.long()[src]  # the expert each permuted row's token chose, among its k
     assert bool((rows_of == expert_of_row[:, None]).any(1).all())
+    # whole batch: the kernel routes every token as top-k of the reference's own router
+    # expression F.linear(x.float(), W.float()) (+ bias) does (megatron_moe.py:95-99)
+    ref_ids_all, _ = orc.topk(orc.router_logits_reference(cpu["x"], cpu["router"], cpu["bias"]),
+                              k, case.score_fn)
+    assert torch.equal(ids, ref_ids_all)
 
     # sampled tokens: fixed-order logits, top-k and outputs against the oracle
     rng = np.random.default_rng(cfg)

@@ -149,11 +149,14 @@ def t3_recipe(cell="moe-T3-L20"):
 
 
 def test_recipe_counts_match_reference_test():
-    """tests/test_megatron_moe.py:51-55."""
+    """tests/test_megatron_moe.py:51-59: the registered cell's parameter counts and the shapes
+    the recipe rejects."""
     from nexttransformer_amd.moe_recipe import MoERecipe
     r = t3_recipe()
     assert r.counts()["block_total"] == 4150558720
     assert r.counts()["block_active"] == 290488320
+    assert r.counts()["model_total"] == (r.counts()["block_total"]
+                                         + r.counts()["embedding_and_head"] + 2 * r.layers + 26)
     with pytest.raises(ValueError):
         replace(r, top_k=257)
     with pytest.raises(ValueError):
@@ -163,33 +166,61 @@ def test_recipe_counts_match_reference_test():
     with pytest.raises(ValueError):
         t3_recipe("dense-T3-L20")
     assert isinstance(r, MoERecipe) and r.activation == "relu2" and r.shared_experts == 1
+    assert (r.width, r.routed_experts, r.top_k, r.expert_width, r.layers) == (1280, 256, 8, 320, 20)
 
 
-def test_recipe_estimates_match_manifest():
-    """tests/test_megatron_moe.py:23-31: estimated tokens and updates of every expert cell."""
+def test_recipe_counts_by_enumerating_the_stack():
+    """counts() against a sum over the tensors of the stack it describes, for a SwiGLU recipe
+    with a wider shared expert (so the activation and shared width terms are exercised)."""
+    from nexttransformer_amd.moe_recipe import MoERecipe
+    r = MoERecipe(layers=5, width=96, heads=4, vocab_size=1000, routed_experts=6, top_k=2,
+                  expert_width=40, activation="swiglu", shared_expert_width=56,
+                  allow_any_expert_width=True, global_batch_tokens=4096)
+    d = 96
+    attn = [(d, d)] * 4
+    dense = [(4 * d, d), (d, 4 * d)]
+    expert = lambda h: [(2 * h, d), (d, h)]
+    moe = sum((expert(40) for _ in range(6)), []) + expert(56) + [(6, d)]
+    used = sum((expert(40) for _ in range(2)), []) + expert(56) + [(6, d)]
+    n = lambda shapes: sum(a * b for a, b in shapes)
+    total = 5 * n(attn) + n(dense) + 4 * n(moe)
+    active = 5 * n(attn) + n(dense) + 4 * n(used)
+    c = r.counts()
+    assert (c["block_total"], c["block_active"]) == (total, active)
+    assert c["embedding_and_head"] == 2 * d * 1024
+    assert r.moe_layer_params() == n(moe)
+
+
+def test_t3_cells_read_their_family_recipe():
+    """Every expert cell of the manifest loads with its family's expert counts and activation;
+    a family that changes them is followed (read, not assumed), and one this build cannot run
+    is rejected."""
     data = json.loads((ROOT / "tests" / "golden" / "t3_expert_cells.json").read_text())
-    checked = 0
     for cell in data["cells"]:
         r = t3_recipe(cell["id"])
-        est = r.estimate()
-        if cell["family"] == "kda-dsa":
-            assert est["estimated_tokens"] is None
-            with pytest.raises(ValueError):
-                r.block_active()
-            continue
-        assert est["estimated_tokens"] == cell["estimatedTokens"], cell["id"]
-        assert est["estimated_updates"] == cell["estimatedUpdates"], cell["id"]
-        assert est["cost_proof_complete"] is False
-        checked += 1
-    assert checked >= 8
-
-
-def test_looped_has_no_capacity_count():
+        assert (r.routed_experts, r.top_k, r.shared_experts, r.activation) == (256, 8, 1, "relu2")
+        assert (r.layers, r.width, r.expert_width, r.family) == (
+            cell["layers"], cell["width"], cell["expertWidth"], cell["family"])
     looped, moe = t3_recipe("looped-T3-L20"), t3_recipe("moe-T3-L20")
     assert looped.layers == moe.layers and looped.unique_layers < looped.layers
-    assert looped.estimate()["estimated_tokens"] == moe.estimate()["estimated_tokens"]
     with pytest.raises(ValueError):
         looped.counts()
+    with pytest.raises(ValueError):
+        t3_recipe("kda-dsa-T3-L20").counts()
+    import tempfile
+    from nexttransformer_amd.moe_recipe import load_t3_recipe
+    with tempfile.TemporaryDirectory() as tmp:
+        def variant(**change):
+            copy = json.loads(json.dumps(data))
+            next(f for f in copy["families"] if f["id"] == "moe")["recipe"].update(change)
+            path = Path(tmp) / "t3.json"
+            path.write_text(json.dumps(copy))
+            return path
+        assert load_t3_recipe("moe-T3-L20", variant(selectedExperts=4)).top_k == 4
+        with pytest.raises(ValueError, match="expert FFN"):
+            load_t3_recipe("moe-T3-L20", variant(ffn="GELU"))
+        with pytest.raises(ValueError, match="dense"):
+            load_t3_recipe("moe-T3-L20", variant(firstLayerDense=False))
 
 
 @pytest.mark.parametrize("change,msg", [
@@ -197,27 +228,57 @@ def test_looped_has_no_capacity_count():
     (dict(activation="gelu"), "activation"),
     (dict(expert_dtype="fp16"), "expert_dtype"),
     (dict(shared_experts=2), "shared_experts"),
-    (dict(aux_loss_coeff=-1.0), "coefficients"),
-    (dict(z_loss_coeff=float("nan")), "coefficients"),
-    (dict(router_init_std=0.0), "standard deviation"),
-    (dict(global_batch_tokens=100), "whole sequences"),
+    (dict(aux_loss_coeff=-1.0), "aux_loss_coeff"),
+    (dict(z_loss_coeff=float("nan")), "z_loss_coeff"),
+    (dict(router_init_std=0.0), "router_init_std"),
+    (dict(global_batch_tokens=100), "whole number of sequences"),
     (dict(heads=3), "divisible"),
+    (dict(layers=1, unique_layers=1), "at least two layers"),
+    (dict(top_k=0), "top_k"),
 ])
 def test_recipe_rejects_invalid_values(change, msg):
     with pytest.raises(ValueError, match=msg):
         replace(t3_recipe(), **change)
 
 
-def test_recipe_added_keys_and_debug_shrink():
+def test_recipe_added_keys():
     from nexttransformer_amd.moe_recipe import MoERecipe
     r = MoERecipe(layers=4, width=1024, heads=8, routed_experts=32, top_k=4, expert_width=512,
                   activation="swiglu", shared_experts=0, allow_any_expert_width=True,
                   global_batch_tokens=16384)
     assert r.fc1_rows == 1024 and r.expert_params() == 1024 * 1024 + 1024 * 512
     assert r.moe_layer_params() == 32 * r.expert_params() + 1024 * 32
-    d = t3_recipe().debug()
-    assert (d.width, d.expert_width, d.routed_experts, d.top_k, d.layers) == (32, 8, 8, 2, 3)
-    assert d.shared_expert_width == 8
+    assert MoERecipe(layers=3, width=32, heads=2).shared_expert_width == 8
+
+
+def _reference_shaped_recipe(**values):
+    """An object carrying exactly the reference MoERecipe's fields
+    (nexttransformer/scaling/moe_recipe.py:27-47) and nothing of this build's."""
+    from types import SimpleNamespace
+    base = dict(layers=3, width=32, heads=2, vocab_size=64, sequence_len=8, routed_experts=8,
+                top_k=2, expert_width=8, seed=42, global_batch_tokens=32,
+                training_flops=10**20, cell_id="moe-T3-L20-cpu-debug", aux_loss_coeff=0.01,
+                z_loss_coeff=0.001, router_init_std=0.02, family="moe", unique_layers=3,
+                loops=1)
+    base.update(values)
+    return SimpleNamespace(**base)
+
+
+def test_recipe_from_reference_fields():
+    """A reference recipe converts field by field; the build keys take the reference layer's
+    values (ReLU^2, softmax, bf16, one shared expert of the routed width)."""
+    from nexttransformer_amd.moe_recipe import MoERecipe
+    ref = _reference_shaped_recipe()
+    r = MoERecipe.from_any(ref)
+    for name in vars(ref):
+        assert getattr(r, name) == getattr(ref, name), name
+    assert (r.activation, r.score_function, r.expert_dtype, r.shared_experts,
+            r.shared_expert_width) == ("relu2", "softmax", "bf16", 1, 8)
+    assert MoERecipe.from_any(r) is r
+    with pytest.raises(ValueError, match="lacks"):
+        MoERecipe.from_any(object())
+    with pytest.raises(ValueError):
+        MoERecipe.from_any(_reference_shaped_recipe(top_k=9))
 
 
 # ---------------------------------------------------------------------------------------------
@@ -387,3 +448,78 @@ def test_plugin_ffn_exposes_shell_linears():
         plugin.check(plugin_config(top_k=99))
     with pytest.raises(ValueError):
         plugin.check(plugin_config(activation="gelu"))
+
+
+def test_plugin_first_layer_dense_and_one_last_aux_per_block():
+    """The T3 families keep layer 0 dense (reference_blocks.py:48-58); with the option on, the
+    plugin's layer 0 is a dense ReLU^2 FFN whose c_fc / c_proj the shell can initialise. In an
+    MoE block exactly one module of the subtree may expose a tensor `last_aux` -- the block --
+    since the shell sums `last_aux` over all modules (lm.py:386-388)."""
+    import importlib
+    plugin = importlib.import_module("nexttransformer_amd.plugins.nt_moe")
+    config = plugin_config()
+    dense = plugin.ffn(config, 0, device="cpu")
+    assert isinstance(dense, plugin.DenseBlockFFN)
+    assert dense.c_fc.weight.shape == (256, 64) and dense.c_proj.weight.shape == (64, 256)
+    assert isinstance(dense.c_fc, nn.Linear) and isinstance(dense.c_proj, nn.Linear)
+    x = torch.randn(2, 3, 64)
+    ref = torch.relu(x @ dense.c_fc.weight.t()).square() @ dense.c_proj.weight.t()
+    torch.testing.assert_close(dense(x), ref)
+    assert isinstance(plugin.ffn(plugin_config(first_layer_dense=False), 0, device="cpu"),
+                      plugin.MoEBlockFFN)
+    with pytest.raises(ValueError, match="first_layer_dense"):
+        plugin.check(plugin_config(first_layer_dense="yes"))
+    block = plugin.ffn(config, 2, device="cpu")
+    assert block.engine.layer_number == 3 and block.engine.aux_grad == "loss"
+    # what the shell's sum would see after a forward: stand the engine's forward in by a value
+    block.last_aux = torch.tensor(0.5)
+    block.engine.last_aux_loss = block.last_aux
+    holders = [m for m in block.modules() if torch.is_tensor(getattr(m, "last_aux", None))]
+    assert holders == [block]
+    total = sum((m.last_aux for m in block.modules()
+                 if torch.is_tensor(getattr(m, "last_aux", None))), torch.zeros(()))
+    assert total.item() == 0.5
+
+
+def test_install_moe_ffns_mirrors_the_scaling_adapter():
+    """megatron_moe.py:203-207: blocks 1.. get MegatronFFN(recipe, index + 1), block 0 keeps its
+    FFN, model.moe_recipe is the recipe as given (here reference-shaped) and moe_cpu_math is
+    False; the engines inject the aux gradient and expose no `last_aux`."""
+    from nexttransformer_amd.moe import MegatronFFN, MoEFFN, install_moe_ffns
+    ref = _reference_shaped_recipe()
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.mlp = nn.Linear(32, 32)
+
+    model = nn.Module()
+    model.transformer = nn.Module()
+    model.transformer.h = nn.ModuleList(Block() for _ in range(3))
+    dense = model.transformer.h[0].mlp
+    install_moe_ffns(model, ref, device="cpu")
+    assert model.transformer.h[0].mlp is dense
+    for i in (1, 2):
+        mlp = model.transformer.h[i].mlp
+        assert isinstance(mlp, MoEFFN) and MegatronFFN is MoEFFN
+        assert mlp.engine.layer_number == i + 1 and mlp.engine.aux_grad == "inject"
+        assert not hasattr(mlp, "last_aux") and not hasattr(mlp.engine, "last_aux")
+        assert mlp.engine.recipe.routed_experts == 8 and mlp.engine.shared_experts is not None
+    assert model.moe_recipe is ref and model.moe_cpu_math is False
+    with pytest.raises(ValueError, match="CPU math"):
+        install_moe_ffns(model, ref, cpu_math=True, device="cpu")
+    # initialisation follows the global numbering: block 2's engine is layer 3's
+    from nexttransformer_amd.moe import MoELayer
+    twin = MoELayer(ref, 3, device="cpu")
+    assert torch.equal(twin.router.weight, model.transformer.h[2].mlp.engine.router.weight)
+
+
+def test_set_aux_loss_scale_value():
+    from nexttransformer_amd import moe
+    try:
+        moe.set_aux_loss_scale(0.25)
+        g = moe._injected_aux_grad(torch.device("cpu"))
+        assert g.tolist() == [0.25, 0.0, 0.0]
+    finally:
+        moe.set_aux_loss_scale(1.0)
+    assert moe._injected_aux_grad(torch.device("cpu")).tolist() == [1.0, 0.0, 0.0]

@@ -370,3 +370,98 @@ def test_oracle_reproduces_golden_vectors():
     assert set(load_golden()) == {"ties", "sigmoid-relu2-shared-bias", "k-equals-E"}
     ties = load_golden()["ties"]
     assert torch.equal(ties["weights"].router[5], ties["weights"].router[3])
+
+
+# ---------------------------------------------------------------------------------------------
+# moe_forward_tokens (the reference of the full-size output checks) is moe_forward's rows
+
+@pytest.mark.parametrize("activation,score_fn,shared,bias", [
+    (orc.SWIGLU, orc.SOFTMAX, False, False),
+    (orc.RELU2, orc.SOFTMAX, True, False),
+    (orc.SWIGLU, orc.SIGMOID, True, True),
+    (orc.RELU2, orc.SIGMOID, False, True),
+])
+def test_moe_forward_tokens_equals_moe_forward_rows(activation, score_fn, shared, bias):
+    """Each token's output depends on its own row and routing alone, so the subset restatement
+    must return exactly the full layer's rows, in the order asked for, for token lists that are
+    unsorted, repeat tokens, or hold a single token. Run in float64: the expert products then
+    carry no rounding that a different batch of rows could change."""
+    g = torch.Generator().manual_seed(21)
+    T, d, E, k, H = 96, 48, 7, 3, 24
+    Fr = 2 * H if activation == orc.SWIGLU else H
+    x = torch.randn(T, d, generator=g).to(torch.bfloat16)
+    wts = orc.Weights(router=torch.randn(E, d, generator=g) * 0.3,
+                      w1=torch.randn(E, Fr, d, generator=g) * 0.2,
+                      w2=torch.randn(E, d, H, generator=g) * 0.2,
+                      shared_w1=torch.randn(Fr, d, generator=g) * 0.2 if shared else None,
+                      shared_w2=torch.randn(d, H, generator=g) * 0.2 if shared else None,
+                      bias=torch.randn(E, generator=g) if bias else None)
+    full = orc.moe_forward(x, wts, k, score_fn=score_fn, activation=activation,
+                           dtype=torch.float64)
+    lists = [torch.randperm(T, generator=g)[:40],            # unsorted
+             torch.tensor([5, 5, 90, 3, 5, 90, 0, T - 1]),   # duplicates
+             torch.tensor([17]),
+             torch.arange(T)]
+    for tokens in lists:
+        sub = orc.moe_forward_tokens(x, wts, k, tokens, logits=full["logits"], score_fn=score_fn,
+                                     activation=activation, dtype=torch.float64)
+        torch.testing.assert_close(sub, full["out"][tokens], rtol=1e-13, atol=1e-15)
+    # discriminates: another token's row, or a dropped shared expert, is far off
+    sub = orc.moe_forward_tokens(x, wts, k, lists[0], logits=full["logits"], score_fn=score_fn,
+                                 activation=activation, dtype=torch.float64)
+    assert not torch.allclose(sub, full["out"][lists[0].roll(1)], rtol=1e-3)
+    if shared:
+        no_shared = orc.Weights(router=wts.router, w1=wts.w1, w2=wts.w2, bias=wts.bias)
+        sub = orc.moe_forward_tokens(x, no_shared, k, lists[0], logits=full["logits"],
+                                     score_fn=score_fn, activation=activation,
+                                     dtype=torch.float64)
+        assert not torch.allclose(sub, full["out"][lists[0]], rtol=1e-3)
+
+
+# ---------------------------------------------------------------------------------------------
+# routing on the fixed-order logits equals routing on the reference's own router expression
+
+@pytest.mark.parametrize("config", [1, 2, 3, 4, 5])
+def test_fixed_order_routing_equals_reference_router_at_benchmark_configs(config):
+    """On the seeded inputs of every benchmark configuration, top-k of the fixed-order logits
+    (which the HIP router reproduces bit for bit) selects the same experts in the same order as
+    top-k of the reference's F.linear(x.float(), W.float()) (+ the logit bias)
+    (megatron_moe.py:95-99, reference_blocks.py:37-38), although most logits differ in their
+    low bits. The weights then differ only by that rounding. The smallest k-th / (k+1)-th logit
+    margin is reported beside the largest logit difference of the two orders."""
+    from tests.moe_cases import CONFIGS, make_router_inputs
+    case = CONFIGS[config]
+    x, router, bias = make_router_inputs(case)
+    fixed = orc.router_logits_fixed(x, router, bias)
+    ref = orc.router_logits_reference(x, router, bias)
+    assert (fixed != ref).any()  # the two orders do round differently
+    ids_f, w_f = orc.topk(fixed, case.k, case.score_fn)
+    ids_r, w_r = orc.topk(ref, case.k, case.score_fn)
+    assert torch.equal(ids_f, ids_r)
+    torch.testing.assert_close(w_f, w_r, rtol=1e-5, atol=1e-7)
+    top = ref.double().sort(-1, descending=True).values
+    margin = (top[:, case.k - 1] - top[:, case.k]).min().item()
+    diff = (fixed.double() - ref.double()).abs().max().item()
+    print(f"config {config}: min top-k margin {margin:.3e}, max |fixed - F.linear| {diff:.3e}")
+    assert margin > diff
+
+
+@pytest.mark.parametrize("activation,score_fn,shared", [
+    (orc.SWIGLU, orc.SOFTMAX, False), (orc.RELU2, orc.SIGMOID, True)])
+def test_reference_eager_forward_is_the_layer(activation, score_fn, shared):
+    """The torch-ops CPU baseline computes the same layer as moe_forward with the reference
+    router (distinct logits, so the tie order cannot matter)."""
+    g = torch.Generator().manual_seed(41)
+    T, d, E, k, H = 80, 32, 6, 2, 16
+    Fr = 2 * H if activation == orc.SWIGLU else H
+    x = torch.randn(T, d, generator=g).to(torch.bfloat16)
+    wts = orc.Weights(router=torch.randn(E, d, generator=g) * 0.3,
+                      w1=torch.randn(E, Fr, d, generator=g) * 0.2,
+                      w2=torch.randn(E, d, H, generator=g) * 0.2,
+                      shared_w1=torch.randn(Fr, d, generator=g) * 0.2 if shared else None,
+                      shared_w2=torch.randn(d, H, generator=g) * 0.2 if shared else None,
+                      bias=torch.randn(E, generator=g))
+    out, aux = orc.reference_eager_forward(x, wts, k, score_fn=score_fn, activation=activation)
+    ref = orc.moe_forward(x, wts, k, score_fn=score_fn, activation=activation, router="reference")
+    torch.testing.assert_close(out, ref["out"], rtol=1e-5, atol=1e-6)
+    assert aux == pytest.approx(ref["aux"], rel=1e-12)
