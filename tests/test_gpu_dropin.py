@@ -140,12 +140,12 @@ def test_injected_aux_gradient_needs_no_aux_in_the_loss_and_skips_eval():
         m = MoEFFN(recipe, 2)
         _randomise_fc2(m.engine, 5)
         m.train(train)
-        m(x).float().square().sum().backward()
+        (m(x).float().square().sum() * 1e-3).backward()  # small beside the aux term
         return m.engine.router.weight.grad.clone()
     with_aux = router_grad(_recipe(aux_loss_coeff=0.5, z_loss_coeff=0.1))
     without = router_grad(_recipe(aux_loss_coeff=0.0, z_loss_coeff=0.0))
     evaluated = router_grad(_recipe(aux_loss_coeff=0.5, z_loss_coeff=0.1), train=False)
-    assert rel_l2(with_aux, without) > 1e-3
+    assert rel_l2(with_aux, without) > 1e-1
     torch.testing.assert_close(evaluated, without, rtol=1e-6, atol=1e-9)
 
 
