@@ -181,7 +181,9 @@ int nt_moe_grouped_ffn_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows, con
  *   c[r, j] = epilogue(a_r . w_s[j, :])  for r in segment s, j in [0, n_out)
  *   w  bf16 [num_segments, 2 n_out (SWIGLU) or n_out, K];  c bf16 [total_rows, n_out]
  * Requirements: K % 64 == 0, n_out % 4 == 0 (n_out % 64 == 0 for SWIGLU), 16-byte alignment;
- * workspace as for nt_moe_grouped_ffn_bf16.
+ * workspace as for nt_moe_grouped_ffn_bf16. With K >= 128 and n_out % 8 == 0 the launch runs
+ * 256 x 256 tiles with both operands staged through LDS, multiplying in the same K order as
+ * nt_moe_grouped_gemm_bf16_packed (bit-identical results).
  */
 int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                              const int32_t* src_row, const int32_t* seg_offsets,

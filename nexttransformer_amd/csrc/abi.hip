@@ -373,10 +373,17 @@ int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
     return fail(NT_MOE_ENOSPC, "grouped_gemm: workspace %zu < %zu bytes", workspace_bytes,
                 kGemmWorkspaceBytes);
   if (total_rows == 0) return ok();
-  hipError_t err = launch_grouped_gemm_bf16(a, ld_a, a_rows, src_row, seg_offsets, num_segments,
-                                            total_rows, w, K, n_out, epilogue, c,
-                                            reinterpret_cast<int*>(workspace),
-                                            reinterpret_cast<hipStream_t>(stream));
+  // 256 x 256 tiles with both operands staged through LDS when K spans two steps of 64 and
+  // output rows are whole 16-byte stores; otherwise the 2 x 4-wave macro-tile kernel
+  hipError_t err =
+      K >= 128 && n_out % 8 == 0
+          ? launch_grouped_gemm_bf16_t256(a, ld_a, a_rows, src_row, seg_offsets, num_segments,
+                                          total_rows, w, K, n_out, epilogue, c,
+                                          reinterpret_cast<hipStream_t>(stream))
+          : launch_grouped_gemm_bf16(a, ld_a, a_rows, src_row, seg_offsets, num_segments,
+                                     total_rows, w, K, n_out, epilogue, c,
+                                     reinterpret_cast<int*>(workspace),
+                                     reinterpret_cast<hipStream_t>(stream));
   return launched(err, "grouped_gemm_bf16");
 }
 

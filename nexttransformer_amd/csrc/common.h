@@ -133,6 +133,11 @@ hipError_t launch_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int6
                                            const uint16_t* wp, int K, int n_out, int epilogue,
                                            uint16_t* c, hipStream_t stream);
 int packed_gemm_min_k();
+hipError_t launch_grouped_gemm_bf16_t256(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                         const int32_t* src_row, const int32_t* seg_offsets,
+                                         int num_segments, int64_t total_rows, const uint16_t* w,
+                                         int K, int n_out, int epilogue, uint16_t* c,
+                                         hipStream_t stream);
 
 int num_cus();
 
