@@ -148,6 +148,25 @@ int nt_moe_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
                       uint16_t* x_perm, nt_moe_stream_t stream);
 
 /*
+ * nt_moe_route_plan without a workspace argument: the same outputs, the same kernels, with
+ * their scratch (ranks and per-block counts) in a static device array of the library instead.
+ * No counterpart in the reference; it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): it calls no
+ * hipMalloc, hipFree or other allocating routine. Limits: T * k <= NT_MOE_NOALLOC_MAX_ASSIGNMENTS
+ * and ceil(T / 256) * E <= NT_MOE_NOALLOC_MAX_BLOCK_COUNTS (the array is 2 MiB per GPU, held
+ * until the process ends); larger sizes fail with NT_MOE_EINVAL. The stream must belong to the
+ * current device. Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (on different streams, or from different threads) race, so serialise them.
+ */
+#define NT_MOE_NOALLOC_MAX_ASSIGNMENTS (1 << 18)
+#define NT_MOE_NOALLOC_MAX_BLOCK_COUNTS (1 << 18)
+int nt_moe_route_plan_noalloc(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
+                              const float* topk_w, int64_t T, int32_t d, int32_t k, int32_t E,
+                              int32_t* counts, int32_t* offsets, int32_t* src_row, float* perm_w,
+                              int32_t* combine_dest, float* combine_w, uint16_t* x_perm,
+                              nt_moe_stream_t stream);
+
+/*
  * Grouped expert FFN over ragged segments, bf16 MFMA with fp32 accumulation:
  *   h[r] = act(a_r . W1_s^T)  (bf16 [rows, H]),   y[r] = h[r] . W2_s^T  (bf16 [rows, d])
  * for every row r of segment s, rows [seg_offsets[s], seg_offsets[s+1]).

@@ -18,6 +18,7 @@ SCORE_SOFTMAX, SCORE_SIGMOID = 0, 1
 ACT_SWIGLU, ACT_RELU2 = 0, 1
 EPI_SWIGLU, EPI_RELU2, EPI_NONE = 0, 1, 2
 MAX_EXPERTS, MAX_TOPK, MAX_SEGMENTS, ROUTE_BLOCK = 256, 8, 512, 64
+NOALLOC_MAX_ASSIGNMENTS = NOALLOC_MAX_BLOCK_COUNTS = 1 << 18
 
 _p, _i64, _i32, _f32, _sz = (ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float,
                              ctypes.c_size_t)
@@ -36,6 +37,8 @@ SIGNATURES = {
                               _p, _p]),
     "nt_moe_route_plan": (_i32, [_p, _i64, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _sz, _p,
                                  _p, _p, _p, _p, _p]),
+    "nt_moe_route_plan_noalloc": (_i32, [_p, _i64, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p,
+                                         _p, _p, _p, _p, _p]),
     "nt_moe_grouped_gemm_bf16_packed_keep": (_i32, [_p, _i64, _i64, _p, _p, _i32, _i64, _p, _i32,
                                                     _i32, _i32, _p, _p, _p]),
     "nt_moe_grouped_wgrad_bf16": (_i32, [_p, _i64, _p, _i64, _i64, _p, _p, _i32, _i64, _i32, _i32,

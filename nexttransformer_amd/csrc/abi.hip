@@ -10,6 +10,7 @@
 #include <stdio.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "common.h"
 
@@ -282,19 +283,18 @@ int nt_moe_router_bwd(const float* logits, const int32_t* topk_ids, const float*
                   "router_bwd");
 }
 
-int nt_moe_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
-                      const float* topk_w, int64_t T, int32_t d, int32_t k, int32_t E,
-                      int32_t* counts, int32_t* offsets, void* workspace, size_t workspace_bytes,
-                      int32_t* src_row, float* perm_w, int32_t* combine_dest, float* combine_w,
-                      uint16_t* x_perm, nt_moe_stream_t stream) {
+namespace {
+
+// Argument checks shared by the route-plan entry points (everything but the scratch memory).
+int check_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
+                     const float* topk_w, int64_t T, int32_t d, int32_t k, int32_t E,
+                     const int32_t* counts, const int32_t* offsets, const int32_t* src_row,
+                     const int32_t* combine_dest, const float* combine_w, const uint16_t* x_perm) {
   int rc = check_route_shape(T, k, E);
   if (rc) return rc;
-  NT_REQUIRE(counts && offsets && workspace, "route_plan: null buffer");
+  NT_REQUIRE(counts && offsets, "route_plan: null buffer");
   NT_REQUIRE(T == 0 || (topk_ids && topk_w && src_row && combine_dest && combine_w),
              "route_plan: null buffer");
-  if (workspace_bytes < route_ws_bytes(T, k, E))
-    return fail(NT_MOE_ENOSPC, "route_plan: workspace %zu < %zu bytes", workspace_bytes,
-                route_ws_bytes(T, k, E));
   if (x_perm && T > 0) {
     NT_REQUIRE(x, "route_plan: x_perm requested without x");
     NT_REQUIRE(d > 0 && d % 8 == 0, "route_plan: d must be a positive multiple of 8, got %d", d);
@@ -302,11 +302,102 @@ int nt_moe_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
     NT_REQUIRE(aligned16(x) && aligned16(x_perm),
                "route_plan: x and x_perm must be 16-byte aligned");
   }
+  return NT_MOE_OK;
+}
+
+}  // namespace
+
+int nt_moe_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
+                      const float* topk_w, int64_t T, int32_t d, int32_t k, int32_t E,
+                      int32_t* counts, int32_t* offsets, void* workspace, size_t workspace_bytes,
+                      int32_t* src_row, float* perm_w, int32_t* combine_dest, float* combine_w,
+                      uint16_t* x_perm, nt_moe_stream_t stream) {
+  int rc = check_route_plan(x, ld_x, topk_ids, topk_w, T, d, k, E, counts, offsets, src_row,
+                            combine_dest, combine_w, x_perm);
+  if (rc) return rc;
+  NT_REQUIRE(workspace, "route_plan: null buffer");
+  if (workspace_bytes < route_ws_bytes(T, k, E))
+    return fail(NT_MOE_ENOSPC, "route_plan: workspace %zu < %zu bytes", workspace_bytes,
+                route_ws_bytes(T, k, E));
   RouteWorkspace ws = route_ws(workspace, T, k);
   hipError_t err = launch_route_plan(x, ld_x, topk_ids, topk_w, T, d, k, E, counts, offsets,
                                      ws.ranks, ws.block_counts, src_row, perm_w, combine_dest,
                                      combine_w, x_perm, reinterpret_cast<hipStream_t>(stream));
   return launched(err, "route_plan");
+}
+
+namespace {
+
+// The route plan's scratch for nt_moe_route_plan_noalloc: NT_MOE_NOALLOC_MAX_ASSIGNMENTS ranks,
+// then NT_MOE_NOALLOC_MAX_BLOCK_COUNTS per-block expert counts (2 MiB). Each GPU holds its own
+// copy at its own address until the process ends. Host code never passes the array's name to a
+// kernel (on the host it is only a stand-in): it uses the device address that
+// hipGetSymbolAddress returns, looked up once per device with that device current.
+constexpr int64_t kNoAllocRanks = NT_MOE_NOALLOC_MAX_ASSIGNMENTS;
+constexpr int64_t kNoAllocBlockCounts = NT_MOE_NOALLOC_MAX_BLOCK_COUNTS;
+static __device__ __align__(256) int32_t scratch[kNoAllocRanks + kNoAllocBlockCounts];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+int32_t* g_scratch_ptr[kMaxDevices];  // device address of `scratch` on each device, or null
+
+// The current device's scratch address (looked up on the device's first call); the stream must
+// belong to that device, since the address is only valid there.
+int scratch_address(hipStream_t stream, int32_t** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(NT_MOE_EDEVICE, "route_plan_noalloc: no usable current device (%s)",
+                hipGetErrorString(err));
+  if (stream) {
+    int stream_dev = -1;
+    err = hipStreamGetDevice(stream, &stream_dev);
+    if (err != hipSuccess)
+      return fail(NT_MOE_EDEVICE, "route_plan_noalloc: hipStreamGetDevice: %s",
+                  hipGetErrorString(err));
+    NT_REQUIRE(stream_dev == dev,
+               "route_plan_noalloc: the stream belongs to device %d but device %d is current",
+               stream_dev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p)
+      return fail(NT_MOE_EDEVICE, "route_plan_noalloc: hipGetSymbolAddress: %s",
+                  hipGetErrorString(err));
+    g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return NT_MOE_OK;
+}
+
+}  // namespace
+
+int nt_moe_route_plan_noalloc(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
+                              const float* topk_w, int64_t T, int32_t d, int32_t k, int32_t E,
+                              int32_t* counts, int32_t* offsets, int32_t* src_row, float* perm_w,
+                              int32_t* combine_dest, float* combine_w, uint16_t* x_perm,
+                              nt_moe_stream_t stream) {
+  int rc = check_route_plan(x, ld_x, topk_ids, topk_w, T, d, k, E, counts, offsets, src_row,
+                            combine_dest, combine_w, x_perm);
+  if (rc) return rc;
+  const int64_t nblk = (T + kHistBlock - 1) / kHistBlock;
+  NT_REQUIRE(T * k <= kNoAllocRanks,
+             "route_plan_noalloc: T * k = %lld exceeds the static scratch's %lld assignments",
+             (long long)(T * k), (long long)kNoAllocRanks);
+  NT_REQUIRE(nblk * E <= kNoAllocBlockCounts,
+             "route_plan_noalloc: ceil(T / %d) * E = %lld exceeds the static scratch's %lld "
+             "block counts", kHistBlock, (long long)(nblk * E), (long long)kNoAllocBlockCounts);
+  int32_t* base = nullptr;
+  rc = scratch_address(reinterpret_cast<hipStream_t>(stream), &base);
+  if (rc) return rc;
+  // Every scratch value the kernels read is written earlier in the same call (ranks of every
+  // assignment, counts of every block and expert), so nothing needs clearing between calls.
+  hipError_t err = launch_route_plan(x, ld_x, topk_ids, topk_w, T, d, k, E, counts, offsets,
+                                     base, base + kNoAllocRanks, src_row, perm_w, combine_dest,
+                                     combine_w, x_perm, reinterpret_cast<hipStream_t>(stream));
+  return launched(err, "route_plan_noalloc");
 }
 
 size_t nt_moe_grouped_gemm_workspace_bytes(void) { return kGemmWorkspaceBytes; }
