@@ -14,7 +14,9 @@ SwiGLU epilogue, 2/3 of the layer's FLOP). bf16 configs: bound "mfma", algorithm
 launch = 2 * (T k) * d * 2H. Config 5: bound "hbm", algorithmic bytes per launch = the e4m3
 weights and scales of the experts that received tokens + the quantised token rows once + h
 written. The average launch duration is measured with HIP events recorded on the launch stream
-around every launch inside the timed region. `traffic` (HBM bytes per launch) comes from the
+around every launch inside the timed region. With --graph the timed forwards replay HIP graphs
+captured from the forward (three segments, so the events sit between replays), and the replays'
+output is checked bit for bit against an eager forward. `traffic` (HBM bytes per launch) comes from the
 rocprofv3 FETCH_SIZE / WRITE_SIZE summary in profiles/traffic.json, when present.
 
 cpu_baseline: the reference's eager CPU layer restated with torch's own ops (oracle/, the
@@ -49,6 +51,10 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--permute-rows", action="store_true",
                    help="move token rows with the permute kernel instead of gathering in the GEMM")
+    p.add_argument("--graph", action="store_true",
+                   help="replay HIP graphs captured from the forward in the timed region instead of "
+                        "launching every kernel from Python (slower on ROCm 7 at config 2: "
+                        "0.323 vs 0.301 ms per forward)")
     p.add_argument("--train", action="store_true",
                    help="time forward + backward (bf16 configs) instead of the forward")
     p.add_argument("--cpu-budget-s", type=float, default=30.0)
@@ -153,6 +159,38 @@ def train_bench(args, case, cpu, g):
                   "frac": round(wg_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
                   "flop_per_step": up + down, "ms_per_step": round(wg_ms, 5)}}
     print(json.dumps(result), flush=True)
+
+
+class Segments(list):
+    """HIP graphs of consecutive pieces of one forward (replayed in order), with its outputs."""
+    out = None
+    aux = None
+
+
+def capture_segments(forward, cuts):
+    """Captures forward(mark) into len(cuts) + 1 HIP graphs that share one memory pool: a new
+    graph starts after each stage named in `cuts` (mark is called once a stage is enqueued).
+    The forward must have run eagerly before (the library's lazy set-up stays out of capture)."""
+    import torch
+    graphs = Segments([torch.cuda.CUDAGraph()])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    pool = torch.cuda.graph_pool_handle()
+    with torch.cuda.stream(side):
+        graphs[0].capture_begin(pool=pool)
+
+        def mark(name):
+            if name in cuts:
+                graphs[-1].capture_end()
+                graphs.append(torch.cuda.CUDAGraph())
+                graphs[-1].capture_begin(pool=pool)
+        graphs.out, graphs.aux, _ = forward(mark)
+        graphs[-1].capture_end()
+    torch.cuda.current_stream().wait_stream(side)
+    if len(graphs) != len(cuts) + 1:
+        raise RuntimeError(f"capture_segments: the forward marked {len(graphs) - 1} of the "
+                           f"{len(cuts)} cut points")
+    return graphs
 
 
 def gpu_inputs(case, fp8):
@@ -330,25 +368,46 @@ def main():
     load_ratio = counts.max().item() / counts.float().mean().item()
     log(f"[bench] warm-up done ({args.warmup} steps); expert load max/mean {load_ratio:.2f}")
 
-    # Timed region: K full forwards; HIP events bracket every up-projection GEMM launch.
+    # Timed region: K full forwards, every kernel launched from Python, with HIP events recorded
+    # on the launch stream around every up-projection launch. With --graph each forward instead
+    # replays three HIP graphs captured from it (routing, the up-projection GEMM, the rest), the
+    # events recorded between the replays.
     before_up = "quantize" if fp8 else "route_plan"
     stream = torch.cuda.current_stream()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(args.steps)]
+    graphs = capture_segments(forward, (before_up, "gemm_up")) if args.graph else None
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        def mark(name, i=i):
-            if name == before_up:
-                ev[i][0].record(stream)
-            elif name == "gemm_up":
-                ev[i][1].record(stream)
-        forward(mark)
+        if graphs is None:
+            def mark(name, i=i):
+                if name == before_up:
+                    ev[i][0].record(stream)
+                elif name == "gemm_up":
+                    ev[i][1].record(stream)
+            forward(mark)
+        else:
+            graphs[0].replay()
+            ev[i][0].record(stream)
+            graphs[1].replay()
+            ev[i][1].record(stream)
+            graphs[2].replay()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms = (t1 - t0) * 1e3 / args.steps
     up_ms = sum(a.elapsed_time(b) for a, b in ev) / args.steps
-    log(f"[bench] timed {args.steps} steps: {ms:.4f} ms/step, gemm_up {up_ms:.4f} ms")
+    log(f"[bench] timed {args.steps} steps ({'eager' if graphs is None else 'graph replay'}): "
+        f"{ms:.4f} ms/step, gemm_up {up_ms:.4f} ms")
+    replay_ok = None
+    if graphs is not None:  # the replays' results equal an eager forward's, bit for bit
+        out_e, aux_e, _ = forward()
+        torch.cuda.synchronize()
+        replay_ok = bool(torch.equal(graphs.out.view(torch.int16), out_e.view(torch.int16))
+                         and torch.equal(graphs.aux, aux_e))
+        if not replay_ok:
+            log("[bench] graph replay differs from the eager forward")
+            sys.exit(1)
 
     # Per-stage breakdown (separate instrumented pass, outside the timed region).
     reps = 10
@@ -408,6 +467,8 @@ def main():
         "layer_tflops": round(layer_flops(case) / (ms * 1e-3) / 1e12, 2),
         "expert_load_max_over_mean": round(load_ratio, 3),
         "stages_ms": stage,
+        "launch": "eager" if graphs is None else "hip_graph_replay",
+        "graph_replay_matches_eager": replay_ok,
     }
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")
