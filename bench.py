@@ -47,7 +47,9 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=50)
-    p.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    p.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6],
+                   help="1-5: the benchmark configurations; 6: the registered T3 expert cell "
+                        "(moe-T3-L20 shapes) on 16384 tokens")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--permute-rows", action="store_true",
                    help="move token rows with the permute kernel instead of gathering in the GEMM")
@@ -84,36 +86,68 @@ def calibrate_copy(reps=20, nbytes=1 << 30):
                       "GB_per_s": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}), flush=True)
 
 
+def train_layer(case, cpu):
+    """An MoELayer (aux gradient injected at scale 1) holding the case's weights as its fp32
+    masters (and the case's logit bias, if any)."""
+    import torch
+    from nexttransformer_amd.moe import MoELayer
+    from nexttransformer_amd.moe_recipe import MoERecipe
+    recipe = MoERecipe(layers=2, width=case.d, heads=max(1, case.d // 64), sequence_len=case.T,
+                       global_batch_tokens=case.T, routed_experts=case.E, top_k=case.k,
+                       expert_width=case.H, score_function=("softmax", "sigmoid")[case.score_fn],
+                       activation=("swiglu", "relu2")[case.activation],
+                       shared_experts=1 if case.shared_H else 0,
+                       shared_expert_width=case.shared_H or None, allow_any_expert_width=True)
+    layer = MoELayer(recipe, 1)
+    with torch.no_grad():
+        layer.router.weight.copy_(cpu["router"])
+        for i, e in enumerate(layer.experts.local_experts):
+            e.linear_fc1.weight.copy_(cpu["w1"][i])
+            e.linear_fc2.weight.copy_(cpu["w2"][i])
+        if case.shared_H:
+            layer.shared_experts.linear_fc1.weight.copy_(cpu["shared_w1"][0])
+            layer.shared_experts.linear_fc2.weight.copy_(cpu["shared_w2"][0])
+    if cpu["bias"] is not None:
+        layer.logit_bias = cpu["bias"].cuda()
+    return layer
+
+
 def train_bench(args, case, cpu, g):
-    """Forward + backward steps (bf16 experts): the forward keeps what the backward reads, the
-    backward gets a fixed random output gradient and a unit aux-loss gradient. Prints one JSON
-    line; the per-stage split of the backward comes from a separate instrumented pass."""
+    """Training steps of the module: MoELayer forward + backward through autograd (loss = <out, G>
+    with a fixed random G, the aux-loss gradient injected at scale 1), bf16 experts. A step's
+    time is the forward + backward on the layer's cached operands plus the rebuild of those
+    operands from the fp32 masters that every optimizer update triggers (bf16 cast / pack, the
+    backward's transposed operands), timed on its own after bumping every master's version
+    (gradient-accumulation micro-steps skip the rebuild). Prints one JSON line; the per-stage
+    split comes from a separate instrumented pass of ops.moe_forward / ops.moe_backward on the
+    same cached operands."""
     import torch
     from nexttransformer_amd import ops
+    from nexttransformer_amd.moe import set_aux_loss_scale
     if g["w1_scale"] is not None:
-        log("bench.py --train: the backward covers bf16 experts (configs 1-4)")
+        log("bench.py --train: the backward covers bf16 experts")
         sys.exit(2)
-    dev = torch.device("cuda")
-    bf = torch.bfloat16
-    w1b, w2b = cpu["w1"].to(bf).to(dev), cpu["w2"].to(bf).to(dev)
-    sw1b = sw2b = None
-    if cpu["shared_w1"] is not None:
-        sw1b, sw2b = cpu["shared_w1"].to(bf).to(dev), cpu["shared_w2"].to(bf).to(dev)
-    bw = ops.backward_weights(w1b, w2b, sw1b, sw2b)
-    grad_out = (torch.randn(case.T, case.d, generator=torch.Generator().manual_seed(1))
-                .to(bf).to(dev))
-    grad_aux = torch.tensor([1.0, 0.0, 0.0], device=dev)
-    stream = torch.cuda.current_stream()
+    set_aux_loss_scale(1.0, device="cuda")
+    layer = train_layer(case, cpu)
+    params = list(layer.parameters())
+    x = g["x"]
+    G = torch.randn(case.T, case.d, generator=torch.Generator().manual_seed(1)).to(
+        torch.bfloat16).cuda()
 
-    def step(mark_f=None, mark_b=None):
-        _, _, st = ops.moe_forward(g["x"], g["wt"], g["w1"], g["w2"], top_k=case.k,
-                                   score_fn=case.score_fn, activation=case.activation,
-                                   logit_bias=g["bias"], shared_w1=g["shared_w1"],
-                                   shared_w2=g["shared_w2"], packed=g["packed"],
-                                   want_logits=True, keep=True, mark=mark_f)
-        return ops.moe_backward(grad_out, grad_aux, g["x"], g["wt"], bw, st, top_k=case.k,
-                                score_fn=case.score_fn, activation=case.activation,
-                                mark=mark_b)
+    def step():
+        for p in params:
+            p.grad = None
+        out, _ = layer(x)
+        out.backward(G)
+
+    def prepare():
+        """Rebuilds every operand the kernels read from the masters (as after an optimizer
+        step): the bf16 cast / pack, the backward's transposed operands and the router's."""
+        w = layer.packed_weights(keep_plain=True)
+        bw = layer.backward_weights(w)
+        bw.w1t, bw.w2t, bw.shared, bw.first(w["router_t"])
+        if not w["packed"]:  # the fc1 recompute operand: the forward keeps no fc1 then
+            bw.w1
 
     for _ in range(max(1, args.warmup)):
         step()
@@ -122,9 +156,25 @@ def train_bench(args, case, cpu, g):
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    reps = 5
-    stage = {}
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    prep = []
+    for _ in range(5):
+        with torch.no_grad():
+            for p in params:
+                p.add_(0.0)  # a new version of every master
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        prepare()
+        torch.cuda.synchronize()
+        prep.append((time.perf_counter() - t0) * 1e3)
+    prep_ms = sorted(prep)[len(prep) // 2]
+    ms = ms_step + prep_ms
+
+    # per-stage split on the layer's cached operands
+    w = layer.packed_weights(keep_plain=True)
+    bw = layer.backward_weights(w)
+    stream = torch.cuda.current_stream()
+    stage, reps, kept = {}, 5, None
     for _ in range(reps):
         evs = [("start", torch.cuda.Event(enable_timing=True))]
         evs[0][1].record(stream)
@@ -133,31 +183,48 @@ def train_bench(args, case, cpu, g):
             e = torch.cuda.Event(enable_timing=True)
             e.record(stream)
             evs.append((name, e))
-        step(lambda n: mark("fwd_" + n), lambda n: mark("bwd_" + n))
+        _, _, st = ops.moe_forward(x, w["router_t"], w["w1"], w["w2"], top_k=case.k,
+                                   score_fn=case.score_fn, activation=case.activation,
+                                   logit_bias=layer.logit_bias, shared_w1=w["shared_w1"],
+                                   shared_w2=w["shared_w2"], packed=w["packed"],
+                                   want_logits=True, keep=True, mark=lambda n: mark("fwd_" + n))
+        kept = st["fc1"] is not None
+        ops.moe_backward(G, torch.tensor([1.0, 0.0, 0.0], device="cuda"), x, w["router_t"], bw,
+                         st, top_k=case.k, score_fn=case.score_fn, activation=case.activation,
+                         mark=lambda n: mark("bwd_" + n))
         torch.cuda.synchronize()
         for (_, a), (n, b) in zip(evs, evs[1:]):
             stage[n] = stage.get(n, 0.0) + a.elapsed_time(b) / reps
     A = case.T * case.k
     F = 2 * case.H if case.activation == 0 else case.H
+    Fs = 2 * case.shared_H if case.activation == 0 else case.shared_H
     up, down = 2.0 * A * case.d * F, 2.0 * A * case.H * case.d
-    # forward: up + down; backward: fc1 recompute + dgrad of both + wgrad of both
-    flops = 4 * up + 3 * down + 3 * 2.0 * case.T * case.d * case.E
-    # the backward's dominant kernel: the two expert weight gradients (dW1: up-sized, dW2:
-    # down-sized), timed by the instrumented pass's events around them
+    sup, sdown = 2.0 * case.T * case.d * Fs, 2.0 * case.T * case.shared_H * case.d
+    router = 2.0 * case.T * case.d * case.E
+    # forward: up + down; backward: dgrad and wgrad of both (+ the fc1 recompute when the forward
+    # kept no pre-activations); the shared expert likewise; the router GEMM once forward and its
+    # two gradient products
+    flops = ((3 if kept else 4) * up + 3 * down + 4 * sup + 3 * sdown + 3 * router)
     wg_ms = stage.get("bwd_wgrad", 0.0)
-    wg_tflops = (up + down) / (wg_ms * 1e-3) / 1e12 if wg_ms > 0 else None
-    result = {"metric": "MoE layer forward+backward tokens/s", "value": round(case.T / (ms * 1e-3), 1),
-              "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-              "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
-              "vs_baseline": None, "dtype": "bf16", "data": "synthetic, seed 0",
-              "config": describe(case, args.config, False, False),
+    wg_flop = up + down + sup + sdown
+    wg_tflops = wg_flop / (wg_ms * 1e-3) / 1e12 if wg_ms > 0 else None
+    result = {"metric": "MoE layer training step (forward + backward) tokens/s",
+              "value": round(case.T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+              "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+              "ms_forward_backward": round(ms_step, 5),
+              "ms_weight_preparation": round(prep_ms, 5),
+              "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+              "data": "synthetic, seed 0", "config": describe(case, args.config, False, False),
+              "path": "MoELayer forward + autograd backward on cached operands, plus the "
+                      "rebuild of those operands after a weight update (median of 5)",
+              "fc1_kept_by_forward": kept,
               "layer_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
               "stages_ms": {n: round(v, 5) for n, v in stage.items()},
               "roofline": None if wg_tflops is None else {
-                  "kernel": "grouped_wgrad_kernel (dW1 + dW2)", "bound": "mfma",
+                  "kernel": "grouped_wgrad_kernel (dW1 + dW2, shared expert's)", "bound": "mfma",
                   "achieved": round(wg_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                   "frac": round(wg_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                  "flop_per_step": up + down, "ms_per_step": round(wg_ms, 5)}}
+                  "flop_per_step": wg_flop, "ms_per_step": round(wg_ms, 5)}}
     print(json.dumps(result), flush=True)
 
 

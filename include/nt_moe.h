@@ -211,6 +211,17 @@ int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                              void* workspace, size_t workspace_bytes, nt_moe_stream_t stream);
 
 /*
+ * Weight preparation: the fp32 master weights w [num_matrices, rows, cols] to bf16, in one read:
+ * out [num_matrices, rows, cols] (the cast MasterLinear applies before each product,
+ * megatron_moe.py:74-75) and out_t [num_matrices, cols, rows] (its transpose, the dgrad
+ * operand of the backward); either may be NULL. Rounding to nearest even. rows and cols
+ * multiples of 64; 16-byte aligned buffers.
+ */
+int nt_moe_convert_expert_weights(const float* w, int64_t num_matrices, int32_t rows,
+                                  int32_t cols, uint16_t* out, uint16_t* out_t,
+                                  nt_moe_stream_t stream);
+
+/*
  * Packed-weight variant of the grouped GEMM. nt_moe_pack_expert_weights_bf16 rearranges
  * w [num_segments, rows, K] once (same bytes, fragment order: 32-row x 64-K blocks in which
  * each lane's 16-byte operand chunk is contiguous with its neighbours', rows inside a block
@@ -367,13 +378,30 @@ int nt_moe_act_bwd(const uint16_t* fc1, const uint16_t* grad_h, int64_t rows, in
  *   c[s, n, m] = sum over rows r of segment s of a[r, n] * b[row(r), m]   (bf16 [S, N, M])
  * row(r) = b_src_row[r] when given (e.g. the gathered token rows), else r. With a = grad_y,
  * b = h this is dW2; with a = grad_fc1, b = x and b_src_row = src_row, dW1. An empty segment's
- * matrix is zero. N and M multiples of 128; lda, ldb multiples of 8.
+ * matrix is zero. N and M multiples of 64; lda, ldb multiples of 8.
  */
 int nt_moe_grouped_wgrad_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                               int64_t b_rows, const int32_t* b_src_row,
                               const int32_t* seg_offsets, int32_t num_segments,
                               int64_t total_rows, int32_t N, int32_t M, uint16_t* c,
                               nt_moe_stream_t stream);
+
+/*
+ * nt_moe_grouped_wgrad_bf16 with the reduction over each segment's rows split into `splits`
+ * chunks (consecutive runs of whole 64-row slabs) that run as separate workgroups, for long
+ * segments: the shared expert's weight gradient (one segment of all T rows,
+ * megatron_moe.py:133,150) and the router's weight gradient (grad_logits^T x,
+ * megatron_moe.py:95-99) would otherwise occupy only a few CUs. The chunks' fp32 sums go to
+ * `partial` (fp32 [splits, num_segments, N, M], partial_bytes >= splits * num_segments * N * M
+ * * 4; unused when splits == 1) and are added in ascending chunk order -- a fixed order -- into
+ * c: fp32 [num_segments, N, M] when c_fp32, else bf16 (rounded once).
+ */
+int nt_moe_grouped_wgrad_splitk(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                                int64_t b_rows, const int32_t* b_src_row,
+                                const int32_t* seg_offsets, int32_t num_segments,
+                                int64_t total_rows, int32_t N, int32_t M, int32_t splits,
+                                float* partial, size_t partial_bytes, int32_t c_fp32, void* c,
+                                nt_moe_stream_t stream);
 
 int nt_moe_router_bwd(const float* logits, const int32_t* topk_ids, const float* topk_w,
                       const float* grad_w, const int32_t* counts, int64_t T, int32_t E,

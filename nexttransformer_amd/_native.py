@@ -43,6 +43,8 @@ SIGNATURES = {
                                                     _i32, _i32, _p, _p, _p]),
     "nt_moe_grouped_wgrad_bf16": (_i32, [_p, _i64, _p, _i64, _i64, _p, _p, _i32, _i64, _i32, _i32,
                                          _p, _p]),
+    "nt_moe_grouped_wgrad_splitk": (_i32, [_p, _i64, _p, _i64, _i64, _p, _p, _i32, _i64, _i32,
+                                           _i32, _i32, _p, _sz, _i32, _p, _p]),
     "nt_moe_combine_bwd": (_i32, [_p, _i64, _p, _p, _p, _p, _i64, _i32, _i32, _p, _p, _p]),
     "nt_moe_act_bwd": (_i32, [_p, _p, _i64, _i32, _i32, _p, _p]),
     "nt_moe_router_bwd": (_i32, [_p, _p, _p, _p, _p, _i64, _i32, _i32, _i32, _p, _f32, _f32, _p,
@@ -52,6 +54,7 @@ SIGNATURES = {
                                        _i32, _p, _p, _p, _sz, _p]),
     "nt_moe_grouped_gemm_bf16": (_i32, [_p, _i64, _i64, _p, _p, _i32, _i64, _p, _i32, _i32, _i32,
                                         _p, _p, _sz, _p]),
+    "nt_moe_convert_expert_weights": (_i32, [_p, _i64, _i32, _i32, _p, _p, _p]),
     "nt_moe_pack_expert_weights_bf16": (_i32, [_p, _i64, _i32, _i32, _i32, _p, _p]),
     "nt_moe_grouped_gemm_bf16_packed": (_i32, [_p, _i64, _i64, _p, _p, _i32, _i64, _p, _i32, _i32,
                                                _i32, _p, _p]),

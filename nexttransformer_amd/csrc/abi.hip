@@ -243,13 +243,13 @@ int nt_moe_act_bwd(const uint16_t* fc1, const uint16_t* grad_h, int64_t rows, in
                   "act_bwd");
 }
 
-int nt_moe_grouped_wgrad_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
-                              int64_t b_rows, const int32_t* b_src_row,
-                              const int32_t* seg_offsets, int32_t num_segments,
-                              int64_t total_rows, int32_t N, int32_t M, uint16_t* c,
-                              nt_moe_stream_t stream) {
-  NT_REQUIRE(N > 0 && N % 128 == 0 && M > 0 && M % 128 == 0,
-             "grouped_wgrad: N and M must be positive multiples of 128, got %d, %d", N, M);
+namespace {
+
+int check_wgrad(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t b_rows,
+                const int32_t* b_src_row, const int32_t* seg_offsets, int32_t num_segments,
+                int64_t total_rows, int32_t N, int32_t M, const void* c) {
+  NT_REQUIRE(N > 0 && N % 64 == 0 && M > 0 && M % 64 == 0,
+             "grouped_wgrad: N and M must be positive multiples of 64, got %d, %d", N, M);
   NT_REQUIRE(num_segments >= 1 && num_segments <= NT_MOE_MAX_SEGMENTS,
              "grouped_wgrad: num_segments must be in [1, %d]", NT_MOE_MAX_SEGMENTS);
   NT_REQUIRE(total_rows >= 0 && total_rows < ((int64_t)1 << 31), "grouped_wgrad: bad total_rows");
@@ -260,10 +260,46 @@ int nt_moe_grouped_wgrad_bf16(const uint16_t* a, int64_t lda, const uint16_t* b,
   NT_REQUIRE(a && b && seg_offsets && c, "grouped_wgrad: null buffer");
   NT_REQUIRE(aligned16(a) && aligned16(b) && aligned16(c),
              "grouped_wgrad: buffers must be 16-byte aligned");
+  return NT_MOE_OK;
+}
+
+}  // namespace
+
+int nt_moe_grouped_wgrad_bf16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                              int64_t b_rows, const int32_t* b_src_row,
+                              const int32_t* seg_offsets, int32_t num_segments,
+                              int64_t total_rows, int32_t N, int32_t M, uint16_t* c,
+                              nt_moe_stream_t stream) {
+  int rc = check_wgrad(a, lda, b, ldb, b_rows, b_src_row, seg_offsets, num_segments, total_rows,
+                       N, M, c);
+  if (rc) return rc;
   return launched(launch_grouped_wgrad(a, lda, b, ldb, b_rows, b_src_row, seg_offsets,
-                                       num_segments, total_rows, N, M, c,
+                                       num_segments, total_rows, N, M, 1, nullptr, false, c,
                                        reinterpret_cast<hipStream_t>(stream)),
                   "grouped_wgrad");
+}
+
+int nt_moe_grouped_wgrad_splitk(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                                int64_t b_rows, const int32_t* b_src_row,
+                                const int32_t* seg_offsets, int32_t num_segments,
+                                int64_t total_rows, int32_t N, int32_t M, int32_t splits,
+                                float* partial, size_t partial_bytes, int32_t c_fp32, void* c,
+                                nt_moe_stream_t stream) {
+  int rc = check_wgrad(a, lda, b, ldb, b_rows, b_src_row, seg_offsets, num_segments, total_rows,
+                       N, M, c);
+  if (rc) return rc;
+  NT_REQUIRE(splits >= 1 && splits <= 256, "grouped_wgrad_splitk: splits must be in [1, 256]");
+  const size_t need = splits > 1 ? (size_t)splits * num_segments * N * M * sizeof(float) : 0;
+  if (splits > 1) {
+    NT_REQUIRE(partial && aligned16(partial), "grouped_wgrad_splitk: null or unaligned partial");
+    if (partial_bytes < need)
+      return fail(NT_MOE_ENOSPC, "grouped_wgrad_splitk: partial %zu < %zu bytes", partial_bytes,
+                  need);
+  }
+  return launched(launch_grouped_wgrad(a, lda, b, ldb, b_rows, b_src_row, seg_offsets,
+                                       num_segments, total_rows, N, M, splits, partial,
+                                       c_fp32 != 0, c, reinterpret_cast<hipStream_t>(stream)),
+                  "grouped_wgrad_splitk");
 }
 
 int nt_moe_router_bwd(const float* logits, const int32_t* topk_ids, const float* topk_w,
@@ -476,6 +512,20 @@ int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                                      reinterpret_cast<int*>(workspace),
                                      reinterpret_cast<hipStream_t>(stream));
   return launched(err, "grouped_gemm_bf16");
+}
+
+int nt_moe_convert_expert_weights(const float* w, int64_t num_matrices, int32_t rows,
+                                  int32_t cols, uint16_t* out, uint16_t* out_t,
+                                  nt_moe_stream_t stream) {
+  NT_REQUIRE(num_matrices >= 0 && rows > 0 && rows % 64 == 0 && cols > 0 && cols % 64 == 0,
+             "convert_expert_weights: rows and cols must be positive multiples of 64, got %d x %d",
+             rows, cols);
+  if (num_matrices == 0 || (!out && !out_t)) return ok();
+  NT_REQUIRE(w && aligned16(w) && (!out || aligned16(out)) && (!out_t || aligned16(out_t)),
+             "convert_expert_weights: null or unaligned buffer");
+  return launched(launch_convert_weights(w, num_matrices, rows, cols, out, out_t,
+                                         reinterpret_cast<hipStream_t>(stream)),
+                  "convert_expert_weights");
 }
 
 int nt_moe_pack_expert_weights_bf16(const uint16_t* w, int64_t num_segments, int32_t rows,

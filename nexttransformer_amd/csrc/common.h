@@ -75,7 +75,8 @@ hipError_t launch_grouped_gemm_bf16_packed_keep(const uint16_t* a, int64_t ld_a,
 hipError_t launch_grouped_wgrad(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                                 int64_t b_rows, const int32_t* b_src_row,
                                 const int32_t* seg_offsets, int num_segments, int64_t total_rows,
-                                int N, int M, uint16_t* c, hipStream_t stream);
+                                int N, int M, int splits, float* partial, bool c_f32, void* c,
+                                hipStream_t stream);
 hipError_t launch_combine_bwd(const uint16_t* g, int64_t ld_g, const uint16_t* y,
                               const int32_t* topk_ids, const int32_t* combine_dest,
                               const float* combine_w, int64_t T, int d, int k, uint16_t* dy,
@@ -133,6 +134,8 @@ hipError_t launch_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int6
                                            const uint16_t* wp, int K, int n_out, int epilogue,
                                            uint16_t* c, hipStream_t stream);
 int packed_gemm_min_k();
+hipError_t launch_convert_weights(const float* w, int64_t S, int R, int K, uint16_t* out,
+                                  uint16_t* out_t, hipStream_t stream);
 hipError_t launch_grouped_gemm_bf16_t256(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                                          const int32_t* src_row, const int32_t* seg_offsets,
                                          int num_segments, int64_t total_rows, const uint16_t* w,

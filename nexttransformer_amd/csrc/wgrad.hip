@@ -13,7 +13,13 @@
 // fragment reads are then 16-byte ds_read_b128 of 8 consecutive rows. Workgroup = 128 (n) x
 // 128 (m) tile of one segment, 4 waves of 64 x 64 (2 x 2 MFMA blocks), LDS double-buffered
 // (72 KB, two workgroups per CU), the next slab's global loads in flight during the current
-// slab's MFMAs. An empty segment's tiles are written as zeros.
+// slab's MFMAs. An empty segment's tiles are written as zeros. N and M are multiples of 64: a
+// last tile 64 wide reads clamped columns and stores only the columns that exist.
+// Split K: with `splits` > 1 each segment's rows are cut into `splits` consecutive chunks of
+// whole 64-row slabs, each chunk's tile a workgroup of its own writing fp32 partial sums
+// partial[i][s]; sum_splits_kernel then adds the chunks in ascending i (a fixed order, so the
+// result does not depend on scheduling) -- for long segments (a shared expert's single segment
+// of every token, the router's weight gradient) that would otherwise leave most CUs idle.
 #include "common.h"
 
 namespace ntmoe {
@@ -33,22 +39,33 @@ __device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
+// OUT_F32: store fp32 (the split-K partials) instead of bf16.
+template <bool OUT_F32>
 __global__ __launch_bounds__(256) void grouped_wgrad_kernel(
     const uint16_t* __restrict__ a, int64_t lda, const uint16_t* __restrict__ b, int64_t ldb,
     int64_t b_rows, const int32_t* __restrict__ b_src_row, const int32_t* __restrict__ seg_offsets,
-    int64_t total_rows, int N, int M, uint16_t* __restrict__ c) {
+    int num_segments, int64_t total_rows, int N, int M, int splits, void* __restrict__ c) {
   __shared__ __align__(16) uint16_t lds[2][2][kWSlab];  // [buffer][operand A, B][col][row]
-  const int ntn = N / kWT, ntm = M / kWT;
+  const int ntn = (N + kWT - 1) / kWT, ntm = (M + kWT - 1) / kWT;
   const int per_seg = ntn * ntm;
-  const int s = blockIdx.x / per_seg;
-  const int tile = blockIdx.x - s * per_seg;
+  const int split = blockIdx.x / (num_segments * per_seg);
+  const int rest = blockIdx.x - split * num_segments * per_seg;
+  const int s = rest / per_seg;
+  const int tile = rest - s * per_seg;
   const int n0 = (tile / ntm) * kWT, m0 = (tile % ntm) * kWT;
   int64_t lo = seg_offsets[s], hi = seg_offsets[s + 1];
   lo = lo < 0 ? 0 : (lo > total_rows ? total_rows : lo);
   hi = hi < lo ? lo : (hi > total_rows ? total_rows : hi);
+  if (splits > 1) {  // this chunk: whole 64-row slabs, the last chunk ending at hi
+    const int64_t slabs = (hi - lo + kWK - 1) / kWK;
+    const int64_t per = (slabs + splits - 1) / splits;
+    const int64_t c_lo = lo + split * per * kWK, c_hi = c_lo + per * kWK;
+    lo = c_lo < hi ? c_lo : hi;
+    hi = c_hi < hi ? c_hi : hi;
+  }
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int wn = wave >> 1, wm = wave & 1;  // the wave's 64 x 64 quarter
-  uint16_t* cs = c + (int64_t)s * N * M;
+  const int64_t c_base = ((int64_t)split * num_segments + s) * N * M;
 
   floatx16 acc[2][2];
 #pragma unroll
@@ -66,7 +83,10 @@ __global__ __launch_bounds__(256) void grouped_wgrad_kernel(
     // 16-byte bank groups (columns 8 apart map to the same group)
     const int rg = lt & 7;         // 0..7: rows 8 rg .. 8 rg + 7 of the slab
     const int cg = lt >> 3;        // 0..15: columns 8 cg .. 8 cg + 7 of the tile
-    const uint16_t* base = op == 0 ? a + n0 + 8 * cg : b + m0 + 8 * cg;
+    // columns past N (or M) in a 64-wide last tile re-read the last 8 columns; their products
+    // land in outputs that are not stored
+    const int col = (op == 0 ? n0 : m0) + 8 * cg, width = op == 0 ? N : M;
+    const uint16_t* base = (op == 0 ? a : b) + (col < width ? col : width - 8);
     const int64_t ld = op == 0 ? lda : ldb;
     // Gathered B rows: the row indices of a slab are loaded one slab ahead of its data (idx), so
     // the data loads do not wait on an index load.
@@ -140,6 +160,8 @@ __global__ __launch_bounds__(256) void grouped_wgrad_kernel(
     }
   }
   // acc[i][j]: n = n0 + 64 wn + 32 i + lane % 32, m = m0 + 64 wm + 32 j + 8 (q / 4) + 4 (lane / 32) + q % 4
+  // (a 64-wide last tile: the quarter past N or M is not stored)
+  if (n0 + 64 * wn >= N || m0 + 64 * wm >= M) return;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int n = n0 + 64 * wn + 32 * i + (lane & 31);
@@ -148,12 +170,37 @@ __global__ __launch_bounds__(256) void grouped_wgrad_kernel(
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int m = m0 + 64 * wm + 32 * j + 8 * g + 4 * (lane >> 5);
-        u32x2 o;
-        o[0] = pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]);
-        o[1] = pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
-        *reinterpret_cast<u32x2*>(cs + (int64_t)n * M + m) = o;
+        const int64_t off = c_base + (int64_t)n * M + m;
+        if constexpr (OUT_F32) {
+          const floatx4 o = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                             acc[i][j][4 * g + 3]};
+          *reinterpret_cast<floatx4*>(reinterpret_cast<float*>(c) + off) = o;
+        } else {
+          u32x2 o;
+          o[0] = pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]);
+          o[1] = pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(c) + off) = o;
+        }
       }
     }
+  }
+}
+
+// out[j] = sum over i = 0, 1, ..., splits - 1 (in that order) of partial[i][j], fp32, stored as
+// fp32 or rounded once to bf16; 4 consecutive elements per thread.
+template <bool OUT_F32>
+__global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict__ partial,
+                                                         int splits, int64_t count,
+                                                         void* __restrict__ out) {
+  const int64_t j = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (j >= count) return;
+  floatx4 v = *reinterpret_cast<const floatx4*>(partial + j);
+  for (int i = 1; i < splits; ++i) v = v + *reinterpret_cast<const floatx4*>(partial + i * count + j);
+  if constexpr (OUT_F32) {
+    *reinterpret_cast<floatx4*>(reinterpret_cast<float*>(out) + j) = v;
+  } else {
+    const u32x2 o = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(out) + j) = o;
   }
 }
 
@@ -162,11 +209,25 @@ __global__ __launch_bounds__(256) void grouped_wgrad_kernel(
 hipError_t launch_grouped_wgrad(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                                 int64_t b_rows, const int32_t* b_src_row,
                                 const int32_t* seg_offsets, int num_segments, int64_t total_rows,
-                                int N, int M, uint16_t* c, hipStream_t stream) {
-  const int64_t blocks = (int64_t)num_segments * (N / kWT) * (M / kWT);
-  if (blocks == 0) return hipSuccess;
-  hipLaunchKernelGGL(grouped_wgrad_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a, lda,
-                     b, ldb, b_rows, b_src_row, seg_offsets, total_rows, N, M, c);
+                                int N, int M, int splits, float* partial, bool c_f32, void* c,
+                                hipStream_t stream) {
+  const int64_t tiles = (int64_t)num_segments * ((N + kWT - 1) / kWT) * ((M + kWT - 1) / kWT);
+  if (tiles == 0) return hipSuccess;
+  if (splits <= 1) {
+    auto kern = c_f32 ? grouped_wgrad_kernel<true> : grouped_wgrad_kernel<false>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256), 0, stream, a, lda, b, ldb, b_rows,
+                       b_src_row, seg_offsets, num_segments, total_rows, N, M, 1, c);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL(grouped_wgrad_kernel<true>, dim3((unsigned)(tiles * splits)), dim3(256), 0,
+                     stream, a, lda, b, ldb, b_rows, b_src_row, seg_offsets, num_segments,
+                     total_rows, N, M, splits, static_cast<void*>(partial));
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  const int64_t count = (int64_t)num_segments * N * M;  // a multiple of 4096
+  auto sum = c_f32 ? sum_splits_kernel<true> : sum_splits_kernel<false>;
+  hipLaunchKernelGGL(sum, dim3((unsigned)((count / 4 + 255) / 256)), dim3(256), 0, stream,
+                     partial, splits, count, c);
   return hipGetLastError();
 }
 

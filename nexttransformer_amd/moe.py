@@ -119,6 +119,29 @@ class LocalExperts(nn.Module):
             ExpertMLP(width, hidden, gated, device) for _ in range(count))
 
 
+def _pool_masters(linears):
+    """Puts the fp32 weights of same-shaped linears into one contiguous [n, rows, cols] buffer
+    and makes each linear's weight a Parameter on its slice (same names, shapes and values), so
+    the stack of them needs no copy; returns the buffer."""
+    w0 = linears[0].weight
+    pool = torch.empty((len(linears),) + tuple(w0.shape), device=w0.device, dtype=w0.dtype)
+    for i, lin in enumerate(linears):
+        pool[i].copy_(lin.weight.detach())
+        lin.weight = nn.Parameter(pool[i], requires_grad=lin.weight.requires_grad)
+    return pool
+
+
+def _stacked(pool, weights):
+    """[n, rows, cols] fp32 of the weights: the pool itself when every weight still sits on its
+    slice of it (in-place updates keep that; replacing a weight's tensor, or moving the module
+    to another device, does not), else a stacked copy."""
+    if pool is not None and pool.device == weights[0].device:
+        base, step = pool.data_ptr(), pool.stride(0) * pool.element_size()
+        if all(w.data_ptr() == base + i * step for i, w in enumerate(weights)):
+            return pool
+    return torch.stack([w.detach() for w in weights])
+
+
 def _ep_size(pg_collection):
     ep = getattr(pg_collection, "ep", None)
     if ep is None:
@@ -129,58 +152,46 @@ def _ep_size(pg_collection):
 
 class _MoETrain(torch.autograd.Function):
     """The layer with gradients (bf16 experts): ops.moe_forward, then ops.moe_backward. Its
-    inputs are the fp32 masters (the experts' stacked), so gradients reach the parameters; the
-    bf16 copies the GEMMs read are made here, as MasterLinear casts its master per call
-    (megatron_moe.py:58-78)."""
+    inputs after x are the fp32 masters themselves (router.weight, each expert's fc1 and fc2, the
+    shared expert's), so autograd hands each its own gradient; the bf16 operands the kernels read
+    are the layer's cached copies of those masters (MasterLinear casts its master per call,
+    megatron_moe.py:58-78; the cache is rebuilt when a master changes)."""
 
     @staticmethod
-    def forward(ctx, x, router_w, w1, w2, sw1, sw2, cfg):
-        bf = torch.bfloat16
-        wr_t = router_w.detach().t().contiguous()
-        w1b = w1.detach().to(bf).contiguous()
-        w2b = w2.detach().to(bf).contiguous()
-        sw1b = sw1.detach().to(bf).contiguous() if sw1 is not None else None
-        sw2b = sw2.detach().to(bf).contiguous() if sw2 is not None else None
-        up = nat.EPI_SWIGLU if cfg["activation"] == nat.ACT_SWIGLU else nat.EPI_RELU2
-        H = w2b.shape[2]
-        widths = [(H, w2b.shape[1])] + ([(sw2b.shape[2], sw2b.shape[1])] if sw1b is not None else [])
-        packed = all(ops.packable(d, h, up) and ops.packable(h, d, nat.EPI_NONE)
-                     for h, d in widths)
-        fw = (lambda w, e: ops.pack_expert_weights(w, e)) if packed else (lambda w, e: w)
+    def forward(ctx, x, cfg, *masters):
+        layer = cfg["layer"]
+        w = layer.packed_weights(keep_plain=True)
         out, aux, state = ops.moe_forward(
-            x, wr_t, fw(w1b, up), fw(w2b, nat.EPI_NONE), top_k=cfg["top_k"],
-            score_fn=cfg["score_fn"], activation=cfg["activation"], aux_coeff=cfg["aux_coeff"],
-            z_coeff=cfg["z_coeff"],
-            shared_w1=fw(sw1b, up) if sw1b is not None else None,
-            shared_w2=fw(sw2b, nat.EPI_NONE) if sw2b is not None else None,
-            want_logits=True, packed=packed, keep=True)
+            x, w["router_t"], w["w1"], w["w2"], top_k=cfg["top_k"], score_fn=cfg["score_fn"],
+            activation=cfg["activation"], aux_coeff=cfg["aux_coeff"], z_coeff=cfg["z_coeff"],
+            logit_bias=layer.logit_bias, shared_w1=w["shared_w1"], shared_w2=w["shared_w2"],
+            want_logits=True, packed=w["packed"], keep=True)
         cfg["counts"] = state["counts"]
-        ctx.cfg = cfg
-        ctx.state = state
-        ctx.tensors = (x, wr_t, w1b, w2b, sw1b, sw2b)
+        ctx.cfg, ctx.state, ctx.x, ctx.w = cfg, state, x, w
         return out, aux
 
     @staticmethod
     def backward(ctx, grad_out, grad_aux):
-        x, wr_t, w1b, w2b, sw1b, sw2b = ctx.tensors
-        cfg = ctx.cfg
-        if x.shape[0] == 0:
-            z = lambda t: None if t is None else torch.zeros(t.shape, device=t.device)
-            return (torch.zeros_like(x), z(wr_t.t()), z(w1b), z(w2b), z(sw1b), z(sw2b), None)
+        cfg, x, w = ctx.cfg, ctx.x, ctx.w
+        layer = cfg["layer"]
+        bw = layer.backward_weights(w)
         if cfg["inject"]:  # MCore: the aux gradient arrives whatever the caller's loss holds
             injected = _injected_aux_grad(x.device)
             grad_aux = injected if grad_aux is None else grad_aux + injected
         if grad_out is None:
             grad_out = torch.zeros(x.shape, device=x.device, dtype=torch.bfloat16)
-        bw = ops.backward_weights(w1b, w2b, sw1b, sw2b)
         g = ops.moe_backward(grad_out, None if grad_aux is None else grad_aux.contiguous(), x,
-                             wr_t, bw, ctx.state, top_k=cfg["top_k"], score_fn=cfg["score_fn"],
-                             activation=cfg["activation"], aux_coeff=cfg["aux_coeff"],
-                             z_coeff=cfg["z_coeff"])
-        ctx.state = ctx.tensors = None
-        f = lambda t: None if t is None else t.float()
-        return (g["x"], g["router"], f(g["w1"]), f(g["w2"]), f(g["shared_w1"]),
-                f(g["shared_w2"]), None)
+                             w["router_t"], bw, ctx.state, top_k=cfg["top_k"],
+                             score_fn=cfg["score_fn"], activation=cfg["activation"],
+                             aux_coeff=cfg["aux_coeff"], z_coeff=cfg["z_coeff"])
+        ctx.state = ctx.x = ctx.w = None
+        g1, g2 = g["w1"].float(), g["w2"].float()
+        grads = [g["x"], None, g["router"]]
+        for i in range(g1.shape[0]):
+            grads += [g1[i], g2[i]]
+        if g["shared_w1"] is not None:
+            grads += [g["shared_w1"][0].float(), g["shared_w2"][0].float()]
+        return tuple(grads)
 
 
 class MoELayer(nn.Module):
@@ -213,13 +224,23 @@ class MoELayer(nn.Module):
         self.router = Router(recipe.routed_experts, recipe.width, device)
         self.experts = LocalExperts(recipe.routed_experts, recipe.width, recipe.expert_width,
                                     gated, device)
+        experts = list(self.experts.local_experts)
+        self._fc1_pool = _pool_masters([e.linear_fc1 for e in experts])
+        self._fc2_pool = _pool_masters([e.linear_fc2 for e in experts])
+        self._pool_ptrs = None  # the pooled weights' addresses on their pool slices
+        self._param_tables = None
         self.shared_experts = (ExpertMLP(recipe.width, recipe.shared_expert_width, gated, device)
                                if recipe.shared_experts else None)
+        # Optional fixed per-expert logit bias [E] fp32 added after the gating GEMM (not a
+        # parameter; None = no bias, the reference router): used to impose a routing skew.
+        self.register_buffer("logit_bias", None)
         self.last_load = None
         self.last_aux_loss = None
         self.last_aux_parts = None
         self._pack_key = None
         self._packed = None
+        self._bw_key = None
+        self._bw = None
         self.reset_parameters()
 
     # -- initialisation --------------------------------------------------------------------
@@ -247,19 +268,58 @@ class MoELayer(nn.Module):
         nn.init.normal_(w, std=r.router_init_std, generator=_seeded(base + r.routed_experts + 1))
         self.router.weight.copy_(w)
         self._pack_key = None
+        self._bw_key = None
 
     # -- packed bf16 weights ---------------------------------------------------------------
 
-    def _masters(self):
-        ps = [self.router.weight]
-        for e in self.experts.local_experts:
-            ps += [e.linear_fc1.weight, e.linear_fc2.weight]
-        if self.shared_experts is not None:
-            ps += [self.shared_experts.linear_fc1.weight, self.shared_experts.linear_fc2.weight]
-        return ps
+    def _masters(self, pooled_only=False):
+        """router.weight, each expert's fc1 and fc2 weights, then the shared expert's (read from
+        the modules' parameter tables, which a replaced weight updates in place)."""
+        if self._param_tables is None:
+            lins = []
+            for e in self.experts.local_experts:
+                lins += [e.linear_fc1, e.linear_fc2]
+            shared = ([] if self.shared_experts is None else
+                      [self.shared_experts.linear_fc1, self.shared_experts.linear_fc2])
+            self._param_tables = ([self.router._parameters],
+                                  [lin._parameters for lin in lins],
+                                  [lin._parameters for lin in shared])
+        router, pooled, shared = self._param_tables
+        if pooled_only:
+            return [t["weight"] for t in pooled]
+        return [t["weight"] for t in router + pooled + shared]
+
+    def _masters_key(self):
+        """Identifies the current values of every master: the tensors' addresses and version
+        counters. The pooled expert weights share their pool's version counter (an in-place
+        update of any of them bumps it), so while they all sit on their pool slices one
+        version stands for each pool."""
+        masters = self._masters()
+        ptrs = tuple(p.data_ptr() for p in masters)
+        pools = (self._fc1_pool, self._fc2_pool)
+        if self._pool_ptrs is None:
+            self._pool_ptrs = None if pools[0] is None else tuple(
+                p.data_ptr() for p in self._masters(pooled_only=True))
+        if self._pool_ptrs is not None and ptrs[1:1 + len(self._pool_ptrs)] == self._pool_ptrs:
+            n = 1 + len(self._pool_ptrs)
+            return (ptrs, masters[0]._version, pools[0]._version, pools[1]._version,
+                    tuple(p._version for p in masters[n:]))
+        return ptrs, tuple(p._version for p in masters)
 
     @torch.no_grad()
-    def packed_weights(self):
+    def backward_weights(self, w):
+        """The backward's GEMM operands for the cached weights `w` (packed_weights(keep_plain=
+        True)), built once per weight version (each operand on first use)."""
+        if self._bw_key is not self._pack_key or self._bw is None:
+            self._bw = ops.backward_weights(w["w1_plain"], w["w2_plain"], w["shared_w1_plain"],
+                                            w["shared_w2_plain"], w["router_t"],
+                                            w1_t=w["w1_t"], w2_t=w["w2_t"],
+                                            shared_w2_t=w["shared_w2_t"])
+            self._bw_key = self._pack_key
+        return self._bw
+
+    @torch.no_grad()
+    def packed_weights(self, keep_plain=False):
         """Device weights the kernels read, rebuilt only when a master tensor changed:
         router_t fp32 [dp, E]; w1 [E, rows, dp]; w2 [E, dp, Hp]; shared_w1/2 [1, ...];
         bf16 (in the packed fragment order of pack_expert_weights when `packed`), or for
@@ -272,9 +332,8 @@ class MoELayer(nn.Module):
         a zero hidden unit has act(0) = 0 under both SwiGLU and ReLU^2, so the padded layer
         computes the same values (an all-zero fp8 block gets scale 1 and codes 0).
         """
-        masters = self._masters()
-        key = tuple((p.data_ptr(), p._version) for p in masters)
-        if key != self._pack_key:
+        key = self._masters_key()
+        if key != self._pack_key or (keep_plain and "w1_plain" not in self._packed):
             r = self.recipe
             fp8 = r.expert_dtype == "fp8"
             align = 128 if fp8 else 64
@@ -288,8 +347,24 @@ class MoELayer(nn.Module):
                 ops.packable(dp, _round_up(h, align), nat.EPI_SWIGLU if gated else nat.EPI_RELU2)
                 and ops.packable(_round_up(h, align), dp, nat.EPI_NONE) for h in widths))
 
-            def stack(experts, hidden):
+            def stack(experts, hidden, pools=(None, None)):
                 hp = _round_up(hidden, align)
+                if not fp8 and hp == hidden and dp == r.width and self.router.weight.is_cuda:
+                    # one pass over the fp32 masters: the bf16 copy (and, for the backward, its
+                    # transpose)
+                    w1, w1t = ops.convert_expert_weights(
+                        _stacked(pools[0], [e.linear_fc1.weight for e in experts]), True,
+                        keep_plain)
+                    w2, w2t = ops.convert_expert_weights(
+                        _stacked(pools[1], [e.linear_fc2.weight for e in experts]), True,
+                        keep_plain)
+                    plain.append((w1, w2, w1t if keep_plain else None,
+                                  w2t if keep_plain else None))
+                    up = nat.EPI_SWIGLU if gated else nat.EPI_RELU2
+                    if use_packed:
+                        return (ops.pack_expert_weights(w1, up), None,
+                                ops.pack_expert_weights(w2, nat.EPI_NONE), None)
+                    return w1, None, w2, None
                 if hp == hidden and dp == r.width:
                     w1 = torch.stack([e.linear_fc1.weight.detach() for e in experts]).to(dtype)
                     w2 = torch.stack([e.linear_fc2.weight.detach() for e in experts]).to(dtype)
@@ -308,6 +383,7 @@ class MoELayer(nn.Module):
                         w2[i, :r.width, :hidden] = e.linear_fc2.weight.detach()
                 if not fp8:
                     up = nat.EPI_SWIGLU if gated else nat.EPI_RELU2
+                    plain.append((w1.contiguous(), w2.contiguous(), None, None))
                     if use_packed:
                         return (ops.pack_expert_weights(w1.contiguous(), up), None,
                                 ops.pack_expert_weights(w2.contiguous(), nat.EPI_NONE), None)
@@ -318,16 +394,23 @@ class MoELayer(nn.Module):
                 return (ops.pack_expert_weights_fp8(w1q, up), w1s,
                         ops.pack_expert_weights_fp8(w2q, nat.EPI_NONE), w2s)
 
+            plain = []  # the bf16 [E, rows, cols] stacks before packing (for the backward)
             router_t = torch.zeros(dp, r.routed_experts, device=self.router.weight.device,
                                    dtype=torch.float32)
             router_t[:r.width] = self.router.weight.detach().t()
             packed = dict(router_t=router_t, shared_w1=None, shared_w2=None,
                           shared_w1_scale=None, shared_w2_scale=None, packed=use_packed)
             (packed["w1"], packed["w1_scale"], packed["w2"],
-             packed["w2_scale"]) = stack(list(self.experts.local_experts), r.expert_width)
+             packed["w2_scale"]) = stack(list(self.experts.local_experts), r.expert_width,
+                                         (self._fc1_pool, self._fc2_pool))
             if self.shared_experts is not None:
                 (packed["shared_w1"], packed["shared_w1_scale"], packed["shared_w2"],
                  packed["shared_w2_scale"]) = stack([self.shared_experts], r.shared_expert_width)
+            if keep_plain and not fp8:
+                (packed["w1_plain"], packed["w2_plain"], packed["w1_t"],
+                 packed["w2_t"]) = plain[0]
+                (packed["shared_w1_plain"], packed["shared_w2_plain"], _,
+                 packed["shared_w2_t"]) = plain[1] if len(plain) > 1 else (None,) * 4
             self._packed = packed
             self._pack_key = key
         return self._packed
@@ -358,7 +441,7 @@ class MoELayer(nn.Module):
         out, aux, state = ops.moe_forward(
             x, w["router_t"], w["w1"], w["w2"], top_k=r.top_k,
             score_fn=_SCORE[r.score_function], activation=_ACT[r.activation],
-            aux_coeff=r.aux_loss_coeff, z_coeff=r.z_loss_coeff,
+            aux_coeff=r.aux_loss_coeff, z_coeff=r.z_loss_coeff, logit_bias=self.logit_bias,
             shared_w1=w["shared_w1"], shared_w2=w["shared_w2"], w1_scale=w["w1_scale"],
             w2_scale=w["w2_scale"], shared_w1_scale=w["shared_w1_scale"],
             shared_w2_scale=w["shared_w2_scale"], packed=w["packed"])
@@ -379,19 +462,14 @@ class MoELayer(nn.Module):
         if r.expert_dtype == "fp8" or any(w % 64 for w in widths):
             raise RuntimeError("the MoE backward covers bf16 experts whose widths are multiples "
                                "of 64; run this configuration under torch.no_grad()")
+        if not self.router.weight.is_cuda:
+            raise ValueError("the MoE layer runs on the GPU only (no CPU path)")
         x = hidden.reshape(-1, r.width).to(torch.bfloat16).contiguous()
-        experts = list(self.experts.local_experts)
-        w1 = torch.stack([e.linear_fc1.weight for e in experts])
-        w2 = torch.stack([e.linear_fc2.weight for e in experts])
-        sw1 = sw2 = None
-        if self.shared_experts is not None:
-            sw1 = self.shared_experts.linear_fc1.weight.unsqueeze(0)
-            sw2 = self.shared_experts.linear_fc2.weight.unsqueeze(0)
         inject = self.aux_grad == "inject"
-        cfg = dict(top_k=r.top_k, score_fn=_SCORE[r.score_function],
+        cfg = dict(layer=self, top_k=r.top_k, score_fn=_SCORE[r.score_function],
                    activation=_ACT[r.activation], aux_coeff=r.aux_loss_coeff,
                    z_coeff=r.z_loss_coeff, inject=inject and self.training)
-        out, aux = _MoETrain.apply(x, self.router.weight, w1, w2, sw1, sw2, cfg)
+        out, aux = _MoETrain.apply(x, cfg, *self._masters())
         self.last_load = cfg["counts"].to(torch.int64)
         self.last_aux_parts = aux.detach()
         # "inject": the gradient comes from the backward itself, so the returned value is

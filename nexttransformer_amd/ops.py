@@ -253,6 +253,30 @@ def _(w, epilogue):
     return torch.empty_like(w)
 
 
+@torch.library.custom_op("ntmoe::convert_expert_weights", mutates_args=())
+def convert_expert_weights(w: Tensor, want_out: bool, want_t: bool) -> tuple[Tensor, Tensor]:
+    """fp32 [S, R, K] -> (bf16 [S, R, K] or empty, bf16 [S, K, R] or empty), one read of w."""
+    _on_gpu(w)
+    _require(w.dtype == torch.float32 and w.dim() == 3 and w.is_contiguous(),
+             "convert_expert_weights: w must be contiguous fp32 [S, R, K]")
+    S, R, K = w.shape
+    out = torch.empty((S, R, K) if want_out else (0,), device=w.device, dtype=torch.bfloat16)
+    out_t = torch.empty((S, K, R) if want_t else (0,), device=w.device, dtype=torch.bfloat16)
+    st = nat.load().nt_moe_convert_expert_weights(ptr(w), S, R, K,
+                                                  ptr(out) if want_out else None,
+                                                  ptr(out_t) if want_t else None,
+                                                  _stream(w.device))
+    nat.check(st, "ntmoe::convert_expert_weights")
+    return out, out_t
+
+
+@convert_expert_weights.register_fake
+def _(w, want_out, want_t):
+    S, R, K = w.shape
+    return (w.new_empty((S, R, K) if want_out else (0,), dtype=torch.bfloat16),
+            w.new_empty((S, K, R) if want_t else (0,), dtype=torch.bfloat16))
+
+
 def packable(K, n_out, epilogue):
     """Whether a [*, n_out or 2 n_out, K] weight stack qualifies for the packed GEMM."""
     return K >= 256 and K % 128 == 0 and n_out % (16 if epilogue == nat.EPI_SWIGLU else 32) == 0
@@ -676,8 +700,10 @@ def _(logits, ids, weights, grad_w, counts, score_fn, grad_aux, aux_coeff, z_coe
 
 @torch.library.custom_op("ntmoe::grouped_wgrad", mutates_args=())
 def grouped_wgrad(a: Tensor, b: Tensor, b_src_row: Optional[Tensor], seg_offsets: Tensor,
-                  total_rows: int) -> Tensor:
-    """c [S, N, M] bf16: c[s] = sum over segment s's rows r of a[r]^T b[row(r)]."""
+                  total_rows: int, splits: int = 1, out_fp32: bool = False) -> Tensor:
+    """c [S, N, M]: c[s] = sum over segment s's rows r of a[r]^T b[row(r)], bf16 (or fp32 with
+    out_fp32); with splits > 1 each segment's rows run as `splits` chunks whose fp32 sums are
+    added in ascending order (for long segments)."""
     _on_gpu(a, b, b_src_row, seg_offsets)
     _require(a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16 and a.dim() == 2
              and b.dim() == 2 and a.stride(1) == 1 and b.stride(1) == 1,
@@ -689,17 +715,49 @@ def grouped_wgrad(a: Tensor, b: Tensor, b_src_row: Optional[Tensor], seg_offsets
                  "grouped_wgrad: b_src_row must be contiguous int32")
     S = seg_offsets.shape[0] - 1
     N, M = a.shape[1], b.shape[1]
-    c = torch.empty(S, N, M, device=a.device, dtype=torch.bfloat16)
-    st = nat.load().nt_moe_grouped_wgrad_bf16(ptr(a), a.stride(0), ptr(b), b.stride(0),
-                                              b.shape[0], ptr(b_src_row), ptr(seg_offsets), S,
-                                              total_rows, N, M, ptr(c), _stream(a.device))
+    c = torch.empty(S, N, M, device=a.device, dtype=torch.float32 if out_fp32 else torch.bfloat16)
+    partial = None
+    if splits > 1:
+        partial = torch.empty(splits, S, N, M, device=a.device, dtype=torch.float32)
+    st = nat.load().nt_moe_grouped_wgrad_splitk(
+        ptr(a), a.stride(0), ptr(b), b.stride(0), b.shape[0], ptr(b_src_row), ptr(seg_offsets),
+        S, total_rows, N, M, splits, ptr(partial),
+        0 if partial is None else partial.numel() * 4, int(out_fp32), ptr(c), _stream(a.device))
     nat.check(st, "ntmoe::grouped_wgrad")
     return c
 
 
 @grouped_wgrad.register_fake
-def _(a, b, b_src_row, seg_offsets, total_rows):
-    return a.new_empty(seg_offsets.shape[0] - 1, a.shape[1], b.shape[1])
+def _(a, b, b_src_row, seg_offsets, total_rows, splits=1, out_fp32=False):
+    return a.new_empty(seg_offsets.shape[0] - 1, a.shape[1], b.shape[1],
+                       dtype=torch.float32 if out_fp32 else torch.bfloat16)
+
+
+_CU_COUNT = {}
+
+
+def wgrad_splits(segments, N, M, rows_per_segment, device):
+    """Chunks per segment for grouped_wgrad: enough workgroups for about two per CU when the
+    tiles alone are fewer, each chunk at least 4 slabs (256 rows) long, at most 32."""
+    cus = _CU_COUNT.get(device)
+    if cus is None:
+        cus = _CU_COUNT.setdefault(device, torch.cuda.get_device_properties(device).multi_processor_count)
+    tiles = segments * -(-N // 128) * -(-M // 128)
+    if tiles >= 2 * cus:
+        return 1
+    return max(1, min(32, -(-2 * cus // tiles), rows_per_segment // 256))
+
+
+def split_bf16(t):
+    """(hi, lo) bf16 with hi + lo = t to within 2^-17 |t| (hi = t rounded to bf16, lo = the
+    remainder, exact in fp32, rounded to bf16): fp32 products on bf16 matrix cores as
+    hi.b + lo.b (b exact in bf16), or hi.h + hi.l + lo.h with both operands split."""
+    hi = t.to(torch.bfloat16)
+    return hi, (t - hi.float()).to(torch.bfloat16)
+
+
+def _round_up(n, m):
+    return (n + m - 1) // m * m
 
 
 class Projection:
@@ -716,17 +774,78 @@ class Projection:
         return gemm(a, src_row, seg_offsets, self.w, nat.EPI_NONE, total_rows)
 
 
-def backward_weights(w1, w2, shared_w1=None, shared_w2=None):
-    """The backward's GEMM operands from the bf16 weights the forward used (plain layout):
-    W1 (recompute of the fc1 pre-activations), W1^T and W2^T (dgrad), and the shared expert's."""
-    t = lambda w: w.transpose(1, 2).contiguous()
-    bw = dict(w1=Projection(w1), w1t=Projection(t(w1)), w2t=Projection(t(w2)), w1_plain=w1,
-              w2_plain=w2, shared=None)
-    if shared_w1 is not None:
-        bw["shared"] = dict(w1=Projection(shared_w1), w1t=Projection(t(shared_w1)),
-                            w2t=Projection(t(shared_w2)), w1_plain=shared_w1,
-                            w2_plain=shared_w2)
-    return bw
+class BackwardWeights:
+    """The backward's GEMM operands, built from the bf16 weights the forward used (plain
+    layout) and the fp32 router weight, each on first use:
+      w1t, w2t     W1^T and W2^T (dgrad of the two projections)
+      w1           W1 (recompute of the fc1 pre-activations; only when the forward kept none)
+      shared       the shared expert's W2^T (its dgrad)
+      first        the token-side first row's operand: [W1s^T | Wr_hi^T | Wr_lo^T | Wr_hi^T]
+                   (K padded to 64), so that one GEMM over [dfc1s | g_hi | g_hi | g_lo] gives the
+                   shared expert's input gradient plus grad_logits . Wr in fp32 (the router's
+                   input gradient; g = grad_logits, hi/lo its exact bf16 split) rounded once
+    """
+
+    def __init__(self, w1, w2, shared_w1=None, shared_w2=None, w_router_t=None, w1_t=None,
+                 w2_t=None, shared_w2_t=None):
+        self.w1_plain, self.w2_plain = w1, w2
+        self.shared_w1, self.shared_w2 = shared_w1, shared_w2
+        self.w_router_t = w_router_t
+        # transposes already made (convert_expert_weights), else made here on first use
+        self._t = dict(w1=w1_t, w2=w2_t, shared_w2=shared_w2_t)
+        self._cache = {}
+
+    def _transposed(self, name, w):
+        t = self._t.get(name)
+        return t if t is not None else w.transpose(1, 2).contiguous()
+
+    def _get(self, name, make):
+        if name not in self._cache:
+            self._cache[name] = make()
+        return self._cache[name]
+
+    @property
+    def w1(self):
+        return self._get("w1", lambda: Projection(self.w1_plain))
+
+    @property
+    def w1t(self):
+        return self._get("w1t", lambda: Projection(self._transposed("w1", self.w1_plain)))
+
+    @property
+    def w2t(self):
+        return self._get("w2t", lambda: Projection(self._transposed("w2", self.w2_plain)))
+
+    @property
+    def shared(self):
+        if self.shared_w1 is None:
+            return None
+        return self._get("shared", lambda: dict(
+            w1=Projection(self.shared_w1),
+            w2t=Projection(self._transposed("shared_w2", self.shared_w2))))
+
+    def first(self, w_router_t):
+        """[1, d, Kc] bf16 (see the class notes) and the column layout (Fs, Ep, Kc)."""
+        def make():
+            d, E = w_router_t.shape
+            Ep = _round_up(E, 32)
+            Fs = 0 if self.shared_w1 is None else self.shared_w1.shape[1]
+            Kc = _round_up(Fs + 3 * Ep, 64)
+            w = torch.zeros(1, d, Kc, device=w_router_t.device, dtype=torch.bfloat16)
+            if Fs:
+                w[0, :, :Fs] = self.shared_w1[0].t()
+            hi, lo = split_bf16(w_router_t)
+            w[0, :, Fs:Fs + E] = hi
+            w[0, :, Fs + Ep:Fs + Ep + E] = lo
+            w[0, :, Fs + 2 * Ep:Fs + 2 * Ep + E] = hi
+            return w, (Fs, Ep, Kc)
+        return self._get("first", make)
+
+
+def backward_weights(w1, w2, shared_w1=None, shared_w2=None, w_router_t=None, **transposes):
+    """The backward's GEMM operands (BackwardWeights) from the bf16 weights the forward used
+    (and, optionally, their transposes w1_t, w2_t, shared_w2_t)."""
+    return BackwardWeights(w1, w2, shared_w1, shared_w2, w_router_t, **transposes)
 
 
 def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
@@ -736,90 +855,88 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
 
     state: moe_forward's state from a call with want_logits=True and keep=True; bw: from
     backward_weights. Returns dict(x bf16 [T, d], router fp32 [E, d] (the router weight's, i.e.
-    of w_router_t^T), w1 [E, F, d], w2 [E, d, H], shared_w1, shared_w2 (bf16)).
+    of w_router_t^T), w1 [E, F, d], w2 [E, d, H], shared_w1, shared_w2 (bf16)). Widths d, F, H
+    (and the shared expert's) must be multiples of 64.
 
-    On the GPU kernels: fc1 recompute, dgrad of both projections (grouped GEMMs), the combine
-    transpose and routing-weight gradient, the activation backward, the token-side sum of the
-    k gradient rows (the forward's combine kernel with unit weights, the router's and the
-    shared expert's input gradients first, rounded to bf16) and
-    the router backward, the expert weight gradients (grouped_wgrad: dy^T h and d_fc1^T x over
-    each expert's rows, x gathered through src_row). The router's two fp32 products are plain
-    library GEMMs, as are the weight gradients of widths that are not multiples of 128. `mark(name)` as in
-    moe_forward.
+    All on this library's kernels: the fc1 recompute (when the forward kept no pre-activations),
+    the dgrad of both projections (grouped GEMMs), the combine transpose and routing-weight
+    gradient, the activation backward, the router backward (routing-weight, load-balance and
+    z-loss terms), the token-side sum of the k input-gradient rows (the forward's combine kernel
+    with unit weights; its first row, the shared expert's input gradient plus the router's,
+    grad_logits . Wr, comes from one grouped GEMM over the concatenated K of BackwardWeights'
+    `first` operand), and every weight gradient on grouped_wgrad: dy^T h and d_fc1^T x over each
+    expert's rows (x gathered through src_row), the shared expert's over all T rows and the
+    router's grad_logits^T x (fp32: the exact bf16 split of grad_logits, fp32 output), the last
+    two split along T in fixed order. `mark(name)` as in moe_forward.
     """
     mark = mark or (lambda name: None)
     T, d = x.shape
     E = w_router_t.shape[1]
     k = top_k
     A = T * k
+    sh = bw.shared_w1 is not None
     if T == 0:
         z = lambda t: None if t is None else torch.zeros_like(t)
-        sh = bw["shared"]
         return dict(x=torch.zeros_like(x), router=torch.zeros(E, d, device=x.device),
-                    w1=z(bw["w1_plain"]), w2=z(bw["w2_plain"]),
-                    shared_w1=None if sh is None else z(sh["w1_plain"]),
-                    shared_w2=None if sh is None else z(sh["w2_plain"]))
+                    w1=z(bw.w1_plain), w2=z(bw.w2_plain), shared_w1=z(bw.shared_w1),
+                    shared_w2=z(bw.shared_w2))
     src, offsets = state["src_row"], state["offsets"]
     cdest, ids = state["combine_dest"], state["ids"]
     g = grad_out.to(torch.bfloat16).contiguous()
     fc1 = state.get("fc1")
     if fc1 is None:  # not kept by the forward: recompute the pre-activations
-        fc1 = bw["w1"](x, src, offsets, A)
+        fc1 = bw.w1(x, src, offsets, A)
     mark("fc1_recompute")
     gy, gw = combine_bwd(g, state["y"], ids, cdest, state["combine_w"])
     mark("combine_bwd")
-    dh = bw["w2t"](gy, None, offsets, A)
+    dh = bw.w2t(gy, None, offsets, A)
     mark("dgrad_down")
     dfc1 = act_bwd(fc1, dh, activation)
     mark("act_bwd")
-    dxp = bw["w1t"](dfc1, None, offsets, A)
+    dxp = bw.w1t(dfc1, None, offsets, A)
     mark("dgrad_up")
-    dxs = None
     res = dict(shared_w1=None, shared_w2=None)
-    if bw["shared"] is not None:
-        sb = bw["shared"]
-        seg = _whole_batch_segment(T, x.device)
+    seg = _whole_batch_segment(T, x.device)
+    dfc1s = None
+    if sh:
+        sb = bw.shared
         fc1s = sb["w1"](x, None, seg, T)
         dhs = sb["w2t"](g, None, seg, T)
         dfc1s = act_bwd(fc1s, dhs, activation)
-        dxs = sb["w1t"](dfc1s, None, seg, T)
-        # one segment over all T rows: a plain library product (a single long reduction, which
-        # the grouped kernel would give to too few workgroups)
-        res["shared_w1"] = (dfc1s.t() @ x).unsqueeze(0)
-        res["shared_w2"] = (g.t() @ state["shared_h"]).unsqueeze(0)
         mark("shared")
     dlogits = router_bwd(state["logits"], ids, state["weights"], gw, state["counts"], score_fn,
                          grad_aux, aux_coeff, z_coeff)
-    # dWr = dlogits^T x in fp32: a long reduction (K = T) over a thin output, which the library
-    # tiles poorly as one product; 16 batched partial products summed in a fixed order are ~4x
-    # faster (T split into equal chunks; fewer when T is not a multiple of 16)
-    chunks = next(c for c in (16, 8, 4, 2, 1) if T % c == 0)
-    res["router"] = torch.bmm(dlogits.view(chunks, T // chunks, E).transpose(1, 2).contiguous(),
-                              x.float().view(chunks, T // chunks, d)).sum(0)
-    # the router's and the shared expert's input gradients enter the token-side sum as its
-    # first term (the combine kernel's shared row), in bf16
-    first = torch.mm(dlogits, w_router_t.t())
-    if dxs is not None:
-        first += dxs.float()
+    # the token-side first row: [dfc1s | g_hi | g_hi | g_lo] . [W1s^T | Wr_hi | Wr_lo | Wr_hi]^T
+    wf, (Fs, Ep, Kc) = bw.first(w_router_t)
+    g_hi, g_lo = split_bf16(dlogits)
+    a_cat = torch.zeros(T, Kc, device=x.device, dtype=torch.bfloat16)
+    if sh:
+        a_cat[:, :Fs] = dfc1s
+    a_cat[:, Fs:Fs + E] = g_hi
+    a_cat[:, Fs + Ep:Fs + Ep + E] = g_hi
+    a_cat[:, Fs + 2 * Ep:Fs + 2 * Ep + E] = g_lo
+    first = grouped_gemm(a_cat, None, seg, wf, nat.EPI_NONE, T)
+    # dWr = grad_logits^T x in fp32: [g_hi | g_lo]^T x (x exact in bf16), fp32 sums split along T
+    g_cat = torch.zeros(T, 2 * Ep, device=x.device, dtype=torch.bfloat16)
+    g_cat[:, :E] = g_hi
+    g_cat[:, Ep:Ep + E] = g_lo
+    wr = grouped_wgrad(g_cat, x, None, seg, T, wgrad_splits(1, 2 * Ep, d, T, x.device), True)[0]
+    res["router"] = wr[:E] + wr[Ep:Ep + E]
     mark("router_bwd")
     ones = torch.ones(T, k, device=x.device, dtype=torch.float32)
-    res["x"], _ = combine_aux(dxp, cdest, ones, first.to(torch.bfloat16), state["prob_partial"],
+    res["x"], _ = combine_aux(dxp, cdest, ones, first, state["prob_partial"],
                               state["z_partial"], state["counts"], 0.0, 0.0)
     mark("dx_sum")
-    # expert weight gradients over each expert's rows
-    F, H = bw["w1_plain"].shape[1], bw["w2_plain"].shape[2]
-    h = state["h"]
-    if F % 128 == 0 and H % 128 == 0 and d % 128 == 0:
-        res["w1"] = grouped_wgrad(dfc1, x, src, offsets, A)
-        res["w2"] = grouped_wgrad(gy, h, None, offsets, A)
-    else:  # widths the grouped kernel does not tile: per-expert library products
-        gw1 = torch.zeros(E, F, d, device=x.device, dtype=torch.bfloat16)
-        gw2 = torch.zeros(E, d, H, device=x.device, dtype=torch.bfloat16)
-        xp = x.index_select(0, src.long())
-        for e, (lo, hi) in enumerate(zip(offsets[:-1].tolist(), offsets[1:].tolist())):
-            if hi > lo:
-                gw1[e] = dfc1[lo:hi].t() @ xp[lo:hi]
-                gw2[e] = gy[lo:hi].t() @ h[lo:hi]
-        res["w1"], res["w2"] = gw1, gw2
+    # expert weight gradients over each expert's rows; the shared expert's over all T rows
+    res["w1"] = grouped_wgrad(dfc1, x, src, offsets, A, wgrad_splits(E, dfc1.shape[1], d, A // E,
+                                                                     x.device))
+    res["w2"] = grouped_wgrad(gy, state["h"], None, offsets, A,
+                              wgrad_splits(E, d, state["h"].shape[1], A // E, x.device))
+    if sh:
+        res["shared_w1"] = grouped_wgrad(dfc1s, x, None, seg, T,
+                                         wgrad_splits(1, dfc1s.shape[1], d, T, x.device))
+        res["shared_w2"] = grouped_wgrad(g, state["shared_h"], None, seg, T,
+                                         wgrad_splits(1, d, state["shared_h"].shape[1], T,
+                                                      x.device))
     mark("wgrad")
     return res

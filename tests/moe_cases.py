@@ -31,6 +31,10 @@ CONFIGS = {
     4: Case("bf16-deepseek-T8192-d2048-E128-k8-sigmoid-shared", 8192, 2048, 128, 8, 768,
             score_fn=1, shared_H=1536),
     5: Case("fp8-T64-d4096-E128-k8", 64, 4096, 128, 8, 1536),
+    # the registered T3 expert cell moe-T3-L20 (width 1280, 256 experts, top-8, ReLU^2 experts
+    # and one shared expert of width 320; configs/scaling/t3.json) on a 8 x 2048-token batch
+    6: Case("t3-moe-T3-L20-T16384-d1280-E256-k8-relu2-H320-shared", 16384, 1280, 256, 8, 320,
+            activation=1, shared_H=320),
 }
 
 

@@ -236,3 +236,41 @@ def test_kept_pre_activations_equal_a_recompute(activation):
     torch.cuda.synchronize()
     assert torch.equal(h, h_ref)
     assert torch.equal(pre, pre_ref)
+
+
+def test_convert_expert_weights_is_the_cast_and_its_transpose():
+    """One pass over fp32 masters gives exactly torch's round-to-nearest-even bf16 cast and the
+    transpose of it, for stacks whose sides are different multiples of 64."""
+    from nexttransformer_amd import ops
+    g = torch.Generator().manual_seed(51)
+    w = (torch.randn(3, 192, 320, generator=g) * torch.logspace(-6, 2, 320)).cuda()
+    out, out_t = ops.convert_expert_weights(w, True, True)
+    ref = w.to(torch.bfloat16)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(out_t.view(torch.int16), ref.transpose(1, 2).contiguous().view(torch.int16))
+    only_t = ops.convert_expert_weights(w, False, True)[1]
+    assert torch.equal(only_t, out_t)
+
+
+def test_module_keeps_masters_in_one_buffer_and_falls_back_when_replaced():
+    """The experts' fp32 masters are slices of one buffer (the weight cast reads it without a
+    stack); an expert whose weight tensor is replaced is still used, through a stacked copy."""
+    from nexttransformer_amd.moe import MoELayer
+    from nexttransformer_amd.moe_recipe import MoERecipe
+    r = MoERecipe(layers=2, width=256, heads=4, routed_experts=8, top_k=2, expert_width=64,
+                  activation="swiglu", shared_experts=0, allow_any_expert_width=True,
+                  global_batch_tokens=2048)
+    m = MoELayer(r, 2)
+    w1 = [e.linear_fc1.weight for e in m.experts.local_experts]
+    assert all(w.data_ptr() == m._fc1_pool[i].data_ptr() for i, w in enumerate(w1))
+    x = torch.randn(300, 256, generator=torch.Generator().manual_seed(52)).to(torch.bfloat16).cuda()
+    with torch.no_grad():
+        for e in m.experts.local_experts:
+            e.linear_fc2.weight.normal_(0, 0.1)
+        a, _ = m(x)
+        e3 = m.experts.local_experts[3]
+        e3.linear_fc1.weight = torch.nn.Parameter(e3.linear_fc1.weight.detach().clone() * 2)
+        b, _ = m(x)
+        e3.linear_fc1.weight.mul_(0.5)
+        c, _ = m(x)
+    assert not torch.equal(a, b) and torch.equal(a, c)

@@ -113,7 +113,7 @@ def test_backward_argument_errors_are_einval(lib):
     assert st == nat.NT_MOE_EINVAL and "E must be" in lib.nt_moe_last_error().decode()
     st = lib.nt_moe_grouped_wgrad_bf16(None, 256, None, 256, 8, None, None, 1, 8, 256, 96, None,
                                        None)
-    assert st == nat.NT_MOE_EINVAL and "multiples of 128" in lib.nt_moe_last_error().decode()
+    assert st == nat.NT_MOE_EINVAL and "multiples of 64" in lib.nt_moe_last_error().decode()
     st = lib.nt_moe_grouped_gemm_bf16_packed_keep(None, 256, 8, None, None, 1, 8, None, 256, 64,
                                                   nat.EPI_NONE, None, None, None)
     assert st == nat.NT_MOE_EINVAL and "SWIGLU or RELU2" in lib.nt_moe_last_error().decode()
