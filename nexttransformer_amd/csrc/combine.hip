@@ -16,10 +16,14 @@
 namespace ntmoe {
 namespace {
 
-// One wave per output row; the row is walked in column chunks of 64 lanes x VPC 16-byte
-// vectors (VPC = 2: 1024 bf16 per chunk) so k * VPC vectors are in flight per lane.
+// One wave per output row at a time; the row is walked in column chunks of 64 lanes x VPC
+// 16-byte vectors (VPC = 2: 1024 bf16 per chunk). Waves are persistent over tokens (t, t + the
+// grid's waves, ...) and, when the row is one chunk (d <= 1024), issue the next token's k row
+// loads before summing the current token's, so 2 k VPC vectors per lane are in flight. KMAX
+// bounds k (registers are sized by it).
 constexpr int VPC = 2;
 
+template <int KMAX>
 __device__ __forceinline__ void combine_rows(
     const uint16_t* __restrict__ y, const int32_t* __restrict__ combine_dest,
     const float* __restrict__ combine_w, int64_t T, int d, int k,
@@ -28,73 +32,108 @@ __device__ __forceinline__ void combine_rows(
   const int lane = lane_id();
   const int vecs = d >> 3;
   const int64_t waves = (int64_t)blocks * 4;
-  for (int64_t t = (int64_t)blockIdx.x * 4 + wave_id(); t < T; t += waves) {
-    int dest = 0;
-    float w = 0.f;
-    if (lane < k) {
+  const int64_t A = T * k;  // rows of y; out-of-range rows are clamped
+  // The token's k destination rows and weights, lane j holding slot j.
+  auto plan = [&](int64_t t, int& dest, float& w) {
+    dest = 0;
+    w = 0.f;
+    if (lane < k && t < T) {
       dest = combine_dest[t * k + lane];
       w = combine_w[t * k + lane];
-      const int64_t A = T * k;  // rows of y; out-of-range rows are clamped
       dest = dest < 0 ? 0 : (dest >= A ? (int)(A - 1) : dest);
     }
-    for (int v0 = 0; v0 < vecs; v0 += 64 * VPC) {
-      float acc[VPC][8];
-      if (shared_y) {
-        const u32x4* srow = reinterpret_cast<const u32x4*>(shared_y + t * ld_shared);
+  };
+  auto load_rows = [&](int dest, int v0, u32x4 (&rows)[KMAX][VPC]) {
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      if (j < k) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(y + (int64_t)__shfl(dest, j) * d);
 #pragma unroll
         for (int q = 0; q < VPC; ++q) {
-          int v = v0 + q * 64 + lane;
-          u32x4 r = v < vecs ? srow[v] : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            acc[q][2 * i] = __builtin_bit_cast(float, r[i] << 16);
-            acc[q][2 * i + 1] = __builtin_bit_cast(float, r[i] & 0xffff0000u);
-          }
+          const int v = v0 + q * 64 + lane;
+          rows[j][q] = v < vecs ? src[v] : u32x4{0u, 0u, 0u, 0u};
         }
-      } else {
+      }
+    }
+  };
+  // Sum of the shared row (if any) and the k weighted rows of chunk v0 of token t, stored.
+  auto finish = [&](int64_t t, int v0, float w, const u32x4 (&rows)[KMAX][VPC]) {
+    float acc[VPC][8];
+    if (shared_y) {
+      const u32x4* srow = reinterpret_cast<const u32x4*>(shared_y + t * ld_shared);
+#pragma unroll
+      for (int q = 0; q < VPC; ++q) {
+        const int v = v0 + q * 64 + lane;
+        const u32x4 r = v < vecs ? srow[v] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[q][2 * i] = __builtin_bit_cast(float, r[i] << 16);
+          acc[q][2 * i + 1] = __builtin_bit_cast(float, r[i] & 0xffff0000u);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < VPC; ++q)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[q][i] = 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      if (j < k) {
+        const float wj = __shfl(w, j);
 #pragma unroll
         for (int q = 0; q < VPC; ++q)
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[q][i] = 0.f;
-      }
-      u32x4 rows[NT_MOE_MAX_TOPK][VPC];
-#pragma unroll
-      for (int j = 0; j < NT_MOE_MAX_TOPK; ++j) {
-        if (j < k) {
-          const u32x4* src = reinterpret_cast<const u32x4*>(y + (int64_t)__shfl(dest, j) * d);
-#pragma unroll
-          for (int q = 0; q < VPC; ++q) {
-            int v = v0 + q * 64 + lane;
-            rows[j][q] = v < vecs ? src[v] : u32x4{0u, 0u, 0u, 0u};
+          for (int i = 0; i < 4; ++i) {
+            acc[q][2 * i] = __builtin_fmaf(
+                wj, __builtin_bit_cast(float, rows[j][q][i] << 16), acc[q][2 * i]);
+            acc[q][2 * i + 1] = __builtin_fmaf(
+                wj, __builtin_bit_cast(float, rows[j][q][i] & 0xffff0000u), acc[q][2 * i + 1]);
           }
-        }
       }
+    }
+    u32x4* orow = reinterpret_cast<u32x4*>(out + t * ld_out);
 #pragma unroll
-      for (int j = 0; j < NT_MOE_MAX_TOPK; ++j) {
-        if (j < k) {
-          const float wj = __shfl(w, j);
+    for (int q = 0; q < VPC; ++q) {
+      const int v = v0 + q * 64 + lane;
+      if (v < vecs) {
+        u32x4 r;
 #pragma unroll
-          for (int q = 0; q < VPC; ++q)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              acc[q][2 * i] = __builtin_fmaf(
-                  wj, __builtin_bit_cast(float, rows[j][q][i] << 16), acc[q][2 * i]);
-              acc[q][2 * i + 1] = __builtin_fmaf(
-                  wj, __builtin_bit_cast(float, rows[j][q][i] & 0xffff0000u), acc[q][2 * i + 1]);
-            }
-        }
+        for (int i = 0; i < 4; ++i) r[i] = pack_bf16x2(acc[q][2 * i], acc[q][2 * i + 1]);
+        orow[v] = r;
       }
-      u32x4* orow = reinterpret_cast<u32x4*>(out + t * ld_out);
+    }
+  };
+
+  int64_t t = (int64_t)blockIdx.x * 4 + wave_id();
+  if (vecs <= 64 * VPC) {  // one chunk per row: the next token's loads go out first
+    int dest, ndest;
+    float w, nw;
+    u32x4 rows[KMAX][VPC], next[KMAX][VPC];
+    plan(t, dest, w);
+    if (t < T) load_rows(dest, 0, rows);
+    for (; t < T; t += waves) {
+      const int64_t tn = t + waves;
+      plan(tn, ndest, nw);
+      if (tn < T) load_rows(ndest, 0, next);
+      finish(t, 0, w, rows);
 #pragma unroll
-      for (int q = 0; q < VPC; ++q) {
-        int v = v0 + q * 64 + lane;
-        if (v < vecs) {
-          u32x4 r;
+      for (int j = 0; j < KMAX; ++j)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) r[i] = pack_bf16x2(acc[q][2 * i], acc[q][2 * i + 1]);
-          orow[v] = r;
-        }
-      }
+        for (int q = 0; q < VPC; ++q) rows[j][q] = next[j][q];
+      dest = ndest;
+      w = nw;
+    }
+    return;
+  }
+  for (; t < T; t += waves) {
+    int dest;
+    float w;
+    plan(t, dest, w);
+    for (int v0 = 0; v0 < vecs; v0 += 64 * VPC) {
+      u32x4 rows[KMAX][VPC];
+      load_rows(dest, v0, rows);
+      finish(t, v0, w, rows);
     }
   }
 }
@@ -159,6 +198,7 @@ struct AuxArgs {
 
 // The combine grid plus, when aux.aux_out is set, one last workgroup that computes the losses
 // (they depend only on the router's partials and the counts, so they run beside the combine).
+template <int KMAX>
 __global__ __launch_bounds__(256) void combine_aux_kernel(
     const uint16_t* __restrict__ y, const int32_t* __restrict__ combine_dest,
     const float* __restrict__ combine_w, int64_t T, int d, int k,
@@ -170,8 +210,8 @@ __global__ __launch_bounds__(256) void combine_aux_kernel(
               aux.aux_coeff, aux.z_coeff, aux.aux_out);
     return;
   }
-  combine_rows(y, combine_dest, combine_w, T, d, k, shared_y, ld_shared, out, ld_out,
-               combine_blocks);
+  combine_rows<KMAX>(y, combine_dest, combine_w, T, d, k, shared_y, ld_shared, out, ld_out,
+                     combine_blocks);
 }
 
 }  // namespace
@@ -185,13 +225,18 @@ hipError_t launch_combine_aux(const uint16_t* y, const int32_t* combine_dest,
   AuxArgs aux{prob_partial, z_partial, counts, ceil_div(T, kRouteBlock), E, 1, aux_coeff,
               z_coeff, aux_out};
   while (aux.P * 2 * E <= kAuxThreads) aux.P *= 2;
+  // persistent waves, as many as stay resident at the variant's register use (each then takes
+  // several tokens), or one per token
   int64_t blocks = (T + 3) / 4;
-  const int64_t cap = (int64_t)num_cus() * 32;
+  const int per_cu = k <= 2 ? 7 : (k <= 4 ? 4 : 3);
+  const int64_t cap = (int64_t)num_cus() * per_cu;
   if (blocks > cap) blocks = cap;
   if (aux_out) ++blocks;
   if (blocks == 0) return hipSuccess;
-  hipLaunchKernelGGL(combine_aux_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, y,
-                     combine_dest, combine_w, T, d, k, shared_y, ld_shared, out, ld_out, aux);
+  auto kern = k <= 2 ? combine_aux_kernel<2> : (k <= 4 ? combine_aux_kernel<4>
+                                                        : combine_aux_kernel<NT_MOE_MAX_TOPK>);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream, y, combine_dest,
+                     combine_w, T, d, k, shared_y, ld_shared, out, ld_out, aux);
   hipError_t err = hipGetLastError();
   return err;
 }
