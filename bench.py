@@ -509,8 +509,13 @@ def main():
     else:
         up_flop = 2.0 * A * case.d * F
         achieved = up_flop / (up_ms * 1e-3) / 1e12
-        roofline = {"kernel": ("grouped_gemm_packed_kernel" if g["packed"] else "grouped_gemm_kernel")
-                              + " (up-projection + SwiGLU epilogue)",
+        # the plain-weight entry point takes the 256x256 kernel when K >= 128 and the output
+        # width is a multiple of 8 (nt_moe_grouped_gemm_bf16)
+        n_out = case.H
+        plain = "grouped_gemm_t256_kernel" if case.d >= 128 and n_out % 8 == 0 else "grouped_gemm_kernel"
+        epi = "SwiGLU" if case.activation == 0 else "ReLU^2"
+        roofline = {"kernel": ("grouped_gemm_packed_kernel" if g["packed"] else plain)
+                              + f" (up-projection + {epi} epilogue)",
                     "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                     "traffic": load_traffic(f"config{args.config}"),

@@ -233,7 +233,15 @@ struct RouterBlock {
       const int e = (c_lo + (rr + 1) * nch / R) * kRouterChunk;
       return e < d ? e : d;
     };
-    const int n_stages = (FE(0) - F(0) + kStageF - 1) / kStageF;  // range 0 is the longest
+    // Every wave steps through the stages of the longest range (the split rounds down, so the
+    // ranges differ by up to one chunk and the longest is not always range 0); a shorter
+    // range's surplus stages hold no groups and their chains are dropped.
+    int n_stages = 0;
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+      const int s = (FE(rr) - F(rr) + kStageF - 1) / kStageF;
+      n_stages = s > n_stages ? s : n_stages;
+    }
     struct Regs {
       u32x4 x[XP];
       float w[WP];

@@ -73,17 +73,24 @@ def test_router_logits_and_topk_bit_exact(case):
     torch.testing.assert_close(zp.cpu().double().sum(), lse2, rtol=1e-5, atol=1e-5)
 
 
-@pytest.mark.parametrize("T", [512, 4096])
-@pytest.mark.parametrize("E", [32, 64, 128])
-@pytest.mark.parametrize("variant", ["no-buffers", "workspace", "logits-buffer"])
-def test_router_variants_bit_exact_via_abi(variant, E, T):
+VARIANTS = ([(v, E, T, 1024) for v in ("no-buffers", "workspace", "logits-buffer")
+             for E in (32, 64, 128) for T in (512, 4096)]
+            # 5 and 10 chunks of 128 features: the fused and logits kernels split them over four
+            # feature ranges of unequal length (1,1,1,2 and 2,3,2,3 chunks)
+            + [(v, E, T, d) for d in (640, 1280) for v in ("no-buffers", "logits-buffer")
+               for E in (32, 128) for T in (512, 4096)]
+            + [(v, 256, 4096, d) for d in (640, 1280) for v in ("workspace", "logits-buffer")])
+
+
+@pytest.mark.parametrize("variant,E,T,d", VARIANTS, ids=lambda v: str(v))
+def test_router_variants_bit_exact_via_abi(variant, E, T, d):
     """Raw C-ABI calls that reach each router kernel (on a 256-CU part): with neither workspace
     nor a logits buffer the fused kernel (top-k in the block; one, two and four expert blocks);
     with the workspace the chunk planes (T = 512) or the logits kernel + top-k (T = 4096); with
     only a logits buffer the logits kernel. All follow the same order: identical bits."""
     import ctypes
     from nexttransformer_amd import _native as nat
-    case = Case("variant", T, 1024, E, 4, 64, seed=11)
+    case = Case("variant", T, d, E, 4, 64, seed=11)
     cpu, g = gpu_inputs(case)
     lib = nat.load()
     d, k = case.d, case.k
