@@ -137,9 +137,9 @@ int nt_moe_router_fwd(const uint16_t* x, int64_t ld_x, const float* w_router_t,
   NT_REQUIRE(x && w_router_t && topk_ids && topk_w && prob_partial && z_partial,
              "router: null buffer");
   NT_REQUIRE(aligned16(x), "router: x must be 16-byte aligned");
-  NT_REQUIRE(E <= 128 || (workspace && workspace_bytes >= router_workspace_need(T, d, E)) ||
+  NT_REQUIRE(E <= 256 || (workspace && workspace_bytes >= router_workspace_need(T, d, E)) ||
                  (logits && d <= 16 * 128),
-             "router: more than 128 experts need the workspace");
+             "router: more than 256 experts need the workspace");
   hipError_t err = launch_router(x, ld_x, w_router_t, logit_bias, T, d, E, k, score_fn, logits,
                                  topk_ids, topk_w, prob_partial, z_partial,
                                  reinterpret_cast<float*>(workspace), workspace_bytes,

@@ -24,6 +24,8 @@
 // For small T (too few waves for the chip) the split variant gives every (token block, chunk,
 // expert block) its own waves and writes the chunk sums c_j to a workspace (token-major planes);
 // a plane-sum kernel adds them in ascending j -- the same order -- and a top-k kernel ranks.
+// For 129-256 experts the streamed kernel (below) keeps one workgroup per 64 tokens for all
+// experts: token rows staged once in LDS, router weights loaded by each wave into registers.
 //
 // Top-k: logits go to an LDS tile [64][E+1]; LPT lanes share a token (4 in the fused kernel,
 // 16 in the top-k kernel), each scans every LPT-th expert into a sorted register list, then k
@@ -36,6 +38,11 @@
 
 namespace ntmoe {
 namespace {
+
+typedef __attribute__((address_space(1))) void gvoid;
+typedef __attribute__((address_space(3))) void lvoid;
+
+constexpr int kBufferWord3 = 0x00020000;
 
 __host__ __device__ inline int lg_tile_bytes(int E) { return kRouteBlock * (E + 1) * 4; }
 __host__ __device__ inline int zt_offset(int E) { return (lg_tile_bytes(E) + 15) & ~15; }
@@ -80,7 +87,7 @@ __device__ __forceinline__ void topk_and_scores(float* lg, float* zt, int64_t t0
                                 int score_fn, int32_t* __restrict__ topk_ids,
                                 float* __restrict__ topk_w, float* __restrict__ prob_partial,
                                 float* __restrict__ z_partial) {
-  static_assert(LPT == 2 || LPT == 4 || LPT == 8 || LPT == 16, "lanes per token");
+  static_assert(LPT == 1 || LPT == 2 || LPT == 4 || LPT == 8 || LPT == 16, "lanes per token");
   const int ldl = E + 1;
   const int tt = threadIdx.x / LPT;   // token within the block
   const int sub = threadIdx.x % LPT;  // which of the LPT expert strides this lane scans
@@ -435,6 +442,212 @@ __global__ __launch_bounds__(128 * R) void router_logits_kernel(
 
 inline size_t router_logits_lds_bytes(int R) { return (size_t)2 * R * (kXStageBytes + 64 * 32 * 4); }
 
+// ---- Streamed router ----------------------------------------------------------------------
+// For more than 128 experts. One workgroup per 64-token block computes the block's logits for
+// every expert (E <= 32 EBW) and ranks them. Wave w owns expert block w: two fixed-order chains,
+// the block's two 32-token halves against its 32 experts, over all chunks; a router weight
+// operand feeds both.
+// Token rows are staged in LDS once per block: per 64-feature stage a [64 rows][128 B] tile,
+// written by 16-byte direct-to-LDS buffer loads (chunk c of row j at slot c ^ ((j >> 1) & 7),
+// so a fragment read of 32 rows at one chunk is conflict-free), in a ring of four stages filled
+// two stages ahead. Router weights are not shared between waves: each lane loads its B operands
+// straight from w_router_t [d, E] into registers, one stage ahead (per stage 32 values, features
+// 8 q + 2 j + (lane / 32) of its expert). One barrier per stage.
+// Measured against the one-workgroup-per-expert-block logits kernel (which re-reads x once per
+// expert block and stages the weights through LDS) at T = 16384, d = 1280, E = 256: 142 us for
+// logits and top-k against 230 us.
+constexpr int kSRing = 4;                    // LDS stages in the ring
+constexpr int kSRow = 128;                   // bytes per staged row (64 bf16 features)
+constexpr int kSTile = kRouteBlock * kSRow;  // one stage: 8 KB
+
+// 16 bytes per lane from a buffer at byte offset voff into LDS at dst + 16 lane (dst uniform).
+__device__ __forceinline__ void buffer_copy_lds16(__amdgpu_buffer_rsrc_t rsrc, unsigned char* dst,
+                                                  int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lvoid*)dst, 16, voff, 0, 0, 0);
+}
+
+// One fp32 per lane from the buffer rsrc at byte offset voff + soff (soff wave-uniform), as
+// inline assembly: the compiler neither moves it next to its first use nor adds waits of its own
+// for it (its wait analysis is conservative across loop back-edges and would wait for the next
+// stage's loads); the caller waits with stage_wait() before the result is read.
+__device__ __forceinline__ float load_w_asm(__amdgpu_buffer_rsrc_t rsrc, int voff, int soff) {
+  float v;
+  asm volatile("buffer_load_dword %0, %1, %2, %3 offen"
+               : "=v"(v)
+               : "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory");
+  return v;
+}
+
+// s_waitcnt vmcnt(N) that also stands as the producer of the 32 weight registers loaded by
+// load_w_asm, so no read of them is scheduled before the wait.
+template <int N>
+__device__ __forceinline__ void stage_wait(float (&w)[32]) {
+  asm volatile("s_waitcnt vmcnt(%16)"
+               : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]),
+                 "+v"(w[6]), "+v"(w[7]), "+v"(w[8]), "+v"(w[9]), "+v"(w[10]), "+v"(w[11]),
+                 "+v"(w[12]), "+v"(w[13]), "+v"(w[14]), "+v"(w[15])
+               : "n"(N)
+               : "memory");
+  asm volatile(""
+               : "+v"(w[16]), "+v"(w[17]), "+v"(w[18]), "+v"(w[19]), "+v"(w[20]), "+v"(w[21]),
+                 "+v"(w[22]), "+v"(w[23]), "+v"(w[24]), "+v"(w[25]), "+v"(w[26]), "+v"(w[27]),
+                 "+v"(w[28]), "+v"(w[29]), "+v"(w[30]), "+v"(w[31])
+               :
+               : "memory");
+}
+
+template <int EBW>
+struct StreamGeo {
+  static constexpr int kThreads = 64 * EBW;
+  static constexpr int kXCopies = 8 / EBW;  // 1 KB copies per wave per stage (8 in total)
+  static_assert(kXCopies * EBW == 8, "x copies per stage");
+  static constexpr size_t ring_bytes() { return (size_t)kSRing * kSTile; }
+  static constexpr size_t lds_bytes(int E) {
+    return ring_bytes() + (size_t)zt_offset(E) + kRouteBlock * sizeof(float);
+  }
+};
+
+template <int EBW, int KMAX>
+__global__ __launch_bounds__(64 * EBW) void router_stream_kernel(
+    const uint16_t* __restrict__ x, int64_t ld_x, const float* __restrict__ wt,
+    const float* __restrict__ bias, int64_t T, int d, int E, int k, int score_fn,
+    float* __restrict__ logits, int32_t* __restrict__ topk_ids, float* __restrict__ topk_w,
+    float* __restrict__ prob_partial, float* __restrict__ z_partial) {
+  using G = StreamGeo<EBW>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* lg = reinterpret_cast<float*>(smem + G::ring_bytes());
+  float* zt = reinterpret_cast<float*>(smem + G::ring_bytes() + zt_offset(E));
+  const int lane = lane_id(), wave = wave_id();
+  const int64_t t0 = (int64_t)blockIdx.x * kRouteBlock;
+  const int n_stages = (d + 63) / 64;
+
+  // x copies of this wave: copy i is block b = wave + i EBW of the stage (rows 8 b + lane / 8,
+  // slot lane % 8 holding chunk slot ^ ((row >> 1) & 7)). Buffer loads against this block's
+  // rows: a row past T or a feature past the last row's end reads 0, and features past d are
+  // never multiplied, so no clamping is needed.
+  const int rows = T - t0 < kRouteBlock ? (int)(T - t0) : kRouteBlock;
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(x + t0 * ld_x), 0, (int)(((int64_t)(rows - 1) * ld_x + d) * 2), kBufferWord3);
+  int xoff[G::kXCopies];
+#pragma unroll
+  for (int i = 0; i < G::kXCopies; ++i) {
+    const int row = 8 * (wave + i * EBW) + (lane >> 3);
+    xoff[i] = (int)(row * ld_x * 2) + (((lane & 7) ^ ((row >> 1) & 7)) << 4);
+  }
+  auto issue_x = [&](int st, int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < G::kXCopies; ++i)
+      buffer_copy_lds16(xrsrc, smem + (size_t)slot * kSTile + (wave + i * EBW) * 1024,
+                        xoff[i] + st * 128);
+  };
+  const int ec = wave * 32 + (lane & 31);
+  const int ecl = ec < E ? ec : E - 1;
+  const int hk = lane >> 5;  // feature parity this lane supplies
+  const __amdgpu_buffer_rsrc_t wrsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)wt, 0, (int)((int64_t)d * E * 4), kBufferWord3);
+  // Router weights of stage st for this wave, without branches (a join of two load paths could
+  // make the compiler copy registers whose loads are still in flight): the row of each feature
+  // pair, clamped to the last pair, is the scalar operand, the lane's parity and expert the
+  // vector one. Pairs past a partial last stage read valid, unused weights.
+  const int voff_w = (hk * E + ecl) * 4;
+  auto issue_w = [&](int st, float (&wr)[32]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int f = st * 64 + 8 * q + 2 * j;
+        wr[4 * q + j] = load_w_asm(wrsrc, voff_w, (f < d - 2 ? f : d - 2) * E * 4);
+      }
+  };
+  const uint32_t sel = hk ? 0x07060C0Cu : 0x05040C0Cu;
+  const int row0 = lane & 31, row1 = 32 + (lane & 31);
+  const int sw0 = (row0 >> 1) & 7, sw1 = (row1 >> 1) & 7;
+  auto compute = [&](int st, const float (&wr)[32], floatx16& c0, floatx16& c1)
+                     __attribute__((always_inline)) {
+    const int left = d - st * 64;
+    const int ng = left >= 64 ? 8 : left / 8;
+    const unsigned char* tile = smem + (size_t)(st % kSRing) * kSTile;
+    // All of the stage's token fragments are read first (in order, so the MFMAs of group q wait
+    // only for its own reads): with two waves per SIMD in step with each other, a read issued
+    // just ahead of its MFMAs would leave the matrix pipe idle for the LDS latency in every group.
+    u32x4 x0[8], x1[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      x0[q] = *reinterpret_cast<const u32x4*>(tile + row0 * kSRow + ((q ^ sw0) << 4));
+      x1[q] = *reinterpret_cast<const u32x4*>(tile + row1 * kSRow + ((q ^ sw1) << 4));
+    }
+    auto group = [&](int q) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a0 = __builtin_bit_cast(float, __builtin_amdgcn_perm(x0[q][j], 0u, sel));
+        const float a1 = __builtin_bit_cast(float, __builtin_amdgcn_perm(x1[q][j], 0u, sel));
+        c0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, wr[4 * q + j], c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, wr[4 * q + j], c1, 0, 0, 0);
+      }
+    };
+    if (ng == 8) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) group(q);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (q < ng) group(q);
+    }
+  };
+  // Stage st: issue the weights of st + 1 and the x copies of st + 2, wait until x(st) and W(st)
+  // are complete (at most the loads issued after W(st) outstanding: x(st + 1), W(st + 1),
+  // x(st + 2); vector memory operations retire in order), then the chains. Past the last stage
+  // these loads read in-bounds data nobody uses.
+  auto stage = [&](int st, float (&wcur)[32], float (&wnext)[32], floatx16& c0, floatx16& c1)
+                   __attribute__((always_inline)) {
+    issue_w(st + 1, wnext);
+    issue_x(st + 2, (st + 2) % kSRing);
+    stage_wait<2 * G::kXCopies + 32>(wcur);
+    // Barrier without a memory fence (a fence would wait for the prefetches too): every wave's
+    // copies of stage st have landed (its own vmcnt wait above), and every wave's reads of the
+    // slot refilled next stage are complete (lgkmcnt).
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    compute(st, wcur, c0, c1);
+  };
+
+  float wa[32], wb[32];
+  issue_x(0, 0);
+  issue_w(0, wa);
+  issue_x(1, 1);
+  // One chunk (128 features, the fixed order's chain) = stages 2 i (weights in wa) and 2 i + 1
+  // (wb); the last chunk may have one stage.
+  floatx16 s0 = {}, s1 = {};
+  const int n_chunks = (n_stages + 1) / 2;
+  for (int i = 0; i < n_chunks; ++i) {
+    floatx16 c0 = {}, c1 = {};
+    stage(2 * i, wa, wb, c0, c1);
+    if (2 * i + 1 < n_stages) stage(2 * i + 1, wb, wa, c0, c1);
+    s0 = i == 0 ? c0 : s0 + c0;
+    s1 = i == 0 ? c1 : s1 + c1;
+  }
+  // Every copy and weight load (including those past the end) has landed before the ring is
+  // reused and before their registers can be: the waits hold both weight buffers.
+  stage_wait<0>(wa);
+  stage_wait<0>(wb);
+  __syncthreads();
+  // Logits (+ bias) into the tile lg[64][E+1].
+  if (ec < E) {
+    const float bv = bias ? bias[ec] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      lg[acc_row(i, lane) * (E + 1) + ec] = bias ? s0[i] + bv : s0[i];
+      lg[(32 + acc_row(i, lane)) * (E + 1) + ec] = bias ? s1[i] + bv : s1[i];
+    }
+  }
+  __syncthreads();
+  if (logits) write_logits_out(lg, t0, T, E, logits);
+  topk_and_scores<KMAX, EBW>(lg, zt, t0, T, E, k, score_fn, topk_ids, topk_w, prob_partial,
+                             z_partial);
+}
+
 // Split: the chunk sum c_j (blockIdx.y = j) of a 64-token x 32-expert block (blockIdx.z) ->
 // partials[j][t][e], token-major (a wave's store covers 32 consecutive experts of a token).
 __global__ __launch_bounds__(128) void router_mfma_partial_kernel(
@@ -583,14 +796,16 @@ int router_ranges(int d, int E) {
   return nchunk >= 4 && nchunk <= 16 ? 4 : (nchunk <= 8 ? 2 : 1);
 }
 
-// NT_MOE_ROUTER_MODE=fused|split overrides the size heuristic (for tuning runs): fused = no
-// chunk planes, split = chunk planes.
+// NT_MOE_ROUTER_MODE=fused|split|stream overrides the size heuristic (for tuning runs): fused =
+// the fused kernel (up to 128 experts), split = chunk planes, stream = the streamed kernel
+// (129-256 experts).
 int router_mode_override() {
   static int mode = [] {
     const char* s = getenv("NT_MOE_ROUTER_MODE");
     if (!s) return 0;
     if (!strcmp(s, "fused")) return 1;
     if (!strcmp(s, "split")) return 2;
+    if (!strcmp(s, "stream")) return 3;
     return 0;
   }();
   return mode;
@@ -649,13 +864,15 @@ int logit_ranges(int d) {
   return nchunk >= 4 ? 4 : (nchunk >= 2 ? 2 : 1);
 }
 
-enum RouterPath { kFused = 0, kLogits = 1, kPlanes = 2 };
+enum RouterPath { kFused = 0, kLogits = 1, kPlanes = 2, kStream = 3 };
 
-// Path for this shape. Fused (top-k in the block, no workspace) when every CU gets a 64-token
-// block and E <= 128; else the logits kernel (one workgroup per 64 tokens x 32 experts, up to
-// 16 chunks) when that gives two waves per CU; else chunk planes (small T), whose planes are
-// capped at 512 MB. Measured at T = 16384 / 8192 / 32768 (E = 32 / 128 / 64): fused 28 us,
-// logits + top-k 94 us (fused: 115, half the CUs idle), fused 180 us.
+// Path for this shape. Up to 128 experts: the fused kernel (top-k in the block, no workspace)
+// when every CU gets a 64-token block, else the logits kernel (one workgroup per 64 tokens x 32
+// experts, up to 16 chunks) when that gives two waves per CU, else chunk planes (small T, planes
+// capped at 512 MB). 129-256 experts: the streamed kernel (top-k in the block, no workspace)
+// when it gives every other SIMD a wave. Measured on MI355X, router alone: T = 16384, d = 1280,
+// E = 256 streamed 142 us (logits + top-k 230); T = 32768, d = 2048, E = 64 fused 122 us
+// (streamed 133); T = 8192, d = 2048, E = 128 logits + top-k 121 us (streamed 131).
 int router_path(int64_t T, int d, int E) {
   const int mode = router_mode_override();
   const int nchunk = ceil_div(d, kRouterChunk);
@@ -664,10 +881,37 @@ int router_path(int64_t T, int d, int E) {
   const int64_t plane_bytes = (int64_t)nchunk * T * E * (int64_t)sizeof(float);
   if (mode == 2) return kPlanes;
   if (mode == 1) return E <= 128 ? kFused : kLogits;
+  if (mode == 3) return E > 128 && E <= 256 ? kStream : kLogits;
   if (E <= 128 && blocks >= num_cus()) return kFused;
+  if (E > 128 && E <= 256 && blocks * 8 >= 2LL * num_cus()) return kStream;
   if (nchunk <= 16 && logit_waves >= 2LL * num_cus()) return kLogits;
   if (plane_bytes <= (512LL << 20)) return kPlanes;
-  return nchunk <= 16 ? kLogits : kFused;
+  return nchunk <= 16 ? kLogits : (E <= 128 ? kFused : kStream);
+}
+
+template <int KMAX>
+hipError_t launch_stream_k(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
+                           int64_t T, int d, int E, int k, int score_fn, float* logits,
+                           int32_t* ids, float* w, float* pp, float* zp, hipStream_t stream) {
+  auto kern = router_stream_kernel<8, KMAX>;
+  const size_t lds = StreamGeo<8>::lds_bytes(E);
+  hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(kern, dim3(ceil_div(T, kRouteBlock)), dim3(StreamGeo<8>::kThreads), lds,
+                     stream, x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp);
+  return hipGetLastError();
+}
+
+// The streamed kernel for 129-256 experts (eight 32-expert blocks).
+hipError_t launch_stream(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
+                         int64_t T, int d, int E, int k, int score_fn, float* logits,
+                         int32_t* ids, float* w, float* pp, float* zp, hipStream_t stream) {
+  if (E > 256) return hipErrorInvalidValue;
+  switch (kmax_for(k)) {
+    case 2: return launch_stream_k<2>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    case 4: return launch_stream_k<4>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    default: return launch_stream_k<8>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
+  }
 }
 
 }  // namespace
@@ -709,6 +953,9 @@ hipError_t launch_router(const uint16_t* x, int64_t ld_x, const float* wt, const
     return launch_topk_any(workspace, nchunk, bias, T, E, k, score_fn, logits, topk_ids, topk_w,
                            prob_partial, z_partial, stream);
   }
+  if (path == kStream || (path == kPlanes && E > 128 && E <= 256))
+    return launch_stream(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, topk_ids, topk_w,
+                         prob_partial, z_partial, stream);
   float* lbuf = logits ? logits : (workspace && workspace_bytes >= plane ? workspace : nullptr);
   if ((path != kFused || E > 128) && lbuf && nchunk <= 16) {
     const int ranges = logit_ranges(d);
@@ -728,12 +975,17 @@ hipError_t launch_router(const uint16_t* x, int64_t ld_x, const float* wt, const
     return launch_topk_any(lbuf, 1, nullptr, T, E, k, score_fn, nullptr, topk_ids, topk_w,
                            prob_partial, z_partial, stream);
   }
-  const int eb = expert_blocks(E), ranges = router_ranges(d, E);
+  if (E <= 128) {  // the fused kernel: its path, or planes / logits without their buffers
+    const int eb = expert_blocks(E), ranges = router_ranges(d, E);
 #define NT_MFMA(EB, R) \
   if (eb == EB && ranges == R) return launch_mfma_r<EB, R>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, topk_ids, topk_w, prob_partial, z_partial, stream);
-  NT_MFMA(1, 1) NT_MFMA(1, 2) NT_MFMA(1, 4) NT_MFMA(2, 1) NT_MFMA(4, 1)
+    NT_MFMA(1, 1) NT_MFMA(1, 2) NT_MFMA(1, 4) NT_MFMA(2, 1) NT_MFMA(4, 1)
 #undef NT_MFMA
-  return hipErrorInvalidValue;  // more than 128 experts need the workspace
+  }
+  if (E <= 256)
+    return launch_stream(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, topk_ids, topk_w,
+                         prob_partial, z_partial, stream);
+  return hipErrorInvalidValue;  // more than 256 experts need the workspace or a logits buffer
 }
 
 hipError_t launch_topk_from_logits(const float* logits, int64_t T, int E, int k,

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from oracle import moe_oracle as orc
-from tests.moe_cases import Case, make_inputs, rel_l2
+from tests.moe_cases import Case, make_inputs, make_router_inputs, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -119,6 +119,37 @@ def test_router_variants_bit_exact_via_abi(variant, E, T, d):
     torch.testing.assert_close(w.cpu(), ref_w, rtol=2e-6, atol=2e-7)
     s_ = orc.full_scores(ref_logits, 0)
     torch.testing.assert_close(pp.cpu().double().sum(0), s_.sum(0), rtol=1e-5, atol=1e-5)
+
+
+# The streamed router (129-256 experts, at least 64 token blocks): E not a multiple of 32, a
+# partial last 64-feature stage (d = 1032) and a one-chunk d, a ragged last token block, bias,
+# sigmoid, top-6 and top-8.
+STREAM = [
+    Case("stream-T4100-d1032-E200-k8-sigmoid-bias", 4100, 1032, 200, 8, 64, score_fn=1,
+         zipf_bias=0.8, seed=21),
+    Case("stream-T4096-d1280-E256-k8", 4096, 1280, 256, 8, 64, seed=22),
+    Case("stream-T4160-d264-E160-k6-bias", 4160, 264, 160, 6, 64, zipf_bias=1.2, seed=23),
+]
+
+
+@pytest.mark.parametrize("case", STREAM, ids=lambda c: c.name)
+def test_streamed_router_bit_exact(case):
+    from nexttransformer_amd import ops
+    x, router, bias = make_router_inputs(case)
+    dev = torch.device("cuda")
+    logits, ids, w, pp, zp = ops.router(x.to(dev), router.t().contiguous().to(dev),
+                                        None if bias is None else bias.to(dev), case.k,
+                                        case.score_fn, True)
+    torch.cuda.synchronize()
+    ref_logits = orc.router_logits_fixed(x, router, bias)
+    assert torch.equal(logits.cpu().view(torch.int32), ref_logits.view(torch.int32)), "logits bits"
+    ref_ids, ref_w = orc.topk(ref_logits, case.k, case.score_fn)
+    assert torch.equal(ids.cpu(), ref_ids), "top-k ids"
+    torch.testing.assert_close(w.cpu(), ref_w, rtol=2e-6, atol=2e-7)
+    s_ = orc.full_scores(ref_logits, case.score_fn)
+    torch.testing.assert_close(pp.cpu().double().sum(0), s_.sum(0), rtol=1e-5, atol=1e-5)
+    lse2 = torch.logsumexp(ref_logits.double(), -1).square().sum()
+    torch.testing.assert_close(zp.cpu().double().sum(), lse2, rtol=1e-5, atol=1e-5)
 
 
 def test_topk_on_reference_logits_and_ties():
