@@ -87,7 +87,8 @@ const char* nt_moe_last_error(void);
  *                full score s_te (softmax over all E, or sigmoid normalised over all E)
  *   z_partial   fp32 [ceil(T/64)]: per block, sum of logsumexp(logits_t)^2
  *   workspace   nt_moe_router_workspace_bytes(T, d, E, k) bytes; may be smaller (or NULL)
- *               for E <= 128, which then takes a slower single-kernel path
+ *               for E <= 256, which then takes a single-kernel path (slower for small T);
+ *               E > 256 needs it (or logits, with d <= 2048)
  */
 size_t nt_moe_router_workspace_bytes(int64_t T, int32_t d, int32_t E, int32_t k);
 int nt_moe_router_fwd(const uint16_t* x, int64_t ld_x, const float* w_router_t,
