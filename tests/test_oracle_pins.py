@@ -421,14 +421,15 @@ def test_moe_forward_tokens_equals_moe_forward_rows(activation, score_fn, shared
 # ---------------------------------------------------------------------------------------------
 # routing on the fixed-order logits equals routing on the reference's own router expression
 
-@pytest.mark.parametrize("config", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("config", [1, 2, 3, 4, 5, 6])
 def test_fixed_order_routing_equals_reference_router_at_benchmark_configs(config):
     """On the seeded inputs of every benchmark configuration, top-k of the fixed-order logits
     (which the HIP router reproduces bit for bit) selects the same experts in the same order as
     top-k of the reference's F.linear(x.float(), W.float()) (+ the logit bias)
     (megatron_moe.py:95-99, reference_blocks.py:37-38), although most logits differ in their
-    low bits. The weights then differ only by that rounding. The smallest k-th / (k+1)-th logit
-    margin is reported beside the largest logit difference of the two orders."""
+    low bits. The weights then differ only by that rounding. Reported: the smallest k-th /
+    (k+1)-th logit margin, the largest logit difference of the two orders and the number of
+    near-tie tokens whose margin is within twice their own difference."""
     from tests.moe_cases import CONFIGS, make_router_inputs
     case = CONFIGS[config]
     x, router, bias = make_router_inputs(case)
@@ -439,11 +440,16 @@ def test_fixed_order_routing_equals_reference_router_at_benchmark_configs(config
     ids_r, w_r = orc.topk(ref, case.k, case.score_fn)
     assert torch.equal(ids_f, ids_r)
     torch.testing.assert_close(w_f, w_r, rtol=1e-5, atol=1e-7)
+    # Per token: the selection can only flip where the gap between the k-th and (k+1)-th logit
+    # is within twice that token's largest difference between the two orders; those tokens
+    # (near ties) are counted -- they select identically here too (asserted above).
     top = ref.double().sort(-1, descending=True).values
-    margin = (top[:, case.k - 1] - top[:, case.k]).min().item()
-    diff = (fixed.double() - ref.double()).abs().max().item()
-    print(f"config {config}: min top-k margin {margin:.3e}, max |fixed - F.linear| {diff:.3e}")
-    assert margin > diff
+    margin_t = top[:, case.k - 1] - top[:, case.k]
+    diff_t = (fixed.double() - ref.double()).abs().max(-1).values
+    near = int((margin_t <= 2 * diff_t).sum())
+    print(f"config {config}: min top-k margin {margin_t.min().item():.3e}, max |fixed - F.linear| "
+          f"{diff_t.max().item():.3e}, near-tie tokens {near} of {case.T}")
+    assert near <= case.T // 100  # near ties are rare: the id check is not vacuous
 
 
 @pytest.mark.parametrize("activation,score_fn,shared", [
