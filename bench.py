@@ -146,8 +146,10 @@ def train_bench(args, case, cpu, g):
         w = layer.packed_weights(keep_plain=True)
         bw = layer.backward_weights(w)
         bw.w1t, bw.w2t, bw.shared, bw.first(w["router_t"])
-        if not w["packed"]:  # the fc1 recompute operand: the forward keeps no fc1 then
-            bw.w1
+        w1 = w["w1"]
+        n_out = w1.shape[1] // 2 if case.activation == 0 else w1.shape[1]
+        if not w["packed"] and not ops.plain_keep_supported(w1.shape[2], n_out):
+            bw.w1  # the fc1 recompute operand: the forward keeps no fc1 then
 
     for _ in range(max(1, args.warmup)):
         step()
@@ -189,6 +191,7 @@ def train_bench(args, case, cpu, g):
                                    shared_w2=w["shared_w2"], packed=w["packed"],
                                    want_logits=True, keep=True, mark=lambda n: mark("fwd_" + n))
         kept = st["fc1"] is not None
+        kept_shared = st["shared_fc1"] is not None
         ops.moe_backward(G, torch.tensor([1.0, 0.0, 0.0], device="cuda"), x, w["router_t"], bw,
                          st, top_k=case.k, score_fn=case.score_fn, activation=case.activation,
                          mark=lambda n: mark("bwd_" + n))
@@ -204,7 +207,8 @@ def train_bench(args, case, cpu, g):
     # forward: up + down; backward: dgrad and wgrad of both (+ the fc1 recompute when the forward
     # kept no pre-activations); the shared expert likewise; the router GEMM once forward and its
     # two gradient products
-    flops = ((3 if kept else 4) * up + 3 * down + 4 * sup + 3 * sdown + 3 * router)
+    flops = ((3 if kept else 4) * up + 3 * down + (3 if kept_shared else 4) * sup + 3 * sdown
+             + 3 * router)
     wg_ms = stage.get("bwd_wgrad", 0.0)
     wg_flop = up + down + sup + sdown
     wg_tflops = wg_flop / (wg_ms * 1e-3) / 1e12 if wg_ms > 0 else None

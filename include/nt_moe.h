@@ -212,6 +212,20 @@ int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                              void* workspace, size_t workspace_bytes, nt_moe_stream_t stream);
 
 /*
+ * nt_moe_grouped_gemm_bf16 with the SWIGLU or RELU2 epilogue that also stores the epilogue's
+ * input, the fc1 pre-activations, to pre: bf16 [total_rows, 2 n_out] (SwiGLU: gate then value)
+ * or [total_rows, n_out] (ReLU^2), rounded from the same fp32 accumulators: what autograd saves
+ * from the fc1 product and activation for the backward (megatron_moe.py:23-24,58-78;
+ * lm.py:29-35), read by nt_moe_act_bwd. Needs the 256 x 256 path: K >= 128, n_out % 8 == 0;
+ * 16-byte aligned; total_rows * width * 2 < 2^31. No workspace.
+ */
+int nt_moe_grouped_gemm_bf16_keep(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                  const int32_t* src_row, const int32_t* seg_offsets,
+                                  int32_t num_segments, int64_t total_rows, const uint16_t* w,
+                                  int32_t K, int32_t n_out, int32_t epilogue, uint16_t* c,
+                                  uint16_t* pre, nt_moe_stream_t stream);
+
+/*
  * Weight preparation: the fp32 master weights w [num_matrices, rows, cols] to bf16, in one read:
  * out [num_matrices, rows, cols] (the cast MasterLinear applies before each product,
  * megatron_moe.py:74-75) and out_t [num_matrices, cols, rows] (its transpose, the dgrad

@@ -472,11 +472,10 @@ int nt_moe_grouped_ffn_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows, con
   return launched(err, "grouped_ffn_bf16");
 }
 
-int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
-                             const int32_t* src_row, const int32_t* seg_offsets,
-                             int32_t num_segments, int64_t total_rows, const uint16_t* w,
-                             int32_t K, int32_t n_out, int32_t epilogue, uint16_t* c,
-                             void* workspace, size_t workspace_bytes, nt_moe_stream_t stream) {
+static int check_plain(const uint16_t* a, int64_t ld_a, int64_t a_rows, const int32_t* src_row,
+                       const int32_t* seg_offsets, int32_t num_segments, int64_t total_rows,
+                       const uint16_t* w, int32_t K, int32_t n_out, int32_t epilogue,
+                       uint16_t* c) {
   NT_REQUIRE(K > 0 && K % 64 == 0, "grouped_gemm: K must be a positive multiple of 64, got %d", K);
   NT_REQUIRE(epilogue == NT_MOE_EPI_SWIGLU || epilogue == NT_MOE_EPI_RELU2 ||
                  epilogue == NT_MOE_EPI_NONE, "grouped_gemm: unknown epilogue %d", epilogue);
@@ -496,6 +495,17 @@ int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
   if (rc) return rc;
   NT_REQUIRE(total_rows * n_out * 2 < ((int64_t)1 << 31),
              "grouped_gemm: the output must stay below 2 GiB");
+  return 0;
+}
+
+int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                             const int32_t* src_row, const int32_t* seg_offsets,
+                             int32_t num_segments, int64_t total_rows, const uint16_t* w,
+                             int32_t K, int32_t n_out, int32_t epilogue, uint16_t* c,
+                             void* workspace, size_t workspace_bytes, nt_moe_stream_t stream) {
+  int rc = check_plain(a, ld_a, a_rows, src_row, seg_offsets, num_segments, total_rows, w, K,
+                       n_out, epilogue, c);
+  if (rc) return rc;
   if (!workspace || workspace_bytes < kGemmWorkspaceBytes)
     return fail(NT_MOE_ENOSPC, "grouped_gemm: workspace %zu < %zu bytes", workspace_bytes,
                 kGemmWorkspaceBytes);
@@ -512,6 +522,31 @@ int nt_moe_grouped_gemm_bf16(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                                      reinterpret_cast<int*>(workspace),
                                      reinterpret_cast<hipStream_t>(stream));
   return launched(err, "grouped_gemm_bf16");
+}
+
+int nt_moe_grouped_gemm_bf16_keep(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                  const int32_t* src_row, const int32_t* seg_offsets,
+                                  int32_t num_segments, int64_t total_rows, const uint16_t* w,
+                                  int32_t K, int32_t n_out, int32_t epilogue, uint16_t* c,
+                                  uint16_t* pre, nt_moe_stream_t stream) {
+  NT_REQUIRE(epilogue == NT_MOE_EPI_SWIGLU || epilogue == NT_MOE_EPI_RELU2,
+             "grouped_gemm_keep: the epilogue must be SWIGLU or RELU2, got %d", epilogue);
+  int rc = check_plain(a, ld_a, a_rows, src_row, seg_offsets, num_segments, total_rows, w, K,
+                       n_out, epilogue, c);
+  if (rc) return rc;
+  NT_REQUIRE(K >= 128 && n_out % 8 == 0,
+             "grouped_gemm_keep: K must be >= 128 and n_out a multiple of 8, got K %d n_out %d",
+             K, n_out);
+  const int64_t pw = epilogue == NT_MOE_EPI_SWIGLU ? 2 * (int64_t)n_out : n_out;
+  NT_REQUIRE(total_rows * pw * 2 < ((int64_t)1 << 31),
+             "grouped_gemm_keep: the pre-activations must stay below 2 GiB");
+  NT_REQUIRE(pre && aligned16(pre), "grouped_gemm_keep: pre must be a 16-byte aligned buffer");
+  if (total_rows == 0) return ok();
+  return launched(launch_grouped_gemm_bf16_t256_keep(a, ld_a, a_rows, src_row, seg_offsets,
+                                                     num_segments, total_rows, w, K, n_out,
+                                                     epilogue, c, pre,
+                                                     reinterpret_cast<hipStream_t>(stream)),
+                  "grouped_gemm_keep");
 }
 
 int nt_moe_convert_expert_weights(const float* w, int64_t num_matrices, int32_t rows,

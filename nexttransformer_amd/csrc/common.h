@@ -141,6 +141,12 @@ hipError_t launch_grouped_gemm_bf16_t256(const uint16_t* a, int64_t ld_a, int64_
                                          int num_segments, int64_t total_rows, const uint16_t* w,
                                          int K, int n_out, int epilogue, uint16_t* c,
                                          hipStream_t stream);
+// The same with the SWIGLU / RELU2 epilogue storing the fc1 pre-activations to pre as well.
+hipError_t launch_grouped_gemm_bf16_t256_keep(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                              const int32_t* src_row, const int32_t* seg_offsets,
+                                              int num_segments, int64_t total_rows,
+                                              const uint16_t* w, int K, int n_out, int epilogue,
+                                              uint16_t* c, uint16_t* pre, hipStream_t stream);
 
 int num_cus();
 

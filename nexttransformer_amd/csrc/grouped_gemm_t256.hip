@@ -77,12 +77,15 @@ __device__ __forceinline__ int weight_row(int nt, int p_tile, int n_out, int R) 
   return row < R ? row : R - 1;
 }
 
-template <int EPI, bool GATHER>
+// KEEP: also store the epilogue's input, the fc1 pre-activations, to Pre: bf16 [rows, R]
+// (SwiGLU: gate columns then value columns; ReLU^2: the output's columns), rounded from the same
+// fp32 accumulators, for the backward.
+template <int EPI, bool GATHER, bool KEEP = false>
 __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
     const uint16_t* __restrict__ A, int64_t ld_a, int64_t a_rows,
     const int32_t* __restrict__ src_row, const int32_t* __restrict__ seg_offsets, int S,
     int total_rows, const uint16_t* __restrict__ W, int K, int n_out,
-    uint16_t* __restrict__ Cout) {
+    uint16_t* __restrict__ Cout, uint16_t* __restrict__ Pre) {
   extern __shared__ __align__(16) unsigned char smem[];
   int* tile_prefix = reinterpret_cast<int*>(smem + kStages * kStageBytes);  // [S+1]
   int* seg_lo = tile_prefix + (S + 1);                                      // [S+1]
@@ -212,6 +215,8 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
 
   const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       Cout, 0, (int)((int64_t)total_rows * n_out * 2), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t pre_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      KEEP ? Pre : Cout, 0, KEEP ? (int)((int64_t)total_rows * R * 2) : 0, kBufferWord3);
 
   // Fragment reads of slice q of stage `slot`: the wave's 4 weight blocks and 4 token blocks
   // (all 4 even in a partial tile: reading rows nobody copied is harmless, their products are
@@ -352,10 +357,26 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
             }
             const u32x4 packed = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
                                   pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
-            const uint32_t voff = (row_ok && nb < NB && col < n_out)
-                                      ? (uint32_t)(((int64_t)m * n_out + col) * 2)
-                                      : 0x80000000u;
+            const bool ok = row_ok && nb < NB && col < n_out;
+            const uint32_t voff = ok ? (uint32_t)(((int64_t)m * n_out + col) * 2) : 0x80000000u;
             __builtin_amdgcn_raw_buffer_store_b128(packed, out_rsrc, voff, 0, 0);
+            if constexpr (KEEP) {
+              // the accumulators behind these columns: SwiGLU gate (elements 0-7) at col and
+              // value (8-15) at n_out + col of a [rows, 2 n_out] row; otherwise elements
+              // 8 st .. 8 st + 7 at col of a [rows, n_out] row
+              const int e0 = EPI == NT_MOE_EPI_SWIGLU ? 0 : 8 * st;
+#pragma unroll
+              for (int part = 0; part < (EPI == NT_MOE_EPI_SWIGLU ? 2 : 1); ++part) {
+                const int eb = e0 + 8 * part;
+                const floatx16& av = acc[b][j];
+                const u32x4 pk = {pack_bf16x2(av[eb], av[eb + 1]), pack_bf16x2(av[eb + 2], av[eb + 3]),
+                                  pack_bf16x2(av[eb + 4], av[eb + 5]),
+                                  pack_bf16x2(av[eb + 6], av[eb + 7])};
+                const uint32_t poff =
+                    ok ? (uint32_t)(((int64_t)m * R + col + part * n_out) * 2) : 0x80000000u;
+                __builtin_amdgcn_raw_buffer_store_b128(pk, pre_rsrc, poff, 0, 0);
+              }
+            }
           }
         }
       }
@@ -373,10 +394,11 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-template <int EPI, bool GATHER>
+template <int EPI, bool GATHER, bool KEEP = false>
 hipError_t launch_t256(const uint16_t* a, int64_t ld_a, int64_t a_rows, const int32_t* src_row,
                        const int32_t* seg_offsets, int S, int64_t total_rows, const uint16_t* w,
-                       int K, int n_out, uint16_t* c, hipStream_t stream) {
+                       int K, int n_out, uint16_t* c, hipStream_t stream,
+                       uint16_t* pre = nullptr) {
   const int R = EPI == NT_MOE_EPI_SWIGLU ? 2 * n_out : n_out;
   const int64_t n_tiles = ((R + 31) / 32 + kBlocksPerTile - 1) / kBlocksPerTile;
   const int64_t upper = ((total_rows + kTM - 1) / kTM + S) * n_tiles;
@@ -384,11 +406,11 @@ hipError_t launch_t256(const uint16_t* a, int64_t ld_a, int64_t a_rows, const in
   if (upper < grid) grid = upper;
   grid = ((grid + 7) / 8) * 8;
   const size_t lds = (size_t)kStages * kStageBytes + (size_t)(2 * S + 2) * sizeof(int);
-  auto kern = grouped_gemm_t256_kernel<EPI, GATHER>;
+  auto kern = grouped_gemm_t256_kernel<EPI, GATHER, KEEP>;
   hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), lds, stream, a, ld_a, a_rows,
-                     src_row, seg_offsets, S, (int)total_rows, w, K, n_out, c);
+                     src_row, seg_offsets, S, (int)total_rows, w, K, n_out, c, pre);
   return hipGetLastError();
 }
 
@@ -411,6 +433,26 @@ hipError_t launch_grouped_gemm_bf16_t256(const uint16_t* a, int64_t ld_a, int64_
     default: NT_T(NT_MOE_EPI_NONE);
   }
 #undef NT_T
+}
+
+hipError_t launch_grouped_gemm_bf16_t256_keep(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                              const int32_t* src_row, const int32_t* seg_offsets,
+                                              int num_segments, int64_t total_rows,
+                                              const uint16_t* w, int K, int n_out, int epilogue,
+                                              uint16_t* c, uint16_t* pre, hipStream_t stream) {
+  if (total_rows == 0) return hipSuccess;
+#define NT_TK(EPI)                                                                            \
+  return src_row ? launch_t256<EPI, true, true>(a, ld_a, a_rows, src_row, seg_offsets,        \
+                                                num_segments, total_rows, w, K, n_out, c,     \
+                                                stream, pre)                                  \
+                 : launch_t256<EPI, false, true>(a, ld_a, a_rows, src_row, seg_offsets,       \
+                                                 num_segments, total_rows, w, K, n_out, c,    \
+                                                 stream, pre)
+  switch (epilogue) {
+    case NT_MOE_EPI_SWIGLU: NT_TK(NT_MOE_EPI_SWIGLU);
+    default: NT_TK(NT_MOE_EPI_RELU2);
+  }
+#undef NT_TK
 }
 
 }  // namespace ntmoe

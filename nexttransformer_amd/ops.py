@@ -234,6 +234,48 @@ def _(a, src_row, seg_offsets, w, epilogue, total_rows):
     return a.new_empty((total_rows, rows // 2 if epilogue == nat.EPI_SWIGLU else rows))
 
 
+def plain_keep_supported(K, n_out):
+    """Whether the plain-weight up projection can keep its fc1 pre-activations (the 256 x 256
+    kernel: K >= 128, n_out a multiple of 8)."""
+    return K >= 128 and n_out % 8 == 0
+
+
+@torch.library.custom_op("ntmoe::grouped_gemm_keep", mutates_args=())
+def grouped_gemm_keep(a: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor, w: Tensor,
+                      epilogue: int, total_rows: int) -> tuple[Tensor, Tensor]:
+    """(c, pre): grouped_gemm with the SwiGLU / ReLU^2 epilogue, plus the epilogue's input (the
+    fc1 pre-activations, [rows, 2 n_out] or [rows, n_out]) for the backward."""
+    _on_gpu(a, src_row, seg_offsets, w)
+    _require(epilogue in (nat.EPI_SWIGLU, nat.EPI_RELU2),
+             "grouped_gemm_keep: the epilogue must be SWIGLU or RELU2")
+    _require(a.dtype == torch.bfloat16 and a.dim() == 2 and a.stride(1) == 1,
+             "grouped_gemm_keep: a must be bf16 [*, K] with contiguous rows")
+    _require(w.dtype == torch.bfloat16 and w.dim() == 3 and w.is_contiguous(),
+             "grouped_gemm_keep: w must be contiguous bf16 [S, rows, K]")
+    S, rows, K = w.shape
+    n_out = rows // 2 if epilogue == nat.EPI_SWIGLU else rows
+    _require(a.shape[1] == K, "grouped_gemm_keep: a and w disagree on K")
+    _require(seg_offsets.dtype == torch.int32 and seg_offsets.shape == (S + 1,)
+             and seg_offsets.is_contiguous(), "grouped_gemm_keep: seg_offsets must be int32 [S+1]")
+    if src_row is not None:
+        _require(src_row.dtype == torch.int32 and src_row.is_contiguous(),
+                 "grouped_gemm_keep: src_row must be contiguous int32")
+    c = torch.empty(total_rows, n_out, device=a.device, dtype=torch.bfloat16)
+    pre = torch.empty(total_rows, rows, device=a.device, dtype=torch.bfloat16)
+    st = nat.load().nt_moe_grouped_gemm_bf16_keep(
+        ptr(a), a.stride(0), a.shape[0], ptr(src_row), ptr(seg_offsets), S, total_rows, ptr(w), K,
+        n_out, epilogue, ptr(c), ptr(pre), _stream(a.device))
+    nat.check(st, "ntmoe::grouped_gemm_keep")
+    return c, pre
+
+
+@grouped_gemm_keep.register_fake
+def _(a, src_row, seg_offsets, w, epilogue, total_rows):
+    S, rows, K = w.shape
+    n_out = rows // 2 if epilogue == nat.EPI_SWIGLU else rows
+    return (a.new_empty(total_rows, n_out), a.new_empty(total_rows, rows))
+
+
 @torch.library.custom_op("ntmoe::pack_expert_weights", mutates_args=())
 def pack_expert_weights(w: Tensor, epilogue: int) -> Tensor:
     """Expert weights [S, rows, K] bf16 rearranged for grouped_gemm_packed (same size)."""
@@ -534,8 +576,9 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
     h are then quantised per row and both projections run on the fp8 grouped GEMM.
     `mark(name)`, when given, is called after each stage is enqueued (used to place timing
     events on the stream). keep (bf16 experts): the state also holds what moe_backward reads
-    (h, y, the shared expert's h, the router's aux partials and, with packed weights, the fc1
-    pre-activations from the up projection's launch).
+    (h, y, the shared expert's h, the router's aux partials and the fc1 pre-activations of
+    the routed and the shared expert from their up projections' launches, with packed weights
+    or plain ones that plain_keep_supported takes; otherwise moe_backward recomputes them).
     """
     T = x.shape[0]
     E = w_router_t.shape[1]
@@ -583,20 +626,28 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
                      x_scale=xs)
         return out, aux, state
     gemm = grouped_gemm_packed if packed else grouped_gemm
-    fc1 = None
+
+    def up(a, rows_src, offs, w, rows):
+        """The up projection; with keep, also the backward's fc1 pre-activations from the same
+        launch where the kernel can store them (else None: the backward recomputes them)."""
+        if keep and packed:
+            return grouped_gemm_packed_keep(a, rows_src, offs, w, up_epi, rows)
+        if keep and plain_keep_supported(
+                w.shape[2], w.shape[1] // 2 if up_epi == nat.EPI_SWIGLU else w.shape[1]):
+            return grouped_gemm_keep(a, rows_src, offs, w, up_epi, rows)
+        return gemm(a, rows_src, offs, w, up_epi, rows), None
+
     if permute_rows:
-        h = gemm(x_perm, None, offsets, w1, up_epi, A)
-    elif packed and keep:  # the backward's fc1 pre-activations from the same launch
-        h, fc1 = grouped_gemm_packed_keep(x, src, offsets, w1, up_epi, A)
+        h, fc1 = gemm(x_perm, None, offsets, w1, up_epi, A), None
     else:
-        h = gemm(x, src, offsets, w1, up_epi, A)
+        h, fc1 = up(x, src, offsets, w1, A)
     mark("gemm_up")
     y = gemm(h, None, offsets, w2, nat.EPI_NONE, A)
     mark("gemm_down")
-    shared_y = hs = None
+    shared_y = hs = fc1s = None
     if shared_w1 is not None:
         seg = _whole_batch_segment(T, x.device)
-        hs = gemm(x, None, seg, shared_w1, up_epi, T)
+        hs, fc1s = up(x, None, seg, shared_w1, T)
         shared_y = gemm(hs, None, seg, shared_w2, nat.EPI_NONE, T)
         mark("shared")
     out, aux = combine_aux(y, cdest, cw, shared_y, pp, zp, counts, aux_coeff, z_coeff)
@@ -604,7 +655,8 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
     state = dict(logits=logits, ids=ids, weights=w, counts=counts, offsets=offsets, src_row=src,
                  perm_w=perm_w, combine_dest=cdest, combine_w=cw)
     if keep:
-        state.update(h=h, y=y, shared_h=hs, prob_partial=pp, z_partial=zp, fc1=fc1)
+        state.update(h=h, y=y, shared_h=hs, prob_partial=pp, z_partial=zp, fc1=fc1,
+                     shared_fc1=fc1s)
     return out, aux, state
 
 
@@ -780,6 +832,7 @@ class BackwardWeights:
       w1t, w2t     W1^T and W2^T (dgrad of the two projections)
       w1           W1 (recompute of the fc1 pre-activations; only when the forward kept none)
       shared       the shared expert's W2^T (its dgrad)
+      shared_w1_proj  the shared expert's W1 (its fc1 recompute; only when the forward kept none)
       first        the token-side first row's operand: [W1s^T | Wr_hi^T | Wr_lo^T | Wr_hi^T]
                    (K padded to 64), so that one GEMM over [dfc1s | g_hi | g_hi | g_lo] gives the
                    shared expert's input gradient plus grad_logits . Wr in fp32 (the router's
@@ -821,8 +874,11 @@ class BackwardWeights:
         if self.shared_w1 is None:
             return None
         return self._get("shared", lambda: dict(
-            w1=Projection(self.shared_w1),
             w2t=Projection(self._transposed("shared_w2", self.shared_w2))))
+
+    @property
+    def shared_w1_proj(self):
+        return self._get("shared_w1", lambda: Projection(self.shared_w1))
 
     def first(self, w_router_t):
         """[1, d, Kc] bf16 (see the class notes) and the column layout (Fs, Ep, Kc)."""
@@ -900,7 +956,9 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
     dfc1s = None
     if sh:
         sb = bw.shared
-        fc1s = sb["w1"](x, None, seg, T)
+        fc1s = state.get("shared_fc1")
+        if fc1s is None:  # not kept by the forward
+            fc1s = bw.shared_w1_proj(x, None, seg, T)
         dhs = sb["w2t"](g, None, seg, T)
         dfc1s = act_bwd(fc1s, dhs, activation)
         mark("shared")

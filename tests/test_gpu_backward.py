@@ -45,8 +45,10 @@ def _packable(case):
                for h in widths)
 
 
-# (case, packed) pairs: every case with plain weights; the packed variant where the widths allow
-RUNS = [(c, False) for c in CASES] + [(c, True) for c in CASES if _packable(c)]
+# (case, mode) pairs: every case with plain weights; the fc1 recompute on three of them; the
+# packed variant where the widths allow
+RUNS = ([(c, "plain") for c in CASES] + [(c, "recompute") for c in CASES[:2] + CASES[4:5]]
+        + [(c, "packed") for c in CASES if _packable(c)])
 
 
 def ffn(x, w1, w2, activation):
@@ -100,11 +102,12 @@ def reference_grads(x, wr, bias, w1, w2, sw1, sw2, ids, G, g_aux, case, aux_coef
     return [t.grad for t in params]
 
 
-@pytest.mark.parametrize("case,packed", RUNS,
-                         ids=[f"{c.name}-{'packed' if p else 'plain'}" for c, p in RUNS])
-def test_backward_matches_fp32_autograd(case, packed):
-    """packed: the forward runs the packed GEMMs and keeps the fc1 pre-activations from the up
-    projection's launch (the module's training path); plain: the backward recomputes them."""
+@pytest.mark.parametrize("case,mode", RUNS, ids=[f"{c.name}-{m}" for c, m in RUNS])
+def test_backward_matches_fp32_autograd(case, mode):
+    """packed: the forward runs the packed GEMMs; plain: the plain-weight GEMMs. Both keep the
+    fc1 pre-activations from the up projection's launch (the module's training path);
+    recompute: the plain forward's kept fc1 (routed and shared) is dropped, so the backward
+    recomputes it."""
     from nexttransformer_amd import _native as nat, ops
     cpu = make_inputs(case)
     dev = torch.device("cuda")
@@ -119,6 +122,7 @@ def test_backward_matches_fp32_autograd(case, packed):
     if cpu["shared_w1"] is not None:
         sw1b, sw2b = cpu["shared_w1"].to(bf).to(dev), cpu["shared_w2"].to(bf).to(dev)
     fw = dict(w1=w1b, w2=w2b, shared_w1=sw1b, shared_w2=sw2b)
+    packed = mode == "packed"
     if packed:
         up = nat.EPI_SWIGLU if case.activation == 0 else nat.EPI_RELU2
         fw = {n: None if w is None else ops.pack_expert_weights(w, up if "1" in n else nat.EPI_NONE)
@@ -128,7 +132,10 @@ def test_backward_matches_fp32_autograd(case, packed):
                                       aux_coeff=aux_coeff, z_coeff=z_coeff, logit_bias=bias,
                                       shared_w1=fw["shared_w1"], shared_w2=fw["shared_w2"],
                                       want_logits=True, keep=True, packed=packed)
-    assert (state["fc1"] is not None) == packed
+    assert state["fc1"] is not None
+    assert (state["shared_fc1"] is not None) == (case.shared_H > 0)
+    if mode == "recompute":
+        state["fc1"] = state["shared_fc1"] = None
     gen = torch.Generator().manual_seed(case.seed + 7)
     G = torch.randn(case.T, case.d, generator=gen)
     grad_aux = torch.tensor([g_aux, 0.0, 0.0], device=dev)
@@ -234,6 +241,32 @@ def test_kept_pre_activations_equal_a_recompute(activation):
     pre_ref = ops.grouped_gemm_packed(x, src, offsets, ops.pack_expert_weights(w1, nat.EPI_NONE),
                                       nat.EPI_NONE, A)
     torch.cuda.synchronize()
+    assert torch.equal(h, h_ref)
+    assert torch.equal(pre, pre_ref)
+
+
+@pytest.mark.parametrize("activation,K,n_out", [(1, 1280, 320), (1, 320, 320), (0, 1280, 192)],
+                         ids=["relu2-K1280-N320", "relu2-K320-N320", "swiglu-K1280-N192"])
+def test_kept_pre_activations_plain_weights(activation, K, n_out):
+    """Plain-weight keep launch (256 x 256 kernel, the T3 cell's widths): its h equals the plain
+    launch's and its pre-activations an EPI_NONE launch over the same rows, bit for bit."""
+    from nexttransformer_amd import _native as nat, ops
+    gen = torch.Generator().manual_seed(51 + K + activation)
+    E, T = 6, 900
+    F = 2 * n_out if activation == 0 else n_out
+    up = nat.EPI_SWIGLU if activation == 0 else nat.EPI_RELU2
+    w1 = (torch.randn(E, F, K, generator=gen) * 0.05).to(torch.bfloat16).cuda()
+    x = torch.randn(T, K, generator=gen).to(torch.bfloat16).cuda()
+    sizes = torch.tensor([0, 300, 1, 513, 0, 250])
+    offsets = torch.cat([torch.zeros(1), sizes.cumsum(0)]).int().cuda()
+    A = int(sizes.sum())
+    src = torch.randint(0, T, (A,), generator=gen, dtype=torch.int32).cuda()
+    assert ops.plain_keep_supported(K, n_out)
+    h, pre = ops.grouped_gemm_keep(x, src, offsets, w1, up, A)
+    h_ref = ops.grouped_gemm(x, src, offsets, w1, up, A)
+    pre_ref = ops.grouped_gemm(x, src, offsets, w1, nat.EPI_NONE, A)
+    torch.cuda.synchronize()
+    assert pre.shape == (A, F)
     assert torch.equal(h, h_ref)
     assert torch.equal(pre, pre_ref)
 
