@@ -148,7 +148,8 @@ def train_bench(args, case, cpu, g):
         bw.w1t, bw.w2t, bw.shared, bw.first(w["router_t"])
         w1 = w["w1"]
         n_out = w1.shape[1] // 2 if case.activation == 0 else w1.shape[1]
-        if not w["packed"] and not ops.plain_keep_supported(w1.shape[2], n_out):
+        packed_up = w["packed"] if isinstance(w["packed"], bool) else w["packed"][0]
+        if not packed_up and not ops.plain_keep_supported(w1.shape[2], n_out):
             bw.w1  # the fc1 recompute operand: the forward keeps no fc1 then
 
     for _ in range(max(1, args.warmup)):
@@ -280,7 +281,8 @@ def gpu_inputs(case, fp8):
             g[name], g[name + "_scale"] = ops.quantize_fp8_blockwise(cpu[name].to(dev))
         else:
             g[name] = cpu[name].to(torch.bfloat16).to(dev)
-    # the packed-weight grouped GEMMs: always for fp8, for bf16 when every projection qualifies
+    # the packed-weight grouped GEMMs: always for fp8; for bf16 the up projections' weights
+    # when every up projection (routed, shared) qualifies, the down projections' likewise
     g["packed"] = False
     if fp8:
         from nexttransformer_amd import _native as nat
@@ -292,15 +294,19 @@ def gpu_inputs(case, fp8):
     else:
         from nexttransformer_amd import _native as nat
         up = nat.EPI_SWIGLU if case.activation == 0 else nat.EPI_RELU2
-        pairs = [("w1", up), ("w2", nat.EPI_NONE)]
+        names = [["w1"], ["w2"]]
         if g["shared_w1"] is not None:
-            pairs += [("shared_w1", up), ("shared_w2", nat.EPI_NONE)]
-        ok = all(ops.packable(g[n].shape[2], g[n].shape[1] // (2 if e == nat.EPI_SWIGLU else 1), e)
-                 for n, e in pairs)
-        if ok:
-            for n, e in pairs:
-                g[n] = ops.pack_expert_weights(g[n], e)
-            g["packed"] = True
+            names[0].append("shared_w1")
+            names[1].append("shared_w2")
+        pk = []
+        for group, e in zip(names, (up, nat.EPI_NONE)):
+            ok = all(ops.packable(g[n].shape[2], g[n].shape[1] // (2 if e == nat.EPI_SWIGLU else 1),
+                                  e) for n in group)
+            if ok:
+                for n in group:
+                    g[n] = ops.pack_expert_weights(g[n], e)
+            pk.append(ok)
+        g["packed"] = tuple(pk)
     torch.cuda.synchronize()
     return cpu, g
 
@@ -518,7 +524,7 @@ def main():
         n_out = case.H
         plain = "grouped_gemm_t256_kernel" if case.d >= 128 and n_out % 8 == 0 else "grouped_gemm_kernel"
         epi = "SwiGLU" if case.activation == 0 else "ReLU^2"
-        roofline = {"kernel": ("grouped_gemm_packed_kernel" if g["packed"] else plain)
+        roofline = {"kernel": ("grouped_gemm_packed_kernel" if g["packed"][0] else plain)
                               + f" (up-projection + {epi} epilogue)",
                     "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
@@ -538,7 +544,8 @@ def main():
         "dtype": "fp8-e4m3 (fp32 accumulate)" if fp8 else "bf16",
         "data": "synthetic: hidden ~N(0,1), router/expert weights ~N(0,0.02) random init, seed 0",
         "config": dict(describe(case, args.config, args.permute_rows, fp8),
-                       weights_packed=g["packed"]),
+                       weights_packed=(g["packed"] if fp8 else
+                                       dict(up=g["packed"][0], down=g["packed"][1]))),
         "roofline": roofline,
         "layer_tflops": round(layer_flops(case) / (ms * 1e-3) / 1e12, 2),
         "expert_load_max_over_mean": round(load_ratio, 3),

@@ -18,9 +18,9 @@ namespace {
 
 // One wave per output row at a time; the row is walked in column chunks of 64 lanes x VPC
 // 16-byte vectors (VPC = 2: 1024 bf16 per chunk). Waves are persistent over tokens (t, t + the
-// grid's waves, ...) and, when the row is one chunk (d <= 1024), issue the next token's k row
-// loads before summing the current token's, so 2 k VPC vectors per lane are in flight. KMAX
-// bounds k (registers are sized by it).
+// grid's waves, ...) and walk the items (token, chunk) in order, issuing the next item's k row
+// loads (and its shared-expert chunk) before summing the current one, so 2 (k + 1) VPC vectors
+// per lane are in flight. KMAX bounds k (registers are sized by it).
 constexpr int VPC = 2;
 
 template <int KMAX>
@@ -31,6 +31,7 @@ __device__ __forceinline__ void combine_rows(
     int64_t ld_out, int blocks) {
   const int lane = lane_id();
   const int vecs = d >> 3;
+  const int chunk = 64 * VPC;
   const int64_t waves = (int64_t)blocks * 4;
   const int64_t A = T * k;  // rows of y; out-of-range rows are clamped
   // The token's k destination rows and weights, lane j holding slot j.
@@ -43,7 +44,8 @@ __device__ __forceinline__ void combine_rows(
       dest = dest < 0 ? 0 : (dest >= A ? (int)(A - 1) : dest);
     }
   };
-  auto load_rows = [&](int dest, int v0, u32x4 (&rows)[KMAX][VPC]) {
+  // Chunk v0 of token t: its k expert rows and its shared-expert row (zeros without one).
+  auto load_rows = [&](int64_t t, int dest, int v0, u32x4 (&rows)[KMAX][VPC], u32x4 (&sh)[VPC]) {
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) {
       if (j < k) {
@@ -55,28 +57,24 @@ __device__ __forceinline__ void combine_rows(
         }
       }
     }
-  };
-  // Sum of the shared row (if any) and the k weighted rows of chunk v0 of token t, stored.
-  auto finish = [&](int64_t t, int v0, float w, const u32x4 (&rows)[KMAX][VPC]) {
-    float acc[VPC][8];
-    if (shared_y) {
-      const u32x4* srow = reinterpret_cast<const u32x4*>(shared_y + t * ld_shared);
+    const u32x4* srow = reinterpret_cast<const u32x4*>(shared_y + t * ld_shared);
 #pragma unroll
-      for (int q = 0; q < VPC; ++q) {
-        const int v = v0 + q * 64 + lane;
-        const u32x4 r = v < vecs ? srow[v] : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc[q][2 * i] = __builtin_bit_cast(float, r[i] << 16);
-          acc[q][2 * i + 1] = __builtin_bit_cast(float, r[i] & 0xffff0000u);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < VPC; ++q)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[q][i] = 0.f;
+    for (int q = 0; q < VPC; ++q) {
+      const int v = v0 + q * 64 + lane;
+      sh[q] = shared_y && v < vecs ? srow[v] : u32x4{0u, 0u, 0u, 0u};
     }
+  };
+  // Sum of the shared row and the k weighted rows of chunk v0 of token t, stored.
+  auto finish = [&](int64_t t, int v0, float w, const u32x4 (&rows)[KMAX][VPC],
+                    const u32x4 (&sh)[VPC]) {
+    float acc[VPC][8];
+#pragma unroll
+    for (int q = 0; q < VPC; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[q][2 * i] = __builtin_bit_cast(float, sh[q][i] << 16);
+        acc[q][2 * i + 1] = __builtin_bit_cast(float, sh[q][i] & 0xffff0000u);
+      }
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) {
       if (j < k) {
@@ -106,35 +104,34 @@ __device__ __forceinline__ void combine_rows(
   };
 
   int64_t t = (int64_t)blockIdx.x * 4 + wave_id();
-  if (vecs <= 64 * VPC) {  // one chunk per row: the next token's loads go out first
-    int dest, ndest;
-    float w, nw;
-    u32x4 rows[KMAX][VPC], next[KMAX][VPC];
-    plan(t, dest, w);
-    if (t < T) load_rows(dest, 0, rows);
-    for (; t < T; t += waves) {
-      const int64_t tn = t + waves;
+  if (t >= T) return;
+  int v0 = 0, dest;
+  float w;
+  u32x4 rows[KMAX][VPC], sh[VPC], nrows[KMAX][VPC], nsh[VPC];
+  plan(t, dest, w);
+  load_rows(t, dest, 0, rows, sh);
+  while (t < T) {
+    // the next item: the row's next chunk, or the first chunk of the wave's next token
+    int64_t tn = t;
+    int vn = v0 + chunk, ndest = dest;
+    float nw = w;
+    if (vn >= vecs) {
+      tn = t + waves;
+      vn = 0;
       plan(tn, ndest, nw);
-      if (tn < T) load_rows(ndest, 0, next);
-      finish(t, 0, w, rows);
-#pragma unroll
-      for (int j = 0; j < KMAX; ++j)
-#pragma unroll
-        for (int q = 0; q < VPC; ++q) rows[j][q] = next[j][q];
-      dest = ndest;
-      w = nw;
     }
-    return;
-  }
-  for (; t < T; t += waves) {
-    int dest;
-    float w;
-    plan(t, dest, w);
-    for (int v0 = 0; v0 < vecs; v0 += 64 * VPC) {
-      u32x4 rows[KMAX][VPC];
-      load_rows(dest, v0, rows);
-      finish(t, v0, w, rows);
-    }
+    if (tn < T) load_rows(tn, ndest, vn, nrows, nsh);
+    finish(t, v0, w, rows, sh);
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j)
+#pragma unroll
+      for (int q = 0; q < VPC; ++q) rows[j][q] = nrows[j][q];
+#pragma unroll
+    for (int q = 0; q < VPC; ++q) sh[q] = nsh[q];
+    t = tn;
+    v0 = vn;
+    dest = ndest;
+    w = nw;
   }
 }
 

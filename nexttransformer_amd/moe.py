@@ -152,13 +152,17 @@ def _ep_size(pg_collection):
 
 class _MoETrain(torch.autograd.Function):
     """The layer with gradients (bf16 experts): ops.moe_forward, then ops.moe_backward. Its
-    inputs after x are the fp32 masters themselves (router.weight, each expert's fc1 and fc2, the
-    shared expert's), so autograd hands each its own gradient; the bf16 operands the kernels read
-    are the layer's cached copies of those masters (MasterLinear casts its master per call,
-    megatron_moe.py:58-78; the cache is rebuilt when a master changes)."""
+    inputs after x are router.weight and the shared expert's fp32 masters, so autograd hands
+    each its own gradient; the bf16 operands the kernels read are the layer's cached copies of
+    the masters (MasterLinear casts its master per call, megatron_moe.py:58-78; the cache is
+    rebuilt when a master changes). The routed experts' masters (two per expert) are not inputs:
+    autograd's per-input bookkeeping costs a few microseconds per tensor (over a millisecond per
+    step at 256 experts), so the backward sets their .grad itself from one fp32 stack per
+    projection (MoELayer._accumulate_expert_grads); `anchor`, an empty tensor that requires
+    grad, keeps the backward in the graph when nothing else does."""
 
     @staticmethod
-    def forward(ctx, x, cfg, *masters):
+    def forward(ctx, x, cfg, anchor, *masters):
         layer = cfg["layer"]
         w = layer.packed_weights(keep_plain=True)
         out, aux, state = ops.moe_forward(
@@ -183,14 +187,15 @@ class _MoETrain(torch.autograd.Function):
         g = ops.moe_backward(grad_out, None if grad_aux is None else grad_aux.contiguous(), x,
                              w["router_t"], bw, ctx.state, top_k=cfg["top_k"],
                              score_fn=cfg["score_fn"], activation=cfg["activation"],
-                             aux_coeff=cfg["aux_coeff"], z_coeff=cfg["z_coeff"])
+                             aux_coeff=cfg["aux_coeff"], z_coeff=cfg["z_coeff"],
+                             weight_grads_fp32=True)
         ctx.state = ctx.x = ctx.w = None
-        g1, g2 = g["w1"].float(), g["w2"].float()
-        grads = [g["x"], None, g["router"]]
-        for i in range(g1.shape[0]):
-            grads += [g1[i], g2[i]]
+        pooled = layer._masters(pooled_only=True)  # fc1, fc2 of expert 0, then expert 1, ...
+        layer._accumulate_expert_grads("fc1", pooled[0::2], g["w1"])
+        layer._accumulate_expert_grads("fc2", pooled[1::2], g["w2"])
+        grads = [g["x"], None, None, g["router"]]
         if g["shared_w1"] is not None:
-            grads += [g["shared_w1"][0].float(), g["shared_w2"][0].float()]
+            grads += [g["shared_w1"][0], g["shared_w2"][0]]
         return tuple(grads)
 
 
@@ -228,6 +233,7 @@ class MoELayer(nn.Module):
         self._fc1_pool = _pool_masters([e.linear_fc1 for e in experts])
         self._fc2_pool = _pool_masters([e.linear_fc2 for e in experts])
         self._pool_ptrs = None  # the pooled weights' addresses on their pool slices
+        self._grad_stacks = {}  # per projection: the fp32 gradient stack the experts' .grad view
         self._param_tables = None
         self.shared_experts = (ExpertMLP(recipe.width, recipe.shared_expert_width, gated, device)
                                if recipe.shared_experts else None)
@@ -270,11 +276,38 @@ class MoELayer(nn.Module):
         self._pack_key = None
         self._bw_key = None
 
+    # -- expert weight gradients -----------------------------------------------------------
+
+    def _accumulate_expert_grads(self, name, params, grad):
+        """Adds one projection's expert gradients, the fp32 stack grad [E, rows, cols], into the
+        experts' .grad as autograd would (a .grad that is None takes the gradient, one that is
+        set accumulates it; parameters that do not require grad are skipped). When no .grad is
+        set (zero_grad with set_to_none), each takes its slice of `grad`, which is kept; when
+        every .grad is still its slice of the stack kept last time, the new gradients are
+        added to that stack in one pass."""
+        kept = self._grad_stacks.get(name)
+        if kept is not None and kept.shape == grad.shape and kept.device == grad.device:
+            base, step = kept.data_ptr(), kept.stride(0) * kept.element_size()
+            if all(p.grad is not None and p.grad.dtype == kept.dtype
+                   and p.grad.data_ptr() == base + i * step for i, p in enumerate(params)):
+                kept.add_(grad)
+                return
+        fresh = all(p.grad is None for p in params)
+        self._grad_stacks[name] = grad if fresh else None
+        for p, v in zip(params, grad.unbind(0)):
+            if not p.requires_grad:
+                continue
+            if p.grad is None:
+                p.grad = v
+            else:
+                p.grad.add_(v)
+
     # -- packed bf16 weights ---------------------------------------------------------------
 
-    def _masters(self, pooled_only=False):
+    def _masters(self, pooled_only=False, skip_pooled=False):
         """router.weight, each expert's fc1 and fc2 weights, then the shared expert's (read from
-        the modules' parameter tables, which a replaced weight updates in place)."""
+        the modules' parameter tables, which a replaced weight updates in place); only the
+        experts' with pooled_only, all but theirs with skip_pooled."""
         if self._param_tables is None:
             lins = []
             for e in self.experts.local_experts:
@@ -287,6 +320,8 @@ class MoELayer(nn.Module):
         router, pooled, shared = self._param_tables
         if pooled_only:
             return [t["weight"] for t in pooled]
+        if skip_pooled:
+            return [t["weight"] for t in router + shared]
         return [t["weight"] for t in router + pooled + shared]
 
     def _masters_key(self):
@@ -322,8 +357,9 @@ class MoELayer(nn.Module):
     def packed_weights(self, keep_plain=False):
         """Device weights the kernels read, rebuilt only when a master tensor changed:
         router_t fp32 [dp, E]; w1 [E, rows, dp]; w2 [E, dp, Hp]; shared_w1/2 [1, ...];
-        bf16 (in the packed fragment order of pack_expert_weights when `packed`), or for
-        expert_dtype "fp8" e4m3 codes (uint8) with their 128 x 128 block scales (w1_scale,
+        bf16 (the up projections' w1 in the packed fragment order of pack_expert_weights when
+        `packed`[0], the down projections' w2 when `packed`[1]), or for expert_dtype "fp8" e4m3
+        codes (uint8, always packed: `packed` True) with their 128 x 128 block scales (w1_scale,
         w2_scale, shared_w1_scale, shared_w2_scale).
 
         The bf16 GEMM tiles K and the SwiGLU halves in multiples of 64, the fp8 GEMM's scale
@@ -340,12 +376,17 @@ class MoELayer(nn.Module):
             dp = _round_up(r.width, align)
             gated = r.activation == "swiglu"
             dtype = torch.float32 if fp8 else torch.bfloat16
-            # The packed-weight GEMM (fragment-ordered weights streamed into registers) when every
-            # projection's K and width qualify and the weights live on the GPU.
+            # The packed-weight GEMM (fragment-ordered weights streamed into registers) for a
+            # projection when its K and width qualify for every expert kind (routed, shared) and
+            # the weights live on the GPU; fp8 always. (The T3 cell: the up projection packed,
+            # K = 1280; the down projection plain, K = 320.)
             widths = [r.expert_width] + ([r.shared_expert_width] if self.shared_experts else [])
-            use_packed = fp8 or (self.router.weight.is_cuda and all(
-                ops.packable(dp, _round_up(h, align), nat.EPI_SWIGLU if gated else nat.EPI_RELU2)
-                and ops.packable(_round_up(h, align), dp, nat.EPI_NONE) for h in widths))
+            on_gpu = self.router.weight.is_cuda
+            pk_up = fp8 or (on_gpu and all(ops.packable(
+                dp, _round_up(h, align), nat.EPI_SWIGLU if gated else nat.EPI_RELU2)
+                for h in widths))
+            pk_down = fp8 or (on_gpu and all(
+                ops.packable(_round_up(h, align), dp, nat.EPI_NONE) for h in widths))
 
             def stack(experts, hidden, pools=(None, None)):
                 hp = _round_up(hidden, align)
@@ -361,10 +402,8 @@ class MoELayer(nn.Module):
                     plain.append((w1, w2, w1t if keep_plain else None,
                                   w2t if keep_plain else None))
                     up = nat.EPI_SWIGLU if gated else nat.EPI_RELU2
-                    if use_packed:
-                        return (ops.pack_expert_weights(w1, up), None,
-                                ops.pack_expert_weights(w2, nat.EPI_NONE), None)
-                    return w1, None, w2, None
+                    return (ops.pack_expert_weights(w1, up) if pk_up else w1, None,
+                            ops.pack_expert_weights(w2, nat.EPI_NONE) if pk_down else w2, None)
                 if hp == hidden and dp == r.width:
                     w1 = torch.stack([e.linear_fc1.weight.detach() for e in experts]).to(dtype)
                     w2 = torch.stack([e.linear_fc2.weight.detach() for e in experts]).to(dtype)
@@ -383,11 +422,10 @@ class MoELayer(nn.Module):
                         w2[i, :r.width, :hidden] = e.linear_fc2.weight.detach()
                 if not fp8:
                     up = nat.EPI_SWIGLU if gated else nat.EPI_RELU2
-                    plain.append((w1.contiguous(), w2.contiguous(), None, None))
-                    if use_packed:
-                        return (ops.pack_expert_weights(w1.contiguous(), up), None,
-                                ops.pack_expert_weights(w2.contiguous(), nat.EPI_NONE), None)
-                    return w1, None, w2, None
+                    w1, w2 = w1.contiguous(), w2.contiguous()
+                    plain.append((w1, w2, None, None))
+                    return (ops.pack_expert_weights(w1, up) if pk_up else w1, None,
+                            ops.pack_expert_weights(w2, nat.EPI_NONE) if pk_down else w2, None)
                 w1q, w1s = ops.quantize_fp8_blockwise(w1.contiguous())
                 w2q, w2s = ops.quantize_fp8_blockwise(w2.contiguous())
                 up = nat.EPI_SWIGLU if gated else nat.EPI_RELU2
@@ -399,7 +437,8 @@ class MoELayer(nn.Module):
                                    dtype=torch.float32)
             router_t[:r.width] = self.router.weight.detach().t()
             packed = dict(router_t=router_t, shared_w1=None, shared_w2=None,
-                          shared_w1_scale=None, shared_w2_scale=None, packed=use_packed)
+                          shared_w1_scale=None, shared_w2_scale=None,
+                          packed=True if fp8 else (pk_up, pk_down))
             (packed["w1"], packed["w1_scale"], packed["w2"],
              packed["w2_scale"]) = stack(list(self.experts.local_experts), r.expert_width,
                                          (self._fc1_pool, self._fc2_pool))
@@ -469,7 +508,8 @@ class MoELayer(nn.Module):
         cfg = dict(layer=self, top_k=r.top_k, score_fn=_SCORE[r.score_function],
                    activation=_ACT[r.activation], aux_coeff=r.aux_loss_coeff,
                    z_coeff=r.z_loss_coeff, inject=inject and self.training)
-        out, aux = _MoETrain.apply(x, cfg, *self._masters())
+        anchor = torch.empty(0, device=x.device, requires_grad=True)
+        out, aux = _MoETrain.apply(x, cfg, anchor, *self._masters(skip_pooled=True))
         self.last_load = cfg["counts"].to(torch.int64)
         self.last_aux_parts = aux.detach()
         # "inject": the gradient comes from the backward itself, so the returned value is

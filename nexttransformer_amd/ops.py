@@ -570,7 +570,8 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
     (x_perm); by default the up-projection GEMM gathers them itself.
     packed: w1 (and shared_w1) were packed by pack_expert_weights (bf16) or
     pack_expert_weights_fp8 (e4m3) with the up epilogue, w2 (and shared_w2) with EPI_NONE; the
-    packed grouped GEMMs run both projections.
+    packed grouped GEMMs run both projections. For bf16 also a pair (up, down): which of the
+    two projections' weights are packed (the other ones plain [E, rows, K]).
     fp8 experts: pass w1/w2 (and the shared expert's) as uint8 e4m3 codes with their 128 x 128
     block scales (w*_scale, from quantize_fp8_blockwise); the token rows and the intermediate
     h are then quantised per row and both projections run on the fp8 grouped GEMM.
@@ -603,6 +604,7 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
     if w1.dtype == torch.uint8:
         _require(w1_scale is not None and w2_scale is not None,
                  "moe_forward: fp8 weights need w1_scale and w2_scale")
+        _require(isinstance(packed, bool), "moe_forward: fp8 weights take packed=True or False")
         xq, xs = quantize_fp8_rowwise(x)
         mark("quantize")
         h = grouped_gemm_fp8(xq, xs, src, offsets, w1, w1_scale, up_epi, A, packed)
@@ -625,30 +627,32 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
                      src_row=src, perm_w=perm_w, combine_dest=cdest, combine_w=cw, x_q=xq,
                      x_scale=xs)
         return out, aux, state
-    gemm = grouped_gemm_packed if packed else grouped_gemm
+    packed_up, packed_down = (packed, packed) if isinstance(packed, bool) else packed
+    gemm_up = grouped_gemm_packed if packed_up else grouped_gemm
+    gemm_down = grouped_gemm_packed if packed_down else grouped_gemm
 
     def up(a, rows_src, offs, w, rows):
         """The up projection; with keep, also the backward's fc1 pre-activations from the same
         launch where the kernel can store them (else None: the backward recomputes them)."""
-        if keep and packed:
+        if keep and packed_up:
             return grouped_gemm_packed_keep(a, rows_src, offs, w, up_epi, rows)
         if keep and plain_keep_supported(
                 w.shape[2], w.shape[1] // 2 if up_epi == nat.EPI_SWIGLU else w.shape[1]):
             return grouped_gemm_keep(a, rows_src, offs, w, up_epi, rows)
-        return gemm(a, rows_src, offs, w, up_epi, rows), None
+        return gemm_up(a, rows_src, offs, w, up_epi, rows), None
 
     if permute_rows:
-        h, fc1 = gemm(x_perm, None, offsets, w1, up_epi, A), None
+        h, fc1 = gemm_up(x_perm, None, offsets, w1, up_epi, A), None
     else:
         h, fc1 = up(x, src, offsets, w1, A)
     mark("gemm_up")
-    y = gemm(h, None, offsets, w2, nat.EPI_NONE, A)
+    y = gemm_down(h, None, offsets, w2, nat.EPI_NONE, A)
     mark("gemm_down")
     shared_y = hs = fc1s = None
     if shared_w1 is not None:
         seg = _whole_batch_segment(T, x.device)
         hs, fc1s = up(x, None, seg, shared_w1, T)
-        shared_y = gemm(hs, None, seg, shared_w2, nat.EPI_NONE, T)
+        shared_y = gemm_down(hs, None, seg, shared_w2, nat.EPI_NONE, T)
         mark("shared")
     out, aux = combine_aux(y, cdest, cw, shared_y, pp, zp, counts, aux_coeff, z_coeff)
     mark("combine")
@@ -906,13 +910,14 @@ def backward_weights(w1, w2, shared_w1=None, shared_w2=None, w_router_t=None, **
 
 def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
                  score_fn=nat.SCORE_SOFTMAX, activation=nat.ACT_SWIGLU, aux_coeff=0.01,
-                 z_coeff=0.001, mark=None):
+                 z_coeff=0.001, mark=None, weight_grads_fp32=False):
     """Gradients of moe_forward (bf16 experts) for grad_out [T, d] and grad_aux [3] (or None).
 
     state: moe_forward's state from a call with want_logits=True and keep=True; bw: from
     backward_weights. Returns dict(x bf16 [T, d], router fp32 [E, d] (the router weight's, i.e.
-    of w_router_t^T), w1 [E, F, d], w2 [E, d, H], shared_w1, shared_w2 (bf16)). Widths d, F, H
-    (and the shared expert's) must be multiples of 64.
+    of w_router_t^T), w1 [E, F, d], w2 [E, d, H], shared_w1, shared_w2 (bf16, or fp32 from the
+    same fp32 sums with weight_grads_fp32)). Widths d, F, H (and the shared expert's) must be
+    multiples of 64.
 
     All on this library's kernels: the fc1 recompute (when the forward kept no pre-activations),
     the dgrad of both projections (grouped GEMMs), the combine transpose and routing-weight
@@ -986,15 +991,16 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
                               state["z_partial"], state["counts"], 0.0, 0.0)
     mark("dx_sum")
     # expert weight gradients over each expert's rows; the shared expert's over all T rows
+    f32 = weight_grads_fp32
     res["w1"] = grouped_wgrad(dfc1, x, src, offsets, A, wgrad_splits(E, dfc1.shape[1], d, A // E,
-                                                                     x.device))
+                                                                     x.device), f32)
     res["w2"] = grouped_wgrad(gy, state["h"], None, offsets, A,
-                              wgrad_splits(E, d, state["h"].shape[1], A // E, x.device))
+                              wgrad_splits(E, d, state["h"].shape[1], A // E, x.device), f32)
     if sh:
         res["shared_w1"] = grouped_wgrad(dfc1s, x, None, seg, T,
-                                         wgrad_splits(1, dfc1s.shape[1], d, T, x.device))
+                                         wgrad_splits(1, dfc1s.shape[1], d, T, x.device), f32)
         res["shared_w2"] = grouped_wgrad(g, state["shared_h"], None, seg, T,
                                          wgrad_splits(1, d, state["shared_h"].shape[1], T,
-                                                      x.device))
+                                                      x.device), f32)
     mark("wgrad")
     return res

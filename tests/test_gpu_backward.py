@@ -307,3 +307,59 @@ def test_module_keeps_masters_in_one_buffer_and_falls_back_when_replaced():
         e3.linear_fc1.weight.mul_(0.5)
         c, _ = m(x)
     assert not torch.equal(a, b) and torch.equal(a, c)
+
+
+def test_module_expert_gradients_accumulate_like_autograd():
+    """The routed experts' .grad is set by the layer's backward (they are not autograd inputs):
+    taken as fresh slices after zero_grad(set_to_none), accumulated into the same stack when
+    every .grad is still its slice, added per tensor when they are mixed, left alone for a
+    master that does not require grad; the router's and the shared expert's go through
+    autograd. The backward is deterministic, so sums are checked bit for bit."""
+    from nexttransformer_amd.moe import MoELayer, set_aux_loss_scale
+    from nexttransformer_amd.moe_recipe import MoERecipe
+    r = MoERecipe(layers=2, width=256, heads=4, routed_experts=8, top_k=2, expert_width=64,
+                  activation="relu2", shared_experts=1, shared_expert_width=64,
+                  allow_any_expert_width=True, global_batch_tokens=2048)
+    m = MoELayer(r, 2)
+    set_aux_loss_scale(1.0, device="cuda")
+    gen = torch.Generator().manual_seed(61)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_(torch.randn(p.shape, generator=gen) * 0.05)
+    x = torch.randn(300, 256, generator=gen).to(torch.bfloat16).cuda()
+    G = torch.randn(300, 256, generator=gen).to(torch.bfloat16).cuda()
+    params = dict(m.named_parameters())
+    experts = [n for n in params if ".local_experts." in n]
+    assert len(experts) == 16
+
+    def backward():
+        out, _ = m(x)
+        out.backward(G)
+
+    m.zero_grad(set_to_none=True)
+    backward()
+    once = {n: p.grad.clone() for n, p in params.items()}
+    assert all(torch.isfinite(g).all() and g.abs().sum() > 0 for g in once.values())
+    ptr0 = params[experts[0]].grad.data_ptr()
+    backward()  # accumulate: every expert .grad is still its slice of the stack
+    for n, p in params.items():
+        assert torch.equal(p.grad, 2 * once[n]), n
+    assert params[experts[0]].grad.data_ptr() == ptr0
+    m.zero_grad(set_to_none=False)
+    backward()
+    for n, p in params.items():
+        assert torch.equal(p.grad, once[n]), n
+    # mixed: one expert's .grad cleared, one replaced by a tensor of its own
+    params[experts[3]].grad = None
+    params[experts[5]].grad = torch.ones_like(once[experts[5]])
+    backward()
+    for n, p in params.items():
+        want = once[n] if n == experts[3] else (
+            1 + once[n] if n == experts[5] else 2 * once[n])
+        assert torch.equal(p.grad, want), n
+    # a frozen expert master keeps no gradient
+    m.zero_grad(set_to_none=True)
+    params[experts[6]].requires_grad_(False)
+    backward()
+    assert params[experts[6]].grad is None
+    assert torch.equal(params[experts[7]].grad, once[experts[7]])

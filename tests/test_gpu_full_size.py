@@ -25,14 +25,16 @@ def _run(case, packed):
     dev = torch.device("cuda")
     up = nat.EPI_SWIGLU if case.activation == 0 else nat.EPI_RELU2
 
-    def bf(t, epi):
+    pk_up, pk_down = (packed, packed) if isinstance(packed, bool) else packed
+
+    def bf(t, epi, pk):
         if t is None:
             return None
         t = t.to(torch.bfloat16).to(dev)
-        return ops.pack_expert_weights(t, epi) if packed else t
+        return ops.pack_expert_weights(t, epi) if pk else t
     g = dict(x=cpu["x"].to(dev), wt=cpu["router"].t().contiguous().to(dev),
-             w1=bf(cpu["w1"], up), w2=bf(cpu["w2"], nat.EPI_NONE),
-             sw1=bf(cpu["shared_w1"], up), sw2=bf(cpu["shared_w2"], nat.EPI_NONE),
+             w1=bf(cpu["w1"], up, pk_up), w2=bf(cpu["w2"], nat.EPI_NONE, pk_down),
+             sw1=bf(cpu["shared_w1"], up, pk_up), sw2=bf(cpu["shared_w2"], nat.EPI_NONE, pk_down),
              bias=None if cpu["bias"] is None else cpu["bias"].to(dev))
 
     def fwd():
@@ -43,10 +45,14 @@ def _run(case, packed):
     return cpu, fwd
 
 
-# config 6 (the registered T3 cell: d=1280 is 10 router chunks, split unevenly over the router
-# waves; K=320 has no packed-weight form) runs on plain weights only
-@pytest.mark.parametrize("cfg,packed", [(c, p) for c in (2, 3, 4) for p in (False, True)] + [(6, False)],
-                         ids=lambda v: {False: "plain", True: "packed"}.get(v, str(v)) if isinstance(v, bool) else str(v))
+# config 6 (the registered T3 cell: d=1280 is 10 router chunks; K=320 has no packed-weight
+# form) runs on plain weights, and with the up projections packed (the module's choice there)
+FULL = [(c, p) for c in (2, 3, 4) for p in (False, True)] + [(6, False), (6, (True, False))]
+
+
+@pytest.mark.parametrize("cfg,packed", FULL, ids=[
+    f"{c}-" + ({False: "plain", True: "packed"}[p] if isinstance(p, bool) else "packed-up")
+    for c, p in FULL])
 def test_full_size_layer(cfg, packed):
     case = CONFIGS[cfg]
     print(f"[full-size] config {cfg} packed={packed}: {case}", flush=True)
