@@ -20,6 +20,10 @@
 // partial[i][s]; sum_splits_kernel then adds the chunks in ascending i (a fixed order, so the
 // result does not depend on scheduling) -- for long segments (a shared expert's single segment
 // of every token, the router's weight gradient) that would otherwise leave most CUs idle.
+#include <stdlib.h>
+#include <string.h>
+#include <type_traits>
+
 #include "common.h"
 
 namespace ntmoe {
@@ -186,6 +190,312 @@ __global__ __launch_bounds__(256) void grouped_wgrad_kernel(
   }
 }
 
+// ---- Transposing-read kernel ---------------------------------------------------------------
+// The same product with the operands staged as they lie in memory: every K step copies a
+// 32-row slab of A (TN columns) and of B (TM columns) straight into LDS with 16-byte direct-to-LDS
+// buffer loads, row-major, in a ring of three slabs, and the matrix-core operands are read out of
+// the slabs with gfx950's transposing LDS read ds_read_b64_tr_b16. That instruction works on
+// groups of 16 lanes: if lane p of a group addresses four consecutive 16-bit elements, lane
+// 4 a + b receives, as its element e, element b of the four addressed by lane 4 e + a. So when
+// lane p addresses row r0 + p / 4 at columns c + 4 (p % 4), lane j receives rows r0 .. r0 + 3 of
+// column c + j: two such reads give a lane the 8 consecutive K values (rows) of one column that
+// a v_mfma_f32_32x32x16_bf16 operand holds, without the register transposes of the kernel above.
+// LDS rows are TN or TM bf16 wide; the 16-byte chunk c of row r sits at chunk c ^ 4 (r % 4), so
+// the 16 lanes of a group (4 rows x 2 chunks) and the 32 of a half wave (4 rows x 4 chunks) each
+// hit distinct bank groups. Rows past the segment read zeros (the buffer range check of A's
+// per-tile resource, an out-of-range offset for B), columns past N or M repeat the last 8
+// columns (their outputs are not stored). With gathered B rows, the rows' indices go into an LDS
+// ring (direct-to-LDS, one instruction per wave) four slabs ahead of the data copies that read
+// them, so one count of outstanding vector memory operations covers indices and data.
+// Tile TN x TM (128 x 256 or 256 x 128) of one segment, 4 waves of TN/2 x TM/2, two workgroups
+// per CU; otherwise as the kernel above (split K, zero tiles for empty segments, fp32 or bf16).
+constexpr int kTK = 32;     // rows per slab
+constexpr int kTRing = 3;   // slabs in the ring
+constexpr int kTIdx = 5;    // index slots (four slabs ahead, plus the one being read)
+
+typedef __attribute__((address_space(1))) void gvoid_t;
+typedef __attribute__((address_space(3))) void lvoid_t;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+constexpr int kBufWord3 = 0x00020000;
+
+// 4 or 16 bytes per lane from a buffer at byte offset voff into LDS at dst + lane * (4 or 16)
+// (dst uniform). A __device__ function of its own: called from a kernel's lambda, the builtin
+// makes the host pass drop the kernel's launch stub.
+__device__ __forceinline__ void buffer_to_lds4(__amdgpu_buffer_rsrc_t rsrc, void* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lvoid_t*)dst, 4, voff, 0, 0, 0);
+}
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t rsrc, void* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lvoid_t*)dst, 16, voff, 0, 0, 0);
+}
+
+template <int TN, int TM>
+struct TrGeo {
+  static constexpr int kSlabA = kTK * TN * 2;             // bytes
+  static constexpr int kSlabB = kTK * TM * 2;
+  static constexpr int kStage = kSlabA + kSlabB;
+  static constexpr int kCopiesA = kSlabA / 1024 / 4;      // per wave per slab
+  static constexpr int kCopiesB = kSlabB / 1024 / 4;
+  static constexpr int kBN = TN / 64, kBM = TM / 64;      // 32-wide blocks per wave
+  static constexpr size_t lds() { return (size_t)kTRing * kStage + kTIdx * kTK * 4; }
+  static_assert(kCopiesA >= 1 && kCopiesB >= 1, "copies per wave");
+};
+
+template <int TN, int TM, bool GATHER, bool OUT_F32>
+__global__ __launch_bounds__(256, 2) void grouped_wgrad_tr_kernel(
+    const uint16_t* __restrict__ a, int64_t lda, const uint16_t* __restrict__ b, int64_t ldb,
+    int64_t b_rows, const int32_t* __restrict__ b_src_row, const int32_t* __restrict__ seg_offsets,
+    int num_segments, int64_t total_rows, int N, int M, int splits, void* __restrict__ c) {
+  using G = TrGeo<TN, TM>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  int* idx_ring = reinterpret_cast<int*>(smem + kTRing * G::kStage);  // [kTIdx][kTK]
+  const int ntn = (N + TN - 1) / TN, ntm = (M + TM - 1) / TM;
+  const int per_seg = ntn * ntm;
+  const int split = blockIdx.x / (num_segments * per_seg);
+  const int rest = blockIdx.x - split * num_segments * per_seg;
+  const int s = rest / per_seg;
+  const int tile = rest - s * per_seg;
+  const int n0 = (tile / ntm) * TN, m0 = (tile % ntm) * TM;
+  int64_t lo = seg_offsets[s], hi = seg_offsets[s + 1];
+  lo = lo < 0 ? 0 : (lo > total_rows ? total_rows : lo);
+  hi = hi < lo ? lo : (hi > total_rows ? total_rows : hi);
+  if (splits > 1) {  // this chunk: whole 64-row slabs, the last chunk ending at hi
+    const int64_t slabs = (hi - lo + 63) / 64;
+    const int64_t per = (slabs + splits - 1) / splits;
+    const int64_t c_lo = lo + split * per * 64, c_hi = c_lo + per * 64;
+    lo = c_lo < hi ? c_lo : hi;
+    hi = c_hi < hi ? c_hi : hi;
+  }
+  const int lane = lane_id(), wave = wave_id();
+  const int wn = wave >> 1, wm = wave & 1;  // the wave's TN/2 x TM/2 quarter
+  const int64_t c_base = ((int64_t)split * num_segments + s) * N * M;
+
+  floatx16 acc[G::kBN][G::kBM];
+#pragma unroll
+  for (int i = 0; i < G::kBN; ++i)
+#pragma unroll
+    for (int j = 0; j < G::kBM; ++j)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
+
+  const int rows = (int)(hi - lo);
+  const int n_slabs = (rows + kTK - 1) / kTK;
+  if (n_slabs > 0) {
+    // A: this tile's rows of the segment (a row past hi is out of range: zeros)
+    const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a + lo * lda), 0, (int)((int64_t)rows * lda * 2), kBufWord3);
+    // B: the whole matrix (gathered rows) or this tile's rows; an explicit out-of-range offset
+    // for rows past hi
+    const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(GATHER ? b : b + lo * ldb), 0,
+        (int)(GATHER ? b_rows * ldb * 2 : (int64_t)rows * ldb * 2), kBufWord3);
+    const __amdgpu_buffer_rsrc_t ir = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(GATHER ? b_src_row + lo : seg_offsets), 0, GATHER ? rows * 4 : 0, kBufWord3);
+
+    // Copy instruction i of this wave for an operand W columns wide covers rows
+    // (wave * copies + i) * rpi + lane / cpr of the slab, cpr = W / 8 chunks per row, rpi =
+    // 64 / cpr rows per instruction; the lane writes chunk position lane % cpr, i.e. global chunk
+    // (lane % cpr) ^ 4 (row % 4).
+    auto chunk_col = [&](int row, int cpr, int col0, int width) {
+      const int cg = (lane % cpr) ^ (4 * (row & 3));
+      const int col = col0 + 8 * cg;
+      return col < width ? col : width - 8;
+    };
+    int a_voff[G::kCopiesA], b_coloff[G::kCopiesB], b_row[G::kCopiesB];
+#pragma unroll
+    for (int i = 0; i < G::kCopiesA; ++i) {
+      constexpr int cpr = TN / 8, rpi = 64 / cpr;
+      const int row = (wave * G::kCopiesA + i) * rpi + lane / cpr;
+      a_voff[i] = row * (int)lda * 2 + chunk_col(row, cpr, n0, N) * 2;
+    }
+#pragma unroll
+    for (int i = 0; i < G::kCopiesB; ++i) {
+      constexpr int cpr = TM / 8, rpi = 64 / cpr;
+      b_row[i] = (wave * G::kCopiesB + i) * rpi + lane / cpr;
+      b_coloff[i] = chunk_col(b_row[i], cpr, m0, M) * 2;
+    }
+    // Index loads of slab t (GATHER): wave w copies indices of rows 8 w .. 8 w + 7 with lanes
+    // 0-7 (the other lanes are masked off: lane l would write dst + 4 l).
+    auto issue_idx = [&](int t) __attribute__((always_inline)) {
+      if constexpr (GATHER) {
+        int* dst = idx_ring + (t % kTIdx) * kTK + 8 * wave;
+        const int r = t * kTK + 8 * wave + lane;
+        if (lane < 8) buffer_to_lds4(ir, dst, r * 4);
+      }
+    };
+    auto issue_copies = [&](int t) __attribute__((always_inline)) {
+      unsigned char* st = smem + (t % kTRing) * G::kStage;
+      const int r0 = t * kTK;
+#pragma unroll
+      for (int i = 0; i < G::kCopiesA; ++i)
+        buffer_to_lds16(ar, st + (wave * G::kCopiesA + i) * 1024,
+                          a_voff[i] + r0 * (int)lda * 2);
+#pragma unroll
+      for (int i = 0; i < G::kCopiesB; ++i) {
+        const int r = r0 + b_row[i];
+        int voff;
+        if (GATHER) {
+          int g = idx_ring[(t % kTIdx) * kTK + b_row[i]];
+          g = g < 0 ? 0 : (g >= b_rows ? (int)b_rows - 1 : g);
+          voff = r < rows ? g * (int)ldb * 2 + b_coloff[i] : 0x7fffffff;
+        } else {
+          voff = r < rows ? r * (int)ldb * 2 + b_coloff[i] : 0x7fffffff;
+        }
+        buffer_to_lds16(br, st + G::kSlabA + (wave * G::kCopiesB + i) * 1024, voff);
+      }
+    };
+    // Vector memory operations per slab and wave after its copies: the next slab's index load
+    // and copies.
+    constexpr int kPer = G::kCopiesA + G::kCopiesB + (GATHER ? 1 : 0);
+
+    // Fragment reads: lane l = 16 g + p of a 32 x 32 x 16 operand block at column cb (tile
+    // relative) and K rows k0 .. k0 + 15: provider row k0 + 8 (l / 32) + 4 t + p / 4, columns
+    // cb + 16 (g % 2) + 4 (p % 4); lane l gets column cb + l % 32, rows k0 + 8 (l / 32) + 4 t ..
+    // + 3. Per-lane byte offsets inside a slab for k0 = 0 and t = 0; t and the K step add whole
+    // rows (4 and 16), multiples of 4, so the chunk swizzle 4 (row % 4) is unchanged and they
+    // go into the instruction's offset field.
+    const int pg = (lane >> 4) & 1, pp = lane & 15, ph = lane >> 5;
+    auto tr_off = [&](int width, int cb) {
+      const int row = 8 * ph + (pp >> 2);
+      const int col = cb + 16 * pg + 4 * (pp & 3);
+      const int chunk = (col >> 3) ^ (4 * (row & 3));
+      return (uint32_t)(row * width * 2 + chunk * 16 + (col & 7) * 2);
+    };
+    const uint32_t smem_base = (uint32_t)(uintptr_t)smem;
+    uint32_t offa[G::kBN], offb[G::kBM];
+#pragma unroll
+    for (int i = 0; i < G::kBN; ++i) offa[i] = smem_base + tr_off(TN, (TN / 2) * wn + 32 * i);
+#pragma unroll
+    for (int j = 0; j < G::kBM; ++j)
+      offb[j] = smem_base + G::kSlabA + tr_off(TM, (TM / 2) * wm + 32 * j);
+    // Inline assembly keeps the reads where they are written and out of the compiler's wait
+    // analysis (which would wait for every outstanding direct-to-LDS copy before any LDS read);
+    // frag_wait completes them with a wait that names their registers.
+    struct Frags {
+      u32x2 a[G::kBN][2], b[G::kBM][2];
+    };
+    auto read_frags = [](uint32_t stage_off, auto kk_c, const uint32_t (&oa)[G::kBN],
+                         const uint32_t (&ob)[G::kBM], Frags& f) __attribute__((always_inline)) {
+      constexpr int kk = decltype(kk_c)::value;
+#pragma unroll
+      for (int i = 0; i < G::kBN; ++i) {
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                     : "=v"(f.a[i][0]) : "v"(oa[i] + stage_off), "n"(16 * kk * TN * 2));
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                     : "=v"(f.a[i][1]) : "v"(oa[i] + stage_off), "n"((16 * kk + 4) * TN * 2));
+      }
+#pragma unroll
+      for (int j = 0; j < G::kBM; ++j) {
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                     : "=v"(f.b[j][0]) : "v"(ob[j] + stage_off), "n"(16 * kk * TM * 2));
+        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                     : "=v"(f.b[j][1]) : "v"(ob[j] + stage_off), "n"((16 * kk + 4) * TM * 2));
+      }
+    };
+    auto frag_wait = [](Frags& f) __attribute__((always_inline)) {
+      static_assert(G::kBN + G::kBM == 6, "operand count of the wait");
+      if constexpr (G::kBN == 2) {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(f.a[0][0]), "+v"(f.a[0][1]), "+v"(f.a[1][0]), "+v"(f.a[1][1]),
+                       "+v"(f.b[0][0]), "+v"(f.b[0][1]), "+v"(f.b[1][0]), "+v"(f.b[1][1]),
+                       "+v"(f.b[2][0]), "+v"(f.b[2][1]), "+v"(f.b[3][0]), "+v"(f.b[3][1])
+                     :
+                     : "memory");
+      } else {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(f.a[0][0]), "+v"(f.a[0][1]), "+v"(f.a[1][0]), "+v"(f.a[1][1]),
+                       "+v"(f.a[2][0]), "+v"(f.a[2][1]), "+v"(f.a[3][0]), "+v"(f.a[3][1]),
+                       "+v"(f.b[0][0]), "+v"(f.b[0][1]), "+v"(f.b[1][0]), "+v"(f.b[1][1])
+                     :
+                     : "memory");
+      }
+    };
+    auto mfmas = [&](const Frags& f) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < G::kBN; ++i) {
+        const bf16x8 fa = __builtin_bit_cast(
+            bf16x8, u32x4{f.a[i][0][0], f.a[i][0][1], f.a[i][1][0], f.a[i][1][1]});
+#pragma unroll
+        for (int j = 0; j < G::kBM; ++j) {
+          const bf16x8 fb = __builtin_bit_cast(
+              bf16x8, u32x4{f.b[j][0][0], f.b[j][0][1], f.b[j][1][0], f.b[j][1][1]});
+          // D[m][n] += B-side (m x k) . A-side (k x n): lane holds column n, runs of 4 rows m
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb, fa, acc[i][j], 0, 0, 0);
+        }
+      }
+    };
+    // Workgroup barrier without a memory fence (a fence would wait for the copies in flight).
+    auto barrier = []() __attribute__((always_inline)) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    };
+
+    if (GATHER) {
+      issue_idx(0);
+      issue_idx(1);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      barrier();
+      issue_idx(2);
+      issue_copies(0);
+      issue_idx(3);
+      issue_copies(1);
+    } else {
+      issue_copies(0);
+      issue_copies(1);
+    }
+    Frags f0, f1;
+    for (int t = 0; t < n_slabs; ++t) {
+      // slab t's copies (and every index load issued before them) have landed once at most the
+      // next slab's operations are outstanding
+      if (t + 1 < n_slabs) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kPer) : "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      barrier();
+      if (t + 2 < n_slabs) {
+        issue_idx(t + 4);
+        issue_copies(t + 2);
+      }
+      const uint32_t st = (t % kTRing) * G::kStage;
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(st, std::integral_constant<int, 0>(), offa, offb, f0);
+      frag_wait(f0);
+      read_frags(st, std::integral_constant<int, 1>(), offa, offb, f1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(f0);
+      __builtin_amdgcn_sched_barrier(0);
+      frag_wait(f1);
+      mfmas(f1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // acc[i][j]: n = n0 + TN/2 wn + 32 i + lane % 32,
+  //            m = m0 + TM/2 wm + 32 j + 8 (q / 4) + 4 (lane / 32) + q % 4
+#pragma unroll
+  for (int i = 0; i < G::kBN; ++i) {
+    const int n = n0 + (TN / 2) * wn + 32 * i + (lane & 31);
+    if (n0 + (TN / 2) * wn + 32 * i >= N) continue;
+#pragma unroll
+    for (int j = 0; j < G::kBM; ++j) {
+      if (m0 + (TM / 2) * wm + 32 * j >= M) continue;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int m = m0 + (TM / 2) * wm + 32 * j + 8 * g + 4 * (lane >> 5);
+        const int64_t off = c_base + (int64_t)n * M + m;
+        if constexpr (OUT_F32) {
+          const floatx4 o = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                             acc[i][j][4 * g + 3]};
+          *reinterpret_cast<floatx4*>(reinterpret_cast<float*>(c) + off) = o;
+        } else {
+          u32x2 o;
+          o[0] = pack_bf16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]);
+          o[1] = pack_bf16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(c) + off) = o;
+        }
+      }
+    }
+  }
+}
+
 // out[j] = sum over i = 0, 1, ..., splits - 1 (in that order) of partial[i][j], fp32, stored as
 // fp32 or rounded once to bf16; 4 consecutive elements per thread.
 template <bool OUT_F32>
@@ -206,6 +516,53 @@ __global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict
 
 }  // namespace
 
+namespace {
+
+// NT_MOE_WGRAD=regs selects the register-transpose kernel (for comparisons).
+bool wgrad_regs_override() {
+  static const bool v = [] {
+    const char* e = getenv("NT_MOE_WGRAD");
+    return e && !strcmp(e, "regs");
+  }();
+  return v;
+}
+
+template <int TN, int TM, bool GATHER, bool OUT_F32>
+hipError_t launch_tr(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                     int64_t b_rows, const int32_t* b_src_row, const int32_t* seg_offsets,
+                     int num_segments, int64_t total_rows, int N, int M, int splits, void* c,
+                     hipStream_t stream) {
+  auto kern = grouped_wgrad_tr_kernel<TN, TM, GATHER, OUT_F32>;
+  const size_t lds = TrGeo<TN, TM>::lds();
+  hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
+  if (err != hipSuccess) return err;
+  const int64_t tiles = (int64_t)num_segments * ((N + TN - 1) / TN) * ((M + TM - 1) / TM);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(tiles * splits)), dim3(256), lds, stream, a, lda, b,
+                     ldb, b_rows, b_src_row, seg_offsets, num_segments, total_rows, N, M, splits,
+                     c);
+  return hipGetLastError();
+}
+
+// The transposing-read kernel, 128 x 256 tiles when N <= M, else 256 x 128.
+template <bool OUT_F32>
+hipError_t launch_tr_any(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                         int64_t b_rows, const int32_t* b_src_row, const int32_t* seg_offsets,
+                         int num_segments, int64_t total_rows, int N, int M, int splits, void* c,
+                         hipStream_t stream) {
+  const bool g = b_src_row != nullptr;
+#define NT_TR(TN, TM, GG)                                                                      \
+  return launch_tr<TN, TM, GG, OUT_F32>(a, lda, b, ldb, b_rows, b_src_row, seg_offsets,         \
+                                        num_segments, total_rows, N, M, splits, c, stream);
+  if (N <= M) {
+    if (g) { NT_TR(128, 256, true) } else { NT_TR(128, 256, false) }
+  } else {
+    if (g) { NT_TR(256, 128, true) } else { NT_TR(256, 128, false) }
+  }
+#undef NT_TR
+}
+
+}  // namespace
+
 hipError_t launch_grouped_wgrad(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                                 int64_t b_rows, const int32_t* b_src_row,
                                 const int32_t* seg_offsets, int num_segments, int64_t total_rows,
@@ -213,6 +570,25 @@ hipError_t launch_grouped_wgrad(const uint16_t* a, int64_t lda, const uint16_t* 
                                 hipStream_t stream) {
   const int64_t tiles = (int64_t)num_segments * ((N + kWT - 1) / kWT) * ((M + kWT - 1) / kWT);
   if (tiles == 0) return hipSuccess;
+  // The transposing-read kernel addresses its operands through 32-bit buffer offsets.
+  const int64_t lim = (int64_t)1 << 31;
+  if (!wgrad_regs_override() && total_rows * lda * 2 < lim &&
+      (b_src_row ? b_rows : total_rows) * ldb * 2 < lim) {
+    hipError_t err;
+    if (splits <= 1)
+      return c_f32 ? launch_tr_any<true>(a, lda, b, ldb, b_rows, b_src_row, seg_offsets,
+                                         num_segments, total_rows, N, M, 1, c, stream)
+                   : launch_tr_any<false>(a, lda, b, ldb, b_rows, b_src_row, seg_offsets,
+                                          num_segments, total_rows, N, M, 1, c, stream);
+    err = launch_tr_any<true>(a, lda, b, ldb, b_rows, b_src_row, seg_offsets, num_segments,
+                              total_rows, N, M, splits, static_cast<void*>(partial), stream);
+    if (err != hipSuccess) return err;
+    const int64_t count = (int64_t)num_segments * N * M;
+    auto sum = c_f32 ? sum_splits_kernel<true> : sum_splits_kernel<false>;
+    hipLaunchKernelGGL(sum, dim3((unsigned)((count / 4 + 255) / 256)), dim3(256), 0, stream,
+                       partial, splits, count, c);
+    return hipGetLastError();
+  }
   if (splits <= 1) {
     auto kern = c_f32 ? grouped_wgrad_kernel<true> : grouped_wgrad_kernel<false>;
     hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(256), 0, stream, a, lda, b, ldb, b_rows,

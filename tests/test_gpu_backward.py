@@ -221,6 +221,43 @@ def test_grouped_wgrad_matches_float64(gather):
             torch.testing.assert_close(got[s].double(), ref, rtol=8e-3, atol=1e-2)
 
 
+WGRAD_SHAPES = [(320, 192, False, 1), (192, 320, True, 1), (64, 64, True, 1),
+                (320, 1280, True, 1), (1280, 320, False, 1), (128, 256, True, 3),
+                (256, 128, False, 4)]
+
+
+@pytest.mark.parametrize("N,M,gather,splits", WGRAD_SHAPES,
+                         ids=[f"N{n}-M{m}-{'gather' if g else 'rows'}-s{k}"
+                              for n, m, g, k in WGRAD_SHAPES])
+def test_grouped_wgrad_shapes_fp32_and_bf16(N, M, gather, splits):
+    """Both tile orientations (N <= M: 128 x 256, else 256 x 128), partial tiles in N and M
+    (320 = 256 + 64, 192 = 128 + 64), ragged segments (empty, 1 row, not a multiple of the
+    32-row slab, several slabs), gathered B rows (with indices past a slab boundary), split K in
+    fixed order; fp32 output against float64 at fp32-accumulation tolerance, bf16 output equal
+    to the fp32 result rounded once."""
+    from nexttransformer_amd import ops
+    gen = torch.Generator().manual_seed(N + 3 * M + splits)
+    sizes = [0, 1, 31, 33, 96, 0, 257, 64]
+    total = sum(sizes)
+    offsets = torch.tensor([0] + list(torch.tensor(sizes).cumsum(0)), dtype=torch.int32)
+    a = torch.randn(total, N, generator=gen).to(torch.bfloat16)
+    b_rows = 97 if gather else total
+    b = torch.randn(b_rows, M, generator=gen).to(torch.bfloat16)
+    src = torch.randint(0, b_rows, (total,), generator=gen, dtype=torch.int32) if gather else None
+    args = (a.cuda(), b.cuda(), None if src is None else src.cuda(), offsets.cuda(), total, splits)
+    got32 = ops.grouped_wgrad(*args, out_fp32=True).cpu()
+    got16 = ops.grouped_wgrad(*args).cpu()
+    assert torch.equal(got16, got32.to(torch.bfloat16))
+    bb = b[src.long()] if gather else b
+    for s in range(len(sizes)):
+        lo, hi = int(offsets[s]), int(offsets[s + 1])
+        ref = a[lo:hi].double().t() @ bb[lo:hi].double()
+        if hi == lo:
+            assert torch.equal(got32[s], torch.zeros(N, M))
+        else:
+            torch.testing.assert_close(got32[s].double(), ref, rtol=1e-5, atol=1e-4)
+
+
 @pytest.mark.parametrize("activation", [0, 1])
 def test_kept_pre_activations_equal_a_recompute(activation):
     """The keep launch's h equals the plain packed launch's, and its pre-activations equal an
