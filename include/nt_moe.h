@@ -381,6 +381,19 @@ int nt_moe_act_bwd(const uint16_t* fc1, const uint16_t* grad_h, int64_t rows, in
                    int32_t activation, uint16_t* grad_fc1, nt_moe_stream_t stream);
 
 /*
+ * The backward's first-row operand (the shared expert's and the router's input gradients as
+ * one GEMM over a concatenated K; autograd of megatron_moe.py:95-99's router GEMM and of the
+ * shared expert, :150): out bf16 [T, Kc] rows
+ *   [dfc1s (Fs) | g_hi (Ep) | g_hi (Ep) | g_lo (Ep) | 0 ...],   g = grad_logits fp32 [T, E]
+ * g_hi = g rounded to bf16 (nearest even), g_lo = (g - g_hi) rounded to bf16, columns past E of
+ * each Ep block zero. dfc1s bf16 [T, Fs] (the shared expert's fc1 gradient; Fs = 0: none).
+ * E <= Ep; Fs, Ep, Kc multiples of 8; Kc >= Fs + 3 Ep. 16-byte aligned.
+ */
+int nt_moe_backward_first_operand(const float* grad_logits, int32_t E, const uint16_t* dfc1s,
+                                  int32_t Fs, int64_t T, int32_t Ep, int32_t Kc, uint16_t* out,
+                                  nt_moe_stream_t stream);
+
+/*
  * Router backward: grad_logits fp32 [T, E] from grad_w (the routing weights' gradient, top-k
  * slot order) through the k-selected normalisation of score_fn, plus the load-balance and
  * z-loss terms when grad_aux (device fp32 [3], the gradient of nt_moe_combine_aux's

@@ -69,6 +69,7 @@ SIGNATURES = {
                                               _i32, _i32, _p, _p]),
     "nt_moe_combine_aux": (_i32, [_p, _p, _p, _i64, _i32, _i32, _p, _i64, _p, _i64, _p, _p, _p,
                                   _i32, _f32, _f32, _p, _p]),
+    "nt_moe_backward_first_operand": (_i32, [_p, _i32, _p, _i32, _i64, _i32, _i32, _p, _p]),
 }
 
 _LIB = None

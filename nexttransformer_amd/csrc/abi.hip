@@ -243,6 +243,22 @@ int nt_moe_act_bwd(const uint16_t* fc1, const uint16_t* grad_h, int64_t rows, in
                   "act_bwd");
 }
 
+int nt_moe_backward_first_operand(const float* grad_logits, int32_t E, const uint16_t* dfc1s,
+                                  int32_t Fs, int64_t T, int32_t Ep, int32_t Kc, uint16_t* out,
+                                  nt_moe_stream_t stream) {
+  NT_REQUIRE(T >= 0 && E > 0 && Ep >= E && Ep % 8 == 0 && Fs >= 0 && Fs % 8 == 0 && Kc % 8 == 0 &&
+                 Kc >= Fs + 3 * Ep,
+             "backward_first_operand: need E <= Ep, Kc >= Fs + 3 Ep, Fs, Ep, Kc multiples of 8");
+  if (T == 0) return ok();
+  NT_REQUIRE(grad_logits && out && (Fs == 0 || dfc1s),
+             "backward_first_operand: null buffer");
+  NT_REQUIRE(aligned16(out) && (Fs == 0 || aligned16(dfc1s)),
+             "backward_first_operand: buffers must be 16-byte aligned");
+  return launched(launch_first_operand(grad_logits, E, dfc1s, Fs, T, Ep, Kc, out,
+                                       reinterpret_cast<hipStream_t>(stream)),
+                  "backward_first_operand");
+}
+
 namespace {
 
 int check_wgrad(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t b_rows,

@@ -246,6 +246,40 @@ __global__ __launch_bounds__(256) void router_bwd_kernel(
   }
 }
 
+// The backward's first-row operand: a [T, Kc] bf16 row is
+//   [dfc1_shared (Fs) | g_hi (Ep) | g_hi (Ep) | g_lo (Ep) | 0 ...]
+// with g = grad_logits (fp32 [T, E], columns past E zero in each Ep block), g_hi = g rounded to
+// bf16 and g_lo = (g - g_hi) rounded to bf16 (the remainder is exact in fp32). One thread per 8
+// columns (Fs, Ep and Kc are multiples of 8, so 8 columns never straddle two parts).
+__global__ __launch_bounds__(256) void first_operand_kernel(
+    const float* __restrict__ g, int E, const uint16_t* __restrict__ dfc1s, int Fs, int64_t T,
+    int Ep, int Kc, uint16_t* __restrict__ out) {
+  const int per_row = Kc / 8;
+  const int64_t n = T * per_row;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / per_row;
+    const int j0 = (int)(i - t * per_row) * 8;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (j0 < Fs) {
+      v = *reinterpret_cast<const u32x4*>(dfc1s + t * Fs + j0);
+    } else if (j0 < Fs + 3 * Ep) {
+      const int part = (j0 - Fs) / Ep, e0 = (j0 - Fs) - part * Ep;
+      const float* row = g + t * E;
+      uint16_t h[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float x = e0 + q < E ? row[e0 + q] : 0.f;
+        const uint16_t hi = f32_to_bf16_bits(x);
+        h[q] = part < 2 ? hi : f32_to_bf16_bits(x - __builtin_bit_cast(float, (uint32_t)hi << 16));
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = (uint32_t)h[2 * q] | ((uint32_t)h[2 * q + 1] << 16);
+    }
+    *reinterpret_cast<u32x4*>(out + t * Kc + j0) = v;
+  }
+}
+
 }  // namespace
 
 hipError_t launch_combine_bwd(const uint16_t* g, int64_t ld_g, const uint16_t* y,
@@ -288,6 +322,18 @@ hipError_t launch_router_bwd(const float* logits, const int32_t* topk_ids, const
   hipLaunchKernelGGL(router_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, logits,
                      topk_ids, topk_w, dw, counts, T, E, k, score_fn, grad_aux, aux_coeff, z_coeff,
                      dlogits);
+  return hipGetLastError();
+}
+
+hipError_t launch_first_operand(const float* grad_logits, int E, const uint16_t* dfc1s, int Fs,
+                                int64_t T, int Ep, int Kc, uint16_t* out, hipStream_t stream) {
+  const int64_t n = T * (Kc / 8);
+  if (n == 0) return hipSuccess;
+  int64_t blocks = (n + 255) / 256;
+  const int64_t cap = (int64_t)num_cus() * 16;
+  if (blocks > cap) blocks = cap;
+  hipLaunchKernelGGL(first_operand_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     grad_logits, E, dfc1s, Fs, T, Ep, Kc, out);
   return hipGetLastError();
 }
 

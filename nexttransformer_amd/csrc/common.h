@@ -83,6 +83,8 @@ hipError_t launch_combine_bwd(const uint16_t* g, int64_t ld_g, const uint16_t* y
                               float* dw, hipStream_t stream);
 hipError_t launch_act_bwd(const uint16_t* fc1, const uint16_t* dh, int64_t rows, int H,
                           int activation, uint16_t* dfc1, hipStream_t stream);
+hipError_t launch_first_operand(const float* grad_logits, int E, const uint16_t* dfc1s, int Fs,
+                                int64_t T, int Ep, int Kc, uint16_t* out, hipStream_t stream);
 hipError_t launch_router_bwd(const float* logits, const int32_t* topk_ids, const float* topk_w,
                              const float* dw, const int32_t* counts, int64_t T, int E, int k,
                              int score_fn, const float* grad_aux, float aux_coeff, float z_coeff,

@@ -444,6 +444,9 @@ __global__ __launch_bounds__(256, 2) void grouped_wgrad_tr_kernel(
       issue_copies(0);
       issue_copies(1);
     }
+    // A wave whose quarter lies wholly past N or M (the second half of a 64-wide last tile)
+    // only copies and waits: its products would all be dropped.
+    const bool live = n0 + (TN / 2) * wn < N && m0 + (TM / 2) * wm < M;
     Frags f0, f1;
     for (int t = 0; t < n_slabs; ++t) {
       // slab t's copies (and every index load issued before them) have landed once at most the
@@ -455,6 +458,7 @@ __global__ __launch_bounds__(256, 2) void grouped_wgrad_tr_kernel(
         issue_idx(t + 4);
         issue_copies(t + 2);
       }
+      if (!live) continue;
       const uint32_t st = (t % kTRing) * G::kStage;
       __builtin_amdgcn_sched_barrier(0);
       read_frags(st, std::integral_constant<int, 0>(), offa, offb, f0);

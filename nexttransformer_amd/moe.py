@@ -191,8 +191,8 @@ class _MoETrain(torch.autograd.Function):
                              weight_grads_fp32=True)
         ctx.state = ctx.x = ctx.w = None
         pooled = layer._masters(pooled_only=True)  # fc1, fc2 of expert 0, then expert 1, ...
-        layer._accumulate_expert_grads("fc1", pooled[0::2], g["w1"])
-        layer._accumulate_expert_grads("fc2", pooled[1::2], g["w2"])
+        layer._accumulate_expert_grads(pooled[0::2], g["w1"])
+        layer._accumulate_expert_grads(pooled[1::2], g["w2"])
         grads = [g["x"], None, None, g["router"]]
         if g["shared_w1"] is not None:
             grads += [g["shared_w1"][0], g["shared_w2"][0]]
@@ -233,7 +233,6 @@ class MoELayer(nn.Module):
         self._fc1_pool = _pool_masters([e.linear_fc1 for e in experts])
         self._fc2_pool = _pool_masters([e.linear_fc2 for e in experts])
         self._pool_ptrs = None  # the pooled weights' addresses on their pool slices
-        self._grad_stacks = {}  # per projection: the fp32 gradient stack the experts' .grad view
         self._param_tables = None
         self.shared_experts = (ExpertMLP(recipe.width, recipe.shared_expert_width, gated, device)
                                if recipe.shared_experts else None)
@@ -278,22 +277,30 @@ class MoELayer(nn.Module):
 
     # -- expert weight gradients -----------------------------------------------------------
 
-    def _accumulate_expert_grads(self, name, params, grad):
+    def _accumulate_expert_grads(self, params, grad):
         """Adds one projection's expert gradients, the fp32 stack grad [E, rows, cols], into the
         experts' .grad as autograd would (a .grad that is None takes the gradient, one that is
         set accumulates it; parameters that do not require grad are skipped). When no .grad is
-        set (zero_grad with set_to_none), each takes its slice of `grad`, which is kept; when
-        every .grad is still its slice of the stack kept last time, the new gradients are
-        added to that stack in one pass."""
-        kept = self._grad_stacks.get(name)
-        if kept is not None and kept.shape == grad.shape and kept.device == grad.device:
-            base, step = kept.data_ptr(), kept.stride(0) * kept.element_size()
-            if all(p.grad is not None and p.grad.dtype == kept.dtype
-                   and p.grad.data_ptr() == base + i * step for i, p in enumerate(params)):
-                kept.add_(grad)
+        set (zero_grad with set_to_none), each takes its slice of `grad`; when every .grad is
+        still its slice of one such stack (same storage, consecutive, contiguous), the new
+        gradients are added to that stack in one pass; otherwise tensor by tensor."""
+        if all(p.grad is None for p in params):
+            for p, v in zip(params, grad.unbind(0)):
+                if p.requires_grad:
+                    p.grad = v
+            return
+        g0 = params[0].grad
+        if (g0 is not None and g0.dtype == grad.dtype and g0.device == grad.device
+                and tuple(g0.shape) == tuple(grad.shape[1:]) and g0.is_contiguous()):
+            storage, base, step = g0.untyped_storage().data_ptr(), g0.data_ptr(), g0.nbytes
+            if all(p.grad is not None and p.grad.is_contiguous()
+                   and p.grad.data_ptr() == base + i * step
+                   and p.grad.untyped_storage().data_ptr() == storage
+                   for i, p in enumerate(params)):
+                # as_strided checks that the extent lies inside the storage
+                g0.as_strided(grad.shape, (g0.numel(),) + tuple(g0.stride()),
+                              g0.storage_offset()).add_(grad)
                 return
-        fresh = all(p.grad is None for p in params)
-        self._grad_stacks[name] = grad if fresh else None
         for p, v in zip(params, grad.unbind(0)):
             if not p.requires_grad:
                 continue

@@ -721,6 +721,34 @@ def _(fc1, grad_h, activation):
     return torch.empty_like(fc1)
 
 
+@torch.library.custom_op("ntmoe::backward_first_operand", mutates_args=())
+def backward_first_operand(grad_logits: Tensor, dfc1s: Optional[Tensor], Ep: int,
+                           Kc: int) -> Tensor:
+    """bf16 [T, Kc] rows [dfc1s | g_hi | g_hi | g_lo | 0], g = grad_logits split as
+    split_bf16 does, each g block Ep wide (columns past E zero); dfc1s bf16 [T, Fs] or None."""
+    _on_gpu(grad_logits, dfc1s)
+    _require(grad_logits.dtype == torch.float32 and grad_logits.dim() == 2
+             and grad_logits.is_contiguous(), "backward_first_operand: grad_logits must be "
+             "contiguous fp32 [T, E]")
+    T, E = grad_logits.shape
+    Fs = 0
+    if dfc1s is not None:
+        _require(dfc1s.dtype == torch.bfloat16 and dfc1s.dim() == 2 and dfc1s.shape[0] == T
+                 and dfc1s.is_contiguous(), "backward_first_operand: dfc1s must be contiguous "
+                 "bf16 [T, Fs]")
+        Fs = dfc1s.shape[1]
+    out = torch.empty(T, Kc, device=grad_logits.device, dtype=torch.bfloat16)
+    st = nat.load().nt_moe_backward_first_operand(ptr(grad_logits), E, ptr(dfc1s), Fs, T, Ep, Kc,
+                                                  ptr(out), _stream(grad_logits.device))
+    nat.check(st, "ntmoe::backward_first_operand")
+    return out
+
+
+@backward_first_operand.register_fake
+def _(grad_logits, dfc1s, Ep, Kc):
+    return grad_logits.new_empty(grad_logits.shape[0], Kc, dtype=torch.bfloat16)
+
+
 @torch.library.custom_op("ntmoe::router_bwd", mutates_args=())
 def router_bwd(logits: Tensor, ids: Tensor, weights: Tensor, grad_w: Tensor, counts: Tensor,
                score_fn: int, grad_aux: Optional[Tensor], aux_coeff: float,
@@ -971,18 +999,11 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
                          grad_aux, aux_coeff, z_coeff)
     # the token-side first row: [dfc1s | g_hi | g_hi | g_lo] . [W1s^T | Wr_hi | Wr_lo | Wr_hi]^T
     wf, (Fs, Ep, Kc) = bw.first(w_router_t)
-    g_hi, g_lo = split_bf16(dlogits)
-    a_cat = torch.zeros(T, Kc, device=x.device, dtype=torch.bfloat16)
-    if sh:
-        a_cat[:, :Fs] = dfc1s
-    a_cat[:, Fs:Fs + E] = g_hi
-    a_cat[:, Fs + Ep:Fs + Ep + E] = g_hi
-    a_cat[:, Fs + 2 * Ep:Fs + 2 * Ep + E] = g_lo
+    a_cat = backward_first_operand(dlogits, dfc1s, Ep, Kc)
     first = grouped_gemm(a_cat, None, seg, wf, nat.EPI_NONE, T)
-    # dWr = grad_logits^T x in fp32: [g_hi | g_lo]^T x (x exact in bf16), fp32 sums split along T
-    g_cat = torch.zeros(T, 2 * Ep, device=x.device, dtype=torch.bfloat16)
-    g_cat[:, :E] = g_hi
-    g_cat[:, Ep:Ep + E] = g_lo
+    # dWr = grad_logits^T x in fp32: [g_hi | g_lo]^T x (x exact in bf16), fp32 sums split along
+    # T; [g_hi | g_lo] are a_cat's last two blocks
+    g_cat = a_cat[:, Fs + Ep:Fs + 3 * Ep]
     wr = grouped_wgrad(g_cat, x, None, seg, T, wgrad_splits(1, 2 * Ep, d, T, x.device), True)[0]
     res["router"] = wr[:E] + wr[Ep:Ep + E]
     mark("router_bwd")

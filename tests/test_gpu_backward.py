@@ -400,3 +400,30 @@ def test_module_expert_gradients_accumulate_like_autograd():
     backward()
     assert params[experts[6]].grad is None
     assert torch.equal(params[experts[7]].grad, once[experts[7]])
+
+
+@pytest.mark.parametrize("E,Fs", [(40, 64), (256, 320), (8, 0)])
+def test_backward_first_operand_is_the_split_and_concatenation(E, Fs):
+    """[dfc1s | g_hi | g_hi | g_lo | 0] bit for bit against split_bf16 and torch slicing: E not a
+    multiple of the 32-wide blocks, values spanning exponents, exact bf16 values (lo = 0),
+    negative zero, no shared expert."""
+    from nexttransformer_amd import ops
+    gen = torch.Generator().manual_seed(E + Fs)
+    T = 333
+    Ep = (E + 31) // 32 * 32
+    Kc = (Fs + 3 * Ep + 63) // 64 * 64
+    g = torch.randn(T, E, generator=gen) * torch.exp2(torch.randint(-30, 30, (T, E),
+                                                                   generator=gen).float())
+    g[0] = g[0].to(torch.bfloat16).float()
+    g[1, :4] = torch.tensor([0.0, -0.0, 1.0, -3.5])
+    dfc1s = torch.randn(T, Fs, generator=gen).to(torch.bfloat16) if Fs else None
+    got = ops.backward_first_operand(g.cuda(), None if dfc1s is None else dfc1s.cuda(), Ep,
+                                     Kc).cpu()
+    hi, lo = ops.split_bf16(g)
+    want = torch.zeros(T, Kc, dtype=torch.bfloat16)
+    if Fs:
+        want[:, :Fs] = dfc1s
+    want[:, Fs:Fs + E] = hi
+    want[:, Fs + Ep:Fs + Ep + E] = hi
+    want[:, Fs + 2 * Ep:Fs + 2 * Ep + E] = lo
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
