@@ -59,6 +59,10 @@ def parse():
                         "0.323 vs 0.301 ms per forward)")
     p.add_argument("--train", action="store_true",
                    help="time forward + backward (bf16 configs) instead of the forward")
+    p.add_argument("--gemms", action="store_true",
+                   help="time the grouped GEMMs alone (bf16 configs) on the configuration's "
+                        "routing: packed weights (where the widths allow) and plain ones, up and "
+                        "down projection, --steps launches each; prints one JSON line")
     p.add_argument("--cpu-budget-s", type=float, default=30.0)
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 1 GiB device-to-device copy (known HBM bytes), used to "
@@ -403,6 +407,50 @@ def describe(case, cfg, permute_rows, fp8):
             "expert_weights": "fp8 e4m3 + block scales" if fp8 else "bf16"}
 
 
+def gemm_bench(args, case, cpu):
+    """Median launch time of each grouped GEMM of the layer on the configuration's routing."""
+    import torch
+    from nexttransformer_amd import _native as nat, ops
+    dev = torch.device("cuda")
+    x = cpu["x"].to(dev)
+    wt = cpu["router"].t().contiguous().to(dev)
+    bias = None if cpu["bias"] is None else cpu["bias"].to(dev)
+    _, ids, w, _, _ = ops.router(x, wt, bias, case.k, case.score_fn, False)
+    _, offsets, src, _, _, _, _ = ops.route_plan(ids, w, case.E, None, False)
+    A = case.T * case.k
+    up = nat.EPI_SWIGLU if case.activation == 0 else nat.EPI_RELU2
+    w1 = cpu["w1"].to(torch.bfloat16).to(dev)
+    w2 = cpu["w2"].to(torch.bfloat16).to(dev)
+    h = ops.grouped_gemm(x, src, offsets, w1, up, A)
+    F = w1.shape[1]
+    runs = {"plain_up": lambda: ops.grouped_gemm(x, src, offsets, w1, up, A),
+            "plain_down": lambda: ops.grouped_gemm(h, None, offsets, w2, nat.EPI_NONE, A)}
+    if ops.packable(case.d, F // 2 if up == nat.EPI_SWIGLU else F, up):
+        w1p = ops.pack_expert_weights(w1, up)
+        runs["packed_up"] = lambda: ops.grouped_gemm_packed(x, src, offsets, w1p, up, A)
+    if ops.packable(case.H, case.d, nat.EPI_NONE):
+        w2p = ops.pack_expert_weights(w2, nat.EPI_NONE)
+        runs["packed_down"] = lambda: ops.grouped_gemm_packed(h, None, offsets, w2p, nat.EPI_NONE, A)
+    flop = {"up": 2.0 * A * case.d * F, "down": 2.0 * A * case.H * case.d}
+    out = {"config": args.config, "launches": args.steps}
+    for name, fn in runs.items():
+        fn()
+        torch.cuda.synchronize()
+        evs = []
+        for _ in range(args.steps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            evs.append((a, b))
+        torch.cuda.synchronize()
+        ms = sorted(a.elapsed_time(b) for a, b in evs)[len(evs) // 2]
+        tf = flop[name.split("_")[1]] / (ms * 1e-3) / 1e12
+        out[name] = {"median_us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                     "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4)}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -422,6 +470,13 @@ def main():
     case = CONFIGS[args.config]
     fp8 = args.config == 5
     log(f"[bench] config {args.config}: {case}")
+    if args.gemms:
+        if fp8:
+            log("bench.py --gemms: bf16 configurations only")
+            sys.exit(2)
+        from tests.moe_cases import make_inputs
+        gemm_bench(args, case, make_inputs(case))
+        return
     cpu, g = gpu_inputs(case, fp8)
 
     def forward(mark=None):
