@@ -14,7 +14,9 @@ SwiGLU epilogue, 2/3 of the layer's FLOP). bf16 configs: bound "mfma", algorithm
 launch = 2 * (T k) * d * 2H. Config 5: bound "hbm", algorithmic bytes per launch = the e4m3
 weights and scales of the experts that received tokens + the quantised token rows once + h
 written. The average launch duration is measured with HIP events recorded on the launch stream
-around every launch inside the timed region. With --graph the timed forwards replay HIP graphs
+around the launches of every --event-every-th forward (default 8) inside the timed region: an
+event record writes back the L2 of every XCD and idles the stream for about 6 us, so events
+around every launch would add 12 us to every step. With --graph the timed forwards replay HIP graphs
 captured from the forward (three segments, so the events sit between replays), and the replays'
 output is checked bit for bit against an eager forward. `traffic` (HBM bytes per launch) comes from the
 rocprofv3 FETCH_SIZE / WRITE_SIZE summary in profiles/traffic.json, when present.
@@ -42,10 +44,63 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+class DeviceEvent:
+    """A HIP timing event recorded with a device-scope release (hipEventReleaseToDevice).
+    torch.cuda.Event's record releases to system scope: the L2 is written back and invalidated
+    at every record, which idles the GPU for about 6 us between the kernels the event separates
+    and starts the next kernel on a cold L2. The events here only time work on this GPU."""
+    _hip = None
+    _RELEASE_TO_DEVICE = 0x40000000
+
+    @classmethod
+    def _lib(cls):
+        if cls._hip is None:
+            import ctypes
+            import torch
+            torch.cuda.init()
+            # the HIP runtime torch loaded (the native library binds to the same one)
+            with open("/proc/self/maps") as f:
+                path = next(line.split()[-1] for line in f if "libamdhip64" in line)
+            lib = ctypes.CDLL(path)
+            vp = ctypes.c_void_p
+            lib.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(vp), ctypes.c_uint]
+            lib.hipEventRecord.argtypes = [vp, vp]
+            lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+            cls._hip = lib
+        return cls._hip
+
+    def __init__(self):
+        import ctypes
+        self._ctypes = ctypes
+        self.ev = ctypes.c_void_p()
+        rc = self._lib().hipEventCreateWithFlags(ctypes.byref(self.ev), self._RELEASE_TO_DEVICE)
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags failed: {rc}")
+
+    def record(self, stream=None):
+        import torch
+        stream = stream if stream is not None else torch.cuda.current_stream()
+        rc = self._lib().hipEventRecord(self.ev, self._ctypes.c_void_p(stream.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed: {rc}")
+
+    def elapsed_time(self, end):
+        ms = self._ctypes.c_float()
+        rc = self._lib().hipEventElapsedTime(self._ctypes.byref(ms), self.ev, end.ev)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed: {rc}")
+        return ms.value
+    # (no destructor: the few events of a run live until the process ends, and destroying them
+    # during interpreter shutdown could run after the HIP runtime is gone)
+
+
 def parse():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--event-every", type=int, default=8,
+                   help="time the up-projection launch with HIP events in every N-th timed "
+                        "forward (each event record idles the stream about 6 us)")
     p.add_argument("--warmup", type=int, default=50)
     p.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6],
                    help="1-5: the benchmark configurations; 6: the registered T3 expert cell "
@@ -78,7 +133,7 @@ def calibrate_copy(reps=20, nbytes=1 << 30):
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a, b = DeviceEvent(), DeviceEvent()
     a.record()
     for _ in range(reps):
         dst.copy_(src)
@@ -183,11 +238,11 @@ def train_bench(args, case, cpu, g):
     stream = torch.cuda.current_stream()
     stage, reps, kept = {}, 5, None
     for _ in range(reps):
-        evs = [("start", torch.cuda.Event(enable_timing=True))]
+        evs = [("start", DeviceEvent())]
         evs[0][1].record(stream)
 
         def mark(name):
-            e = torch.cuda.Event(enable_timing=True)
+            e = DeviceEvent()
             e.record(stream)
             evs.append((name, e))
         _, _, st = ops.moe_forward(x, w["router_t"], w["w1"], w["w2"], top_k=case.k,
@@ -438,7 +493,7 @@ def gemm_bench(args, case, cpu):
         torch.cuda.synchronize()
         evs = []
         for _ in range(args.steps):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a, b = DeviceEvent(), DeviceEvent()
             a.record()
             fn()
             b.record()
@@ -501,34 +556,44 @@ def main():
     log(f"[bench] warm-up done ({args.warmup} steps); expert load max/mean {load_ratio:.2f}")
 
     # Timed region: K full forwards, every kernel launched from Python, with HIP events recorded
-    # on the launch stream around every up-projection launch. With --graph each forward instead
-    # replays three HIP graphs captured from it (routing, the up-projection GEMM, the rest), the
-    # events recorded between the replays.
+    # on the launch stream around the up-projection launch of every --event-every-th forward
+    # (an event record releases the memory model's device scope, which on this GPU writes back
+    # the L2 of every XCD and idles the stream about 6 us; recording around every launch would
+    # add 12 us to every step). With --graph each forward instead replays three HIP graphs
+    # captured from it (routing, the up-projection GEMM, the rest), the events recorded between
+    # the replays of the sampled forwards.
     before_up = "quantize" if fp8 else "route_plan"
     stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.steps)]
+    every = max(1, args.event_every)
+    sampled = list(range(0, args.steps, every))
+    ev = {i: (DeviceEvent(), DeviceEvent()) for i in sampled}
     graphs = capture_segments(forward, (before_up, "gemm_up")) if args.graph else None
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
+        pair = ev.get(i)
         if graphs is None:
-            def mark(name, i=i):
-                if name == before_up:
-                    ev[i][0].record(stream)
-                elif name == "gemm_up":
-                    ev[i][1].record(stream)
-            forward(mark)
+            if pair is None:
+                forward()
+            else:
+                def mark(name, pair=pair):
+                    if name == before_up:
+                        pair[0].record(stream)
+                    elif name == "gemm_up":
+                        pair[1].record(stream)
+                forward(mark)
         else:
             graphs[0].replay()
-            ev[i][0].record(stream)
+            if pair is not None:
+                pair[0].record(stream)
             graphs[1].replay()
-            ev[i][1].record(stream)
+            if pair is not None:
+                pair[1].record(stream)
             graphs[2].replay()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms = (t1 - t0) * 1e3 / args.steps
-    up_ms = sum(a.elapsed_time(b) for a, b in ev) / args.steps
+    up_ms = sum(a.elapsed_time(b) for a, b in ev.values()) / len(ev)
     log(f"[bench] timed {args.steps} steps ({'eager' if graphs is None else 'graph replay'}): "
         f"{ms:.4f} ms/step, gemm_up {up_ms:.4f} ms")
     replay_ok = None
@@ -545,11 +610,11 @@ def main():
     reps = 10
     stage = {}
     for _ in range(reps):
-        evs = [("start", torch.cuda.Event(enable_timing=True))]
+        evs = [("start", DeviceEvent())]
         evs[0][1].record(stream)
 
         def mark(name):
-            e = torch.cuda.Event(enable_timing=True)
+            e = DeviceEvent()
             e.record(stream)
             evs.append((name, e))
         forward(mark)
@@ -570,7 +635,7 @@ def main():
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                     "traffic": load_traffic(f"config{args.config}"),
                     "bytes_per_launch": up_bytes, "experts_touched": touched,
-                    "avg_launch_ms": round(up_ms, 5)}
+                    "avg_launch_ms": round(up_ms, 5), "launches_timed": len(ev)}
     else:
         up_flop = 2.0 * A * case.d * F
         achieved = up_flop / (up_ms * 1e-3) / 1e12
@@ -584,7 +649,8 @@ def main():
                     "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                     "traffic": load_traffic(f"config{args.config}"),
-                    "flop_per_launch": up_flop, "avg_launch_ms": round(up_ms, 5)}
+                    "flop_per_launch": up_flop, "avg_launch_ms": round(up_ms, 5),
+                    "launches_timed": len(ev)}
     result = {
         "metric": METRIC,
         "value": round(case.T / (ms * 1e-3), 1),

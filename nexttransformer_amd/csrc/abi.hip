@@ -11,6 +11,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <unordered_map>
 
 #include "common.h"
 
@@ -101,9 +102,22 @@ int num_cus() {
   return n;
 }
 
+// Raises a kernel's dynamic-LDS limit once per (device, kernel) to the largest size asked for so
+// far: hipFuncSetAttribute on every launch stalled the stream for about 6 us before each
+// large-LDS kernel.
 hipError_t allow_dynamic_lds(const void* kernel, size_t bytes) {
   if (bytes <= 65536) return hipSuccess;
-  return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  static std::mutex mu;
+  static std::unordered_map<const void*, size_t> granted[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = granted[dev].find(kernel);
+  if (it != granted[dev].end() && it->second >= bytes) return hipSuccess;
+  hipError_t err =
+      hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (err == hipSuccess) granted[dev][kernel] = bytes;
+  return err;
 }
 
 }  // namespace ntmoe
