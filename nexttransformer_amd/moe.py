@@ -400,17 +400,17 @@ class MoELayer(nn.Module):
                 if not fp8 and hp == hidden and dp == r.width and self.router.weight.is_cuda:
                     # one pass over the fp32 masters: the bf16 copy (and, for the backward, its
                     # transpose)
-                    w1, w1t = ops.convert_expert_weights(
+                    w1, w1t = ops.convert_expert_weights.raw(
                         _stacked(pools[0], [e.linear_fc1.weight for e in experts]), True,
                         keep_plain)
-                    w2, w2t = ops.convert_expert_weights(
+                    w2, w2t = ops.convert_expert_weights.raw(
                         _stacked(pools[1], [e.linear_fc2.weight for e in experts]), True,
                         keep_plain)
                     plain.append((w1, w2, w1t if keep_plain else None,
                                   w2t if keep_plain else None))
                     up = nat.EPI_SWIGLU if gated else nat.EPI_RELU2
-                    return (ops.pack_expert_weights(w1, up) if pk_up else w1, None,
-                            ops.pack_expert_weights(w2, nat.EPI_NONE) if pk_down else w2, None)
+                    return (ops.pack_expert_weights.raw(w1, up) if pk_up else w1, None,
+                            ops.pack_expert_weights.raw(w2, nat.EPI_NONE) if pk_down else w2, None)
                 if hp == hidden and dp == r.width:
                     w1 = torch.stack([e.linear_fc1.weight.detach() for e in experts]).to(dtype)
                     w2 = torch.stack([e.linear_fc2.weight.detach() for e in experts]).to(dtype)
@@ -431,8 +431,8 @@ class MoELayer(nn.Module):
                     up = nat.EPI_SWIGLU if gated else nat.EPI_RELU2
                     w1, w2 = w1.contiguous(), w2.contiguous()
                     plain.append((w1, w2, None, None))
-                    return (ops.pack_expert_weights(w1, up) if pk_up else w1, None,
-                            ops.pack_expert_weights(w2, nat.EPI_NONE) if pk_down else w2, None)
+                    return (ops.pack_expert_weights.raw(w1, up) if pk_up else w1, None,
+                            ops.pack_expert_weights.raw(w2, nat.EPI_NONE) if pk_down else w2, None)
                 w1q, w1s = ops.quantize_fp8_blockwise(w1.contiguous())
                 w2q, w2s = ops.quantize_fp8_blockwise(w2.contiguous())
                 up = nat.EPI_SWIGLU if gated else nat.EPI_RELU2

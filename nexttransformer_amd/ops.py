@@ -36,10 +36,22 @@ def _nblk(T):
     return (T + nat.ROUTE_BLOCK - 1) // nat.ROUTE_BLOCK
 
 
+def _custom_op(name):
+    """torch.library.custom_op(name) that keeps the undecorated function as `.raw`. The layer's
+    own forward, backward and weight rebuild (moe_forward, moe_backward, Projection, the module)
+    call `.raw`: the dispatcher's per-call host cost (about 20 us) is more than some of the
+    kernels take, and with a dozen calls per training step it left the GPU waiting on the host."""
+    def deco(fn):
+        op = torch.library.custom_op(name, mutates_args=())(fn)
+        op.raw = fn
+        return op
+    return deco
+
+
 # ---------------------------------------------------------------------------------------------
 # router
 
-@torch.library.custom_op("ntmoe::router", mutates_args=())
+@_custom_op("ntmoe::router")
 def router(x: Tensor, w_router_t: Tensor, bias: Optional[Tensor], k: int, score_fn: int,
            want_logits: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """(logits [T,E] or empty, ids [T,k] int32, weights [T,k], prob_partial, z_partial)."""
@@ -79,7 +91,7 @@ def _(x, w_router_t, bias, k, score_fn, want_logits):
             f((_nblk(T), E), dtype=torch.float32), f((_nblk(T),), dtype=torch.float32))
 
 
-@torch.library.custom_op("ntmoe::topk_from_logits", mutates_args=())
+@_custom_op("ntmoe::topk_from_logits")
 def topk_from_logits(logits: Tensor, k: int, score_fn: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """Top-k / weights / aux partials from given fp32 logits [T, E]."""
     _on_gpu(logits)
@@ -108,7 +120,7 @@ def _(logits, k, score_fn):
 # ---------------------------------------------------------------------------------------------
 # route plan: histogram + scan + permute
 
-@torch.library.custom_op("ntmoe::route_plan", mutates_args=())
+@_custom_op("ntmoe::route_plan")
 def route_plan(ids: Tensor, weights: Tensor, num_experts: int, x: Optional[Tensor],
                want_x_perm: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """(counts [E], offsets [E+1], src_row [A], perm_w [A], combine_dest [T,k], combine_w [T,k],
@@ -161,7 +173,7 @@ def _(ids, weights, num_experts, x, want_x_perm):
 # ---------------------------------------------------------------------------------------------
 # grouped expert FFN
 
-@torch.library.custom_op("ntmoe::grouped_ffn", mutates_args=())
+@_custom_op("ntmoe::grouped_ffn")
 def grouped_ffn(a: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor, w1: Tensor,
                 w2: Tensor, activation: int, total_rows: int) -> tuple[Tensor, Tensor]:
     """(h [rows, H], y [rows, d]) for ragged segments; rows read a[src_row[r]] if given."""
@@ -200,7 +212,7 @@ def _(a, src_row, seg_offsets, w1, w2, activation, total_rows):
     return (a.new_empty((total_rows, H)), a.new_empty((total_rows, d)))
 
 
-@torch.library.custom_op("ntmoe::grouped_gemm", mutates_args=())
+@_custom_op("ntmoe::grouped_gemm")
 def grouped_gemm(a: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor, w: Tensor,
                  epilogue: int, total_rows: int) -> Tensor:
     """One grouped GEMM launch: c [rows, n_out] = epilogue(a_r . w_s^T) per ragged segment."""
@@ -240,7 +252,7 @@ def plain_keep_supported(K, n_out):
     return K >= 128 and n_out % 8 == 0
 
 
-@torch.library.custom_op("ntmoe::grouped_gemm_keep", mutates_args=())
+@_custom_op("ntmoe::grouped_gemm_keep")
 def grouped_gemm_keep(a: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor, w: Tensor,
                       epilogue: int, total_rows: int) -> tuple[Tensor, Tensor]:
     """(c, pre): grouped_gemm with the SwiGLU / ReLU^2 epilogue, plus the epilogue's input (the
@@ -276,7 +288,7 @@ def _(a, src_row, seg_offsets, w, epilogue, total_rows):
     return (a.new_empty(total_rows, n_out), a.new_empty(total_rows, rows))
 
 
-@torch.library.custom_op("ntmoe::pack_expert_weights", mutates_args=())
+@_custom_op("ntmoe::pack_expert_weights")
 def pack_expert_weights(w: Tensor, epilogue: int) -> Tensor:
     """Expert weights [S, rows, K] bf16 rearranged for grouped_gemm_packed (same size)."""
     _on_gpu(w)
@@ -295,7 +307,7 @@ def _(w, epilogue):
     return torch.empty_like(w)
 
 
-@torch.library.custom_op("ntmoe::convert_expert_weights", mutates_args=())
+@_custom_op("ntmoe::convert_expert_weights")
 def convert_expert_weights(w: Tensor, want_out: bool, want_t: bool) -> tuple[Tensor, Tensor]:
     """fp32 [S, R, K] -> (bf16 [S, R, K] or empty, bf16 [S, K, R] or empty), one read of w."""
     _on_gpu(w)
@@ -324,7 +336,7 @@ def packable(K, n_out, epilogue):
     return K >= 256 and K % 128 == 0 and n_out % (16 if epilogue == nat.EPI_SWIGLU else 32) == 0
 
 
-@torch.library.custom_op("ntmoe::grouped_gemm_packed", mutates_args=())
+@_custom_op("ntmoe::grouped_gemm_packed")
 def grouped_gemm_packed(a: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor,
                         w_packed: Tensor, epilogue: int, total_rows: int) -> Tensor:
     """grouped_gemm on weights packed by pack_expert_weights with the same epilogue."""
@@ -355,7 +367,7 @@ def _(a, src_row, seg_offsets, w_packed, epilogue, total_rows):
     return a.new_empty((total_rows, rows // 2 if epilogue == nat.EPI_SWIGLU else rows))
 
 
-@torch.library.custom_op("ntmoe::grouped_gemm_packed_keep", mutates_args=())
+@_custom_op("ntmoe::grouped_gemm_packed_keep")
 def grouped_gemm_packed_keep(a: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor,
                              w_packed: Tensor, epilogue: int,
                              total_rows: int) -> tuple[Tensor, Tensor]:
@@ -396,7 +408,7 @@ def _(a, src_row, seg_offsets, w_packed, epilogue, total_rows):
 # ---------------------------------------------------------------------------------------------
 # fp8 (OCP e4m3fn bytes held in uint8 tensors)
 
-@torch.library.custom_op("ntmoe::quantize_fp8_rowwise", mutates_args=())
+@_custom_op("ntmoe::quantize_fp8_rowwise")
 def quantize_fp8_rowwise(x: Tensor) -> tuple[Tensor, Tensor]:
     """(q uint8 [rows, d] e4m3 codes, scale fp32 [rows]) with s = amax / 448 per row."""
     _on_gpu(x)
@@ -419,7 +431,7 @@ def _(x):
     return (x.new_empty((rows, d), dtype=torch.uint8), x.new_empty((rows,), dtype=torch.float32))
 
 
-@torch.library.custom_op("ntmoe::quantize_fp8_blockwise", mutates_args=())
+@_custom_op("ntmoe::quantize_fp8_blockwise")
 def quantize_fp8_blockwise(w: Tensor) -> tuple[Tensor, Tensor]:
     """(q uint8 [S, R, C] e4m3 codes, scale fp32 [S, R/128, C/128]) of fp32 w [S, R, C]."""
     _on_gpu(w)
@@ -441,7 +453,7 @@ def _(w):
             w.new_empty((S, R // 128, C // 128), dtype=torch.float32))
 
 
-@torch.library.custom_op("ntmoe::pack_expert_weights_fp8", mutates_args=())
+@_custom_op("ntmoe::pack_expert_weights_fp8")
 def pack_expert_weights_fp8(w: Tensor, epilogue: int) -> Tensor:
     """e4m3 expert weights [S, rows, K] (uint8) rearranged for grouped_gemm_fp8(packed=True)."""
     _on_gpu(w)
@@ -460,7 +472,7 @@ def _(w, epilogue):
     return torch.empty_like(w)
 
 
-@torch.library.custom_op("ntmoe::grouped_gemm_fp8", mutates_args=())
+@_custom_op("ntmoe::grouped_gemm_fp8")
 def grouped_gemm_fp8(a: Tensor, a_scale: Tensor, src_row: Optional[Tensor], seg_offsets: Tensor,
                      w: Tensor, w_scale: Tensor, epilogue: int, total_rows: int,
                      packed: bool = False) -> Tensor:
@@ -502,7 +514,7 @@ def _(a, a_scale, src_row, seg_offsets, w, w_scale, epilogue, total_rows, packed
 # ---------------------------------------------------------------------------------------------
 # combine + aux
 
-@torch.library.custom_op("ntmoe::combine_aux", mutates_args=())
+@_custom_op("ntmoe::combine_aux")
 def combine_aux(y: Tensor, combine_dest: Tensor, combine_w: Tensor, shared_y: Optional[Tensor],
                 prob_partial: Tensor, z_partial: Tensor, counts: Tensor, aux_coeff: float,
                 z_coeff: float) -> tuple[Tensor, Tensor]:
@@ -595,9 +607,9 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
                      perm_w=empty(0, dtype=f32), combine_dest=empty(0, top_k),
                      combine_w=empty(0, top_k, dtype=f32))
         return x.new_empty(0, x.shape[1]), torch.zeros(3, device=dev, dtype=f32), state
-    logits, ids, w, pp, zp = router(x, w_router_t, logit_bias, top_k, score_fn, want_logits)
+    logits, ids, w, pp, zp = router.raw(x, w_router_t, logit_bias, top_k, score_fn, want_logits)
     mark("router")
-    counts, offsets, src, perm_w, cdest, cw, x_perm = route_plan(
+    counts, offsets, src, perm_w, cdest, cw, x_perm = route_plan.raw(
         ids, w, E, x if permute_rows else None, permute_rows)
     mark("route_plan")
     up_epi = nat.EPI_SWIGLU if activation == nat.ACT_SWIGLU else nat.EPI_RELU2
@@ -605,40 +617,40 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
         _require(w1_scale is not None and w2_scale is not None,
                  "moe_forward: fp8 weights need w1_scale and w2_scale")
         _require(isinstance(packed, bool), "moe_forward: fp8 weights take packed=True or False")
-        xq, xs = quantize_fp8_rowwise(x)
+        xq, xs = quantize_fp8_rowwise.raw(x)
         mark("quantize")
-        h = grouped_gemm_fp8(xq, xs, src, offsets, w1, w1_scale, up_epi, A, packed)
+        h = grouped_gemm_fp8.raw(xq, xs, src, offsets, w1, w1_scale, up_epi, A, packed)
         mark("gemm_up")
-        hq, hs = quantize_fp8_rowwise(h)
-        y = grouped_gemm_fp8(hq, hs, None, offsets, w2, w2_scale, nat.EPI_NONE, A, packed)
+        hq, hs = quantize_fp8_rowwise.raw(h)
+        y = grouped_gemm_fp8.raw(hq, hs, None, offsets, w2, w2_scale, nat.EPI_NONE, A, packed)
         mark("gemm_down")
         shared_y = None
         if shared_w1 is not None:
             seg = _whole_batch_segment(T, x.device)
-            hs_ = grouped_gemm_fp8(xq, xs, None, seg, shared_w1, shared_w1_scale, up_epi, T,
+            hs_ = grouped_gemm_fp8.raw(xq, xs, None, seg, shared_w1, shared_w1_scale, up_epi, T,
                                    packed)
-            hsq, hss = quantize_fp8_rowwise(hs_)
-            shared_y = grouped_gemm_fp8(hsq, hss, None, seg, shared_w2, shared_w2_scale,
+            hsq, hss = quantize_fp8_rowwise.raw(hs_)
+            shared_y = grouped_gemm_fp8.raw(hsq, hss, None, seg, shared_w2, shared_w2_scale,
                                         nat.EPI_NONE, T, packed)
             mark("shared")
-        out, aux = combine_aux(y, cdest, cw, shared_y, pp, zp, counts, aux_coeff, z_coeff)
+        out, aux = combine_aux.raw(y, cdest, cw, shared_y, pp, zp, counts, aux_coeff, z_coeff)
         mark("combine")
         state = dict(logits=logits, ids=ids, weights=w, counts=counts, offsets=offsets,
                      src_row=src, perm_w=perm_w, combine_dest=cdest, combine_w=cw, x_q=xq,
                      x_scale=xs)
         return out, aux, state
     packed_up, packed_down = (packed, packed) if isinstance(packed, bool) else packed
-    gemm_up = grouped_gemm_packed if packed_up else grouped_gemm
-    gemm_down = grouped_gemm_packed if packed_down else grouped_gemm
+    gemm_up = grouped_gemm_packed.raw if packed_up else grouped_gemm.raw
+    gemm_down = grouped_gemm_packed.raw if packed_down else grouped_gemm.raw
 
     def up(a, rows_src, offs, w, rows):
         """The up projection; with keep, also the backward's fc1 pre-activations from the same
         launch where the kernel can store them (else None: the backward recomputes them)."""
         if keep and packed_up:
-            return grouped_gemm_packed_keep(a, rows_src, offs, w, up_epi, rows)
+            return grouped_gemm_packed_keep.raw(a, rows_src, offs, w, up_epi, rows)
         if keep and plain_keep_supported(
                 w.shape[2], w.shape[1] // 2 if up_epi == nat.EPI_SWIGLU else w.shape[1]):
-            return grouped_gemm_keep(a, rows_src, offs, w, up_epi, rows)
+            return grouped_gemm_keep.raw(a, rows_src, offs, w, up_epi, rows)
         return gemm_up(a, rows_src, offs, w, up_epi, rows), None
 
     if permute_rows:
@@ -654,7 +666,7 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
         hs, fc1s = up(x, None, seg, shared_w1, T)
         shared_y = gemm_down(hs, None, seg, shared_w2, nat.EPI_NONE, T)
         mark("shared")
-    out, aux = combine_aux(y, cdest, cw, shared_y, pp, zp, counts, aux_coeff, z_coeff)
+    out, aux = combine_aux.raw(y, cdest, cw, shared_y, pp, zp, counts, aux_coeff, z_coeff)
     mark("combine")
     state = dict(logits=logits, ids=ids, weights=w, counts=counts, offsets=offsets, src_row=src,
                  perm_w=perm_w, combine_dest=cdest, combine_w=cw)
@@ -667,7 +679,7 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
 # ---------------------------------------------------------------------------------------------
 # backward (bf16 experts)
 
-@torch.library.custom_op("ntmoe::combine_bwd", mutates_args=())
+@_custom_op("ntmoe::combine_bwd")
 def combine_bwd(grad_out: Tensor, y: Tensor, ids: Tensor, combine_dest: Tensor,
                 combine_w: Tensor) -> tuple[Tensor, Tensor]:
     """(grad_y bf16 [T*k, d] expert-major, grad_w fp32 [T, k] in top-k slot order)."""
@@ -699,7 +711,7 @@ def _(grad_out, y, ids, combine_dest, combine_w):
             y.new_empty((T, k), dtype=torch.float32))
 
 
-@torch.library.custom_op("ntmoe::act_bwd", mutates_args=())
+@_custom_op("ntmoe::act_bwd")
 def act_bwd(fc1: Tensor, grad_h: Tensor, activation: int) -> Tensor:
     """grad of the fc1 pre-activations [rows, F] from grad_h [rows, H]."""
     _on_gpu(fc1, grad_h)
@@ -721,7 +733,7 @@ def _(fc1, grad_h, activation):
     return torch.empty_like(fc1)
 
 
-@torch.library.custom_op("ntmoe::backward_first_operand", mutates_args=())
+@_custom_op("ntmoe::backward_first_operand")
 def backward_first_operand(grad_logits: Tensor, dfc1s: Optional[Tensor], Ep: int,
                            Kc: int) -> Tensor:
     """bf16 [T, Kc] rows [dfc1s | g_hi | g_hi | g_lo | 0], g = grad_logits split as
@@ -749,7 +761,7 @@ def _(grad_logits, dfc1s, Ep, Kc):
     return grad_logits.new_empty(grad_logits.shape[0], Kc, dtype=torch.bfloat16)
 
 
-@torch.library.custom_op("ntmoe::router_bwd", mutates_args=())
+@_custom_op("ntmoe::router_bwd")
 def router_bwd(logits: Tensor, ids: Tensor, weights: Tensor, grad_w: Tensor, counts: Tensor,
                score_fn: int, grad_aux: Optional[Tensor], aux_coeff: float,
                z_coeff: float) -> Tensor:
@@ -782,7 +794,7 @@ def _(logits, ids, weights, grad_w, counts, score_fn, grad_aux, aux_coeff, z_coe
     return torch.empty_like(logits)
 
 
-@torch.library.custom_op("ntmoe::grouped_wgrad", mutates_args=())
+@_custom_op("ntmoe::grouped_wgrad")
 def grouped_wgrad(a: Tensor, b: Tensor, b_src_row: Optional[Tensor], seg_offsets: Tensor,
                   total_rows: int, splits: int = 1, out_fp32: bool = False) -> Tensor:
     """c [S, N, M]: c[s] = sum over segment s's rows r of a[r]^T b[row(r)], bf16 (or fp32 with
@@ -851,10 +863,10 @@ class Projection:
     def __init__(self, w):
         S, n, K = w.shape
         self.packed = packable(K, n, nat.EPI_NONE)
-        self.w = pack_expert_weights(w.contiguous(), nat.EPI_NONE) if self.packed else w.contiguous()
+        self.w = pack_expert_weights.raw(w.contiguous(), nat.EPI_NONE) if self.packed else w.contiguous()
 
     def __call__(self, a, src_row, seg_offsets, total_rows):
-        gemm = grouped_gemm_packed if self.packed else grouped_gemm
+        gemm = grouped_gemm_packed.raw if self.packed else grouped_gemm.raw
         return gemm(a, src_row, seg_offsets, self.w, nat.EPI_NONE, total_rows)
 
 
@@ -976,11 +988,11 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
     if fc1 is None:  # not kept by the forward: recompute the pre-activations
         fc1 = bw.w1(x, src, offsets, A)
     mark("fc1_recompute")
-    gy, gw = combine_bwd(g, state["y"], ids, cdest, state["combine_w"])
+    gy, gw = combine_bwd.raw(g, state["y"], ids, cdest, state["combine_w"])
     mark("combine_bwd")
     dh = bw.w2t(gy, None, offsets, A)
     mark("dgrad_down")
-    dfc1 = act_bwd(fc1, dh, activation)
+    dfc1 = act_bwd.raw(fc1, dh, activation)
     mark("act_bwd")
     dxp = bw.w1t(dfc1, None, offsets, A)
     mark("dgrad_up")
@@ -993,34 +1005,34 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
         if fc1s is None:  # not kept by the forward
             fc1s = bw.shared_w1_proj(x, None, seg, T)
         dhs = sb["w2t"](g, None, seg, T)
-        dfc1s = act_bwd(fc1s, dhs, activation)
+        dfc1s = act_bwd.raw(fc1s, dhs, activation)
         mark("shared")
-    dlogits = router_bwd(state["logits"], ids, state["weights"], gw, state["counts"], score_fn,
+    dlogits = router_bwd.raw(state["logits"], ids, state["weights"], gw, state["counts"], score_fn,
                          grad_aux, aux_coeff, z_coeff)
     # the token-side first row: [dfc1s | g_hi | g_hi | g_lo] . [W1s^T | Wr_hi | Wr_lo | Wr_hi]^T
     wf, (Fs, Ep, Kc) = bw.first(w_router_t)
-    a_cat = backward_first_operand(dlogits, dfc1s, Ep, Kc)
-    first = grouped_gemm(a_cat, None, seg, wf, nat.EPI_NONE, T)
+    a_cat = backward_first_operand.raw(dlogits, dfc1s, Ep, Kc)
+    first = grouped_gemm.raw(a_cat, None, seg, wf, nat.EPI_NONE, T)
     # dWr = grad_logits^T x in fp32: [g_hi | g_lo]^T x (x exact in bf16), fp32 sums split along
     # T; [g_hi | g_lo] are a_cat's last two blocks
     g_cat = a_cat[:, Fs + Ep:Fs + 3 * Ep]
-    wr = grouped_wgrad(g_cat, x, None, seg, T, wgrad_splits(1, 2 * Ep, d, T, x.device), True)[0]
+    wr = grouped_wgrad.raw(g_cat, x, None, seg, T, wgrad_splits(1, 2 * Ep, d, T, x.device), True)[0]
     res["router"] = wr[:E] + wr[Ep:Ep + E]
     mark("router_bwd")
     ones = torch.ones(T, k, device=x.device, dtype=torch.float32)
-    res["x"], _ = combine_aux(dxp, cdest, ones, first, state["prob_partial"],
+    res["x"], _ = combine_aux.raw(dxp, cdest, ones, first, state["prob_partial"],
                               state["z_partial"], state["counts"], 0.0, 0.0)
     mark("dx_sum")
     # expert weight gradients over each expert's rows; the shared expert's over all T rows
     f32 = weight_grads_fp32
-    res["w1"] = grouped_wgrad(dfc1, x, src, offsets, A, wgrad_splits(E, dfc1.shape[1], d, A // E,
+    res["w1"] = grouped_wgrad.raw(dfc1, x, src, offsets, A, wgrad_splits(E, dfc1.shape[1], d, A // E,
                                                                      x.device), f32)
-    res["w2"] = grouped_wgrad(gy, state["h"], None, offsets, A,
+    res["w2"] = grouped_wgrad.raw(gy, state["h"], None, offsets, A,
                               wgrad_splits(E, d, state["h"].shape[1], A // E, x.device), f32)
     if sh:
-        res["shared_w1"] = grouped_wgrad(dfc1s, x, None, seg, T,
+        res["shared_w1"] = grouped_wgrad.raw(dfc1s, x, None, seg, T,
                                          wgrad_splits(1, dfc1s.shape[1], d, T, x.device), f32)
-        res["shared_w2"] = grouped_wgrad(g, state["shared_h"], None, seg, T,
+        res["shared_w2"] = grouped_wgrad.raw(g, state["shared_h"], None, seg, T,
                                          wgrad_splits(1, d, state["shared_h"].shape[1], T,
                                                       x.device), f32)
     mark("wgrad")
