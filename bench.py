@@ -359,8 +359,9 @@ def gpu_inputs(case, fp8):
             names[1].append("shared_w2")
         pk = []
         for group, e in zip(names, (up, nat.EPI_NONE)):
-            ok = all(ops.packable(g[n].shape[2], g[n].shape[1] // (2 if e == nat.EPI_SWIGLU else 1),
-                                  e) for n in group)
+            ok = all(ops.prefers_packed(g[n].shape[2],
+                                        g[n].shape[1] // (2 if e == nat.EPI_SWIGLU else 1), e)
+                     for n in group)
             if ok:
                 for n in group:
                     g[n] = ops.pack_expert_weights(g[n], e)

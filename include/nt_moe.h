@@ -247,7 +247,7 @@ int nt_moe_convert_expert_weights(const float* w, int64_t num_matrices, int32_t 
  * the expert loop it replaces (megatron_moe.py:145).
  *   pack:  w bf16 [num_segments, rows, K] -> packed bf16 [num_segments, rows, K] (same size)
  *          rows % 32 == 0 (rows = 2 n_out for SWIGLU), K % 64 == 0
- *   gemm:  as nt_moe_grouped_gemm_bf16 with w = packed weights; K % 128 == 0 and K >= 256;
+ *   gemm:  as nt_moe_grouped_gemm_bf16 with w = packed weights; K % 64 == 0 and K >= 256;
  *          n_out % 16 == 0 (SWIGLU) or % 32; total_rows * n_out * 2 < 2^31; a, w_packed and
  *          c 16-byte aligned.
  */

@@ -614,8 +614,8 @@ static int check_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows, const i
                         const int32_t* seg_offsets, int32_t num_segments, int64_t total_rows,
                         const uint16_t* w_packed, int32_t K, int32_t n_out, int32_t epilogue,
                         uint16_t* c) {
-  NT_REQUIRE(K >= packed_gemm_min_k() && K % 128 == 0,
-             "grouped_gemm_packed: K must be a multiple of 128 and >= %d, got %d",
+  NT_REQUIRE(K >= packed_gemm_min_k() && K % 64 == 0,
+             "grouped_gemm_packed: K must be a multiple of 64 and >= %d, got %d",
              packed_gemm_min_k(), K);
   NT_REQUIRE(epilogue == NT_MOE_EPI_SWIGLU || epilogue == NT_MOE_EPI_RELU2 ||
                  epilogue == NT_MOE_EPI_NONE, "grouped_gemm_packed: unknown epilogue %d", epilogue);

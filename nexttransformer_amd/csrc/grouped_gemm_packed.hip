@@ -37,7 +37,9 @@
 // outstanding vector memory operations (loads and stores retire in order on this GPU family):
 // the even step issues B(g + 1) (weights, registers), then A(g + 2) and A(g + 3) (token rows,
 // LDS, each with one gather-index load); the odd step issues B(g + 2); at the end of a tile the
-// epilogue's fixed number of stores follow.
+// epilogue's fixed number of stores follow. An odd K-step count (K = 320: 5 steps) runs one
+// more odd step per tile that re-reads the last stage and weights but multiplies nothing, so
+// tiles stay whole pairs at the cost of a sixth of the loads.
 #include <math.h>
 #include <stdlib.h>
 #include <type_traits>
@@ -119,7 +121,10 @@ struct Tile {
 
 // KEEP: also store the epilogue's input (the fc1 pre-activations: SwiGLU gate then value, 2 n_out
 // wide, or the ReLU^2 input, n_out wide) to Pre, for a backward pass.
-template <int EPI, bool GATHER, int WAVES, bool KEEP = false>
+// EDGE: shapes with an odd K-step count or a partial last N tile (the extra step, waves that
+// multiply nothing). Without it the kernel holds neither, so the common shapes' code stays small
+// enough for the instruction cache (both together double it).
+template <int EPI, bool GATHER, int WAVES, bool KEEP = false, bool EDGE = false>
 __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
     const uint16_t* __restrict__ A, int64_t ld_a, const int32_t* __restrict__ src_row,
     const int32_t* __restrict__ seg_offsets, int S, int total_rows, int64_t a_rows,
@@ -139,7 +144,11 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
   const int NB = (EPI == NT_MOE_EPI_SWIGLU ? 2 * n_out : n_out) / 32;  // packed 32-row blocks
   const int n_tiles = (NB + kTileBlocks - 1) / kTileBlocks;
   const int nk = K / kBK;
-  __builtin_assume(nk >= kMinK / kBK && nk % 2 == 0);  // the launcher guarantees both
+  __builtin_assume(nk >= kMinK / kBK);  // the launcher guarantees it (and an even nk unless EDGE)
+  if constexpr (!EDGE) __builtin_assume(nk % 2 == 0);
+  // K steps per tile in the pipeline: an odd count gets one more step that loads and waits like
+  // the others but multiplies nothing, so every tile keeps whole pairs.
+  const int nks = EDGE ? nk + (nk & 1) : nk;
 
   // Segment table and tile prefix (as in the unpacked kernel): clamped, non-decreasing.
   for (int i = threadIdx.x; i <= S; i += blockDim.x) {
@@ -264,12 +273,14 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
     asm volatile("global_load_dwordx4 %0, %1, %2 offset:3072"
                  : "=v"(b[3]) : "v"(b_lane), "s"(blk) : "memory");
   };
-  // K step kt of this wave's blocks (kt = nk: the first step of the blocks in wn).
+  // K step kt of this wave's blocks (kt = nks: the first step of the blocks in wn; the extra
+  // step of an odd count, kt = nk < nks, re-reads the last).
   auto load_b = [&](const uint16_t* const (&wc)[kWB], const uint16_t* const (&wn)[kWB], int kt,
                     u32x4 (&b)[kWB][4]) {
 #pragma unroll
     for (int rb = 0; rb < kWB; ++rb)
-      load_blk(kt < nk ? wc[rb] + (int64_t)kt * kBlockElems : wn[rb], b[rb]);
+      load_blk(kt >= nks ? wn[rb] : wc[rb] + (int64_t)(kt < nk ? kt : nk - 1) * kBlockElems,
+               b[rb]);
   };
   // Waits until at most N vector memory operations are outstanding, naming the registers of
   // the weight blocks b: no read of them can be scheduled above the wait.
@@ -305,7 +316,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
   int p_idx = 0, p_kt = 0, p_slot = 0, produced = 0;
   int total_steps = 0x7fffffff;  // known once the producer finds there is no next tile
   uint32_t aoff[kAQ];
-  const int src_lead_kt = nk - 4;  // K step of a tile at which the next tile's indices go out
+  const int src_lead_kt = nks - 4;  // K step of a tile at which the next tile's indices go out
   // Selects between the values (not between the two variables' addresses, which would put
   // them in scratch memory).
   auto pick = [](bool o, int x1, int x0) {
@@ -337,14 +348,14 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
 
   auto produce = [&]() {
     const bool live = produced < total_steps;
-    if (live && p_kt == nk) {  // next tile: its gather indices went out four stages ago
+    if (live && p_kt == nks) {  // next tile: its gather indices went out four stages ago
       pt = tile_at(p_idx + 1);
       ++p_idx;
       p_kt = 0;
       p_slot ^= 1;
       a_offsets(pt, p_slot, aoff);
     }
-    const int kt_load = live ? p_kt : nk - 1;
+    const int kt_load = live && p_kt < nk ? p_kt : nk - 1;  // the extra step re-reads the last
     unsigned char* sb = smem + (produced % kSA) * kStage;
 #pragma unroll
     for (int q = 0; q < kAQ; ++q)
@@ -362,7 +373,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
         tq0 = nx;
         ok0 = real;
       }
-      if (!real) total_steps = (p_idx + 1) * nk;
+      if (!real) total_steps = (p_idx + 1) * nks;
     }
     if (GATHER) {
       const bool load_idx = real && wave < kIdxWaves;
@@ -422,11 +433,15 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
     // step, which names their registers so no copy of them can happen before they are valid;
     // the odd step's wait (vmcnt 0) also lands this wave's part of the next pair's stages,
     // which the next barrier then publishes to every wave.
-    auto step = [&](auto nj_c, auto odd_c, int kt, u32x4 (&bc)[kWB][4], u32x4 (&bn)[kWB][4]) {
-      constexpr int NJ = decltype(nj_c)::value;  // 32-token blocks that hold segment rows
+    auto step = [&](auto nj_c, auto odd_c, int kt, u32x4 (&bc)[kWB][4], u32x4 (&bn)[kWB][4])
+                    __attribute__((always_inline)) {  // (an outlined step spills in-flight loads)
+      constexpr int NJ = decltype(nj_c)::value;  // 32-token blocks that hold segment rows (0:
+                                                 // loads and waits only, no products)
       constexpr bool ODD = decltype(odd_c)::value;
       constexpr int NM = 4 * NJ;                 // token fragments per step (kWB MFMAs each)
       constexpr int PF = NM < 4 ? NM : 4;        // fragment reads kept in flight
+      constexpr int NJd = NJ > 0 ? NJ : 1;        // (divisor; no fragment exists when NJ = 0)
+      constexpr int PFd = PF > 0 ? PF : 1;
       if (!ODD) {
         barrier_nofence();
         // Two workgroups share each CU (b and b + gridDim.x / 2) and the one dispatched first
@@ -446,13 +461,13 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
       const unsigned char* st = smem + (g % kSA) * kStage;
       // NM token fragments (slice q = n / NJ, token block j = n % NJ), read PF ahead.
       auto frag = [&](int n) {
-        return *reinterpret_cast<const bf16x8*>(st + (n % NJ) * 32 * kRB + frag_off[n / NJ]);
+        return *reinterpret_cast<const bf16x8*>(st + (n % NJd) * 32 * kRB + frag_off[n / NJd]);
       };
-      bf16x8 fr[PF];
+      bf16x8 fr[PF > 0 ? PF : 1];
 #pragma unroll
       for (int n = 0; n < PF; ++n) fr[n] = frag(n);
       asm volatile("" ::: "memory");
-      if (kt + 1 == nk && tile_ok(ti + 1)) w_base(tile_at(ti + 1), wb_next);
+      if (kt + 1 == nks && tile_ok(ti + 1)) w_base(tile_at(ti + 1), wb_next);
       load_b(wb, wb_next, kt + 1, bn);  // past the last tile: re-reads of its first step
       asm volatile("" ::: "memory");
       if (!ODD) {
@@ -465,9 +480,9 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
       for (int n = 0; n < NM; ++n) {
 #pragma unroll
         for (int rb = 0; rb < kWB; ++rb)
-          acc[rb][n % NJ] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8, bc[rb][n / NJ]), fr[n % PF], acc[rb][n % NJ], 0, 0, 0);
-        if (n + PF < NM) fr[n % PF] = frag(n + PF);
+          acc[rb][n % NJd] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8, bc[rb][n / NJd]), fr[n % PFd], acc[rb][n % NJd], 0, 0, 0);
+        if (n + PF < NM) fr[n % PFd] = frag(n + PF);
       }
       // Keep PF fragment reads in flight: (kWB MFMAs, 1 read) groups, then the last PF groups'
       // MFMAs. Without this the scheduler pulls each read next to its MFMA and waits on it.
@@ -476,30 +491,41 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
         __builtin_amdgcn_sched_group_barrier(0x008, kWB, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, kWB * PF, 0);
+      if constexpr (PF > 0) __builtin_amdgcn_sched_group_barrier(0x008, kWB * PF, 0);
       // Even step: the two stages and index loads issued after B(g + 1) may stay in flight.
       wait_b(std::integral_constant<int, ODD ? 0 : 2 * (kAQ + G)>(), bn);
       ++g;
     };
-    auto k_loop = [&](auto nj_c) {
+    auto k_loop = [&](auto nj_c) __attribute__((always_inline)) {
       for (int kt = 0; kt < nk; kt += 2) {
         step(nj_c, std::false_type(), kt, b0, b1);
-        step(nj_c, std::true_type(), kt + 1, b1, b0);
+        // The extra step of an odd count multiplies nothing. No register load is in flight at
+        // this branch (the even step waited for its weights) or after it (both sides end with
+        // vmcnt(0)).
+        if (!EDGE || kt + 1 < nk) step(nj_c, std::true_type(), kt + 1, b1, b0);
+        else step(std::integral_constant<int, 0>(), std::true_type(), kt + 1, b1, b0);
       }
     };
     // A partial tile (the last of a segment) multiplies only the 32-token blocks that hold
-    // rows. The loads are the same in every variant.
-    if (live_m > kBM / 2) k_loop(std::integral_constant<int, kNJ>());
+    // rows; in a partial N tile a wave whose weight blocks all lie past the last one multiplies
+    // nothing (its SIMD's matrix core goes to the other workgroup's wave). The loads are the
+    // same in every variant.
+    const bool wave_live = !EDGE || ct.nt * kTileBlocks + wave * kWB < NB;
+    if (EDGE && !wave_live) k_loop(std::integral_constant<int, 0>());
+    else if (live_m > kBM / 2) k_loop(std::integral_constant<int, kNJ>());
     else if (live_m > kBM / 4) k_loop(std::integral_constant<int, kNJ / 2>());
     else if (kNJ >= 8 && live_m > kBM / 8) k_loop(std::integral_constant<int, kNJ / 4 ? kNJ / 4 : 1>());
     else k_loop(std::integral_constant<int, 1>());
 
-    // Epilogue: a fixed store count per wave; rows past the segment or columns past n_out get
-    // an out-of-range offset and are dropped by the buffer range check. Lane (token j, half h)
+    // Epilogue: a fixed store count per working wave (none from a wave past the last block: no
+    // later wait counts stores, as they are older than every load a wait names); rows past the
+    // segment or columns past n_out get an out-of-range offset and are dropped by the buffer
+    // range check. Lane (token j, half h)
     // holds logical block rows 8 h + [0, 8) in elements 0-7 and 16 + 8 h + [0, 8) in 8-15:
     // for SwiGLU gate and value of output columns 16 nb + 8 h + [0, 8), otherwise columns
     // 32 nb + 8 h + [0, 8) and 32 nb + 16 + 8 h + [0, 8).
     const int hbit = lane >> 5;
+    if (wave_live)  // (a wave past the last block would store nothing)
 #pragma unroll
     for (int rb = 0; rb < kWB; ++rb) {
       const int nb = ct.nt * kTileBlocks + wave * kWB + rb;
@@ -581,7 +607,7 @@ __global__ __launch_bounds__(256) void pack_weights_kernel(const uint16_t* __res
       *reinterpret_cast<const u32x4*>(w + (s * R + row) * (int64_t)K + k0);
 }
 
-template <int EPI, bool GATHER, int WAVES, bool KEEP = false>
+template <int EPI, bool GATHER, int WAVES, bool KEEP = false, bool EDGE = false>
 hipError_t launch_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows, const int32_t* src_row,
                          const int32_t* seg_offsets, int S, int64_t total_rows,
                          const uint16_t* wp, int K, int n_out, uint16_t* c, hipStream_t stream,
@@ -594,7 +620,7 @@ hipError_t launch_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows, const 
   if (upper < grid) grid = upper;
   grid = ((grid + 7) / 8) * 8;
   const size_t lds = Gm::lds(S);
-  auto kern = grouped_gemm_packed_kernel<EPI, GATHER, WAVES, KEEP>;
+  auto kern = grouped_gemm_packed_kernel<EPI, GATHER, WAVES, KEEP, EDGE>;
   hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(Gm::kThreads), lds, stream, a, ld_a,
@@ -625,24 +651,36 @@ hipError_t launch_pack_weights_bf16(const uint16_t* w, int64_t S, int R, int K, 
   return hipGetLastError();
 }
 
+// Whether a shape needs the EDGE kernel: an odd count of 64-wide K steps, or a last N tile with
+// fewer than 8 packed blocks.
+static bool packed_edge(int K, int n_out, int epilogue) {
+  const int NB = (epilogue == NT_MOE_EPI_SWIGLU ? 2 * n_out : n_out) / 32;
+  return (K / kBK) % 2 != 0 || NB % kTileBlocks != 0;
+}
+
 hipError_t launch_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                                            const int32_t* src_row, const int32_t* seg_offsets,
                                            int num_segments, int64_t total_rows,
                                            const uint16_t* wp, int K, int n_out, int epilogue,
                                            uint16_t* c, hipStream_t stream) {
   if (total_rows == 0) return hipSuccess;
-#define NT_PW(EPI, W)                                                                      \
-  return src_row ? launch_packed<EPI, true, W>(a, ld_a, a_rows, src_row, seg_offsets,      \
-                                               num_segments, total_rows, wp, K, n_out, c,   \
-                                               stream)                                      \
-                 : launch_packed<EPI, false, W>(a, ld_a, a_rows, src_row, seg_offsets,     \
-                                                num_segments, total_rows, wp, K, n_out, c,  \
-                                                stream)
-#define NT_P(EPI)                  \
-  if (packed_waves() == 8) {       \
-    NT_PW(EPI, 8);                 \
-  } else {                         \
-    NT_PW(EPI, 4);                 \
+  const bool edge = packed_edge(K, n_out, epilogue);
+#define NT_PW(EPI, W, EDGE)                                                                   \
+  return src_row ? launch_packed<EPI, true, W, false, EDGE>(a, ld_a, a_rows, src_row,         \
+                                                            seg_offsets, num_segments,        \
+                                                            total_rows, wp, K, n_out, c,      \
+                                                            stream)                           \
+                 : launch_packed<EPI, false, W, false, EDGE>(a, ld_a, a_rows, src_row,        \
+                                                             seg_offsets, num_segments,       \
+                                                             total_rows, wp, K, n_out, c,     \
+                                                             stream)
+#define NT_P(EPI)                        \
+  if (edge) {                            \
+    NT_PW(EPI, 4, true);                 \
+  } else if (packed_waves() == 8) {      \
+    NT_PW(EPI, 8, false);                \
+  } else {                               \
+    NT_PW(EPI, 4, false);                \
   }
   switch (epilogue) {
     case NT_MOE_EPI_SWIGLU: NT_P(NT_MOE_EPI_SWIGLU);
@@ -660,18 +698,28 @@ hipError_t launch_grouped_gemm_bf16_packed_keep(const uint16_t* a, int64_t ld_a,
                                                 int n_out, int epilogue, uint16_t* c,
                                                 uint16_t* pre, hipStream_t stream) {
   if (total_rows == 0) return hipSuccess;
-#define NT_PK(EPI)                                                                          \
-  return src_row ? launch_packed<EPI, true, 4, true>(a, ld_a, a_rows, src_row, seg_offsets, \
-                                                     num_segments, total_rows, wp, K, n_out, \
-                                                     c, stream, pre)                         \
-                 : launch_packed<EPI, false, 4, true>(a, ld_a, a_rows, src_row, seg_offsets, \
-                                                      num_segments, total_rows, wp, K, n_out, \
-                                                      c, stream, pre)
+  const bool edge = packed_edge(K, n_out, epilogue);
+#define NT_PKE(EPI, EDGE)                                                                    \
+  return src_row ? launch_packed<EPI, true, 4, true, EDGE>(a, ld_a, a_rows, src_row,         \
+                                                           seg_offsets, num_segments,        \
+                                                           total_rows, wp, K, n_out, c,      \
+                                                           stream, pre)                      \
+                 : launch_packed<EPI, false, 4, true, EDGE>(a, ld_a, a_rows, src_row,        \
+                                                            seg_offsets, num_segments,       \
+                                                            total_rows, wp, K, n_out, c,     \
+                                                            stream, pre)
+#define NT_PK(EPI)        \
+  if (edge) {             \
+    NT_PKE(EPI, true);    \
+  } else {                \
+    NT_PKE(EPI, false);   \
+  }
   if (epilogue == NT_MOE_EPI_SWIGLU) {
     NT_PK(NT_MOE_EPI_SWIGLU);
   }
   NT_PK(NT_MOE_EPI_RELU2);
 #undef NT_PK
+#undef NT_PKE
 }
 
 }  // namespace ntmoe

@@ -389,11 +389,11 @@ class MoELayer(nn.Module):
             # K = 1280; the down projection plain, K = 320.)
             widths = [r.expert_width] + ([r.shared_expert_width] if self.shared_experts else [])
             on_gpu = self.router.weight.is_cuda
-            pk_up = fp8 or (on_gpu and all(ops.packable(
+            pk_up = fp8 or (on_gpu and all(ops.prefers_packed(
                 dp, _round_up(h, align), nat.EPI_SWIGLU if gated else nat.EPI_RELU2)
                 for h in widths))
             pk_down = fp8 or (on_gpu and all(
-                ops.packable(_round_up(h, align), dp, nat.EPI_NONE) for h in widths))
+                ops.prefers_packed(_round_up(h, align), dp, nat.EPI_NONE) for h in widths))
 
             def stack(experts, hidden, pools=(None, None)):
                 hp = _round_up(hidden, align)

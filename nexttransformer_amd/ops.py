@@ -333,7 +333,15 @@ def _(w, want_out, want_t):
 
 def packable(K, n_out, epilogue):
     """Whether a [*, n_out or 2 n_out, K] weight stack qualifies for the packed GEMM."""
-    return K >= 256 and K % 128 == 0 and n_out % (16 if epilogue == nat.EPI_SWIGLU else 32) == 0
+    return K >= 256 and K % 64 == 0 and n_out % (16 if epilogue == nat.EPI_SWIGLU else 32) == 0
+
+
+def prefers_packed(K, n_out, epilogue):
+    """Whether the layer packs a projection: packable with an even count of 64-wide K steps. An
+    odd count (K = 320, the T3 cell's down projection and fc1 dgrad) runs a sixth step per tile
+    that multiplies nothing and measured within 2 % of the 256 x 256 plain-weight kernel, less
+    than the repack that a training step pays when the weights change."""
+    return packable(K, n_out, epilogue) and K % 128 == 0
 
 
 @_custom_op("ntmoe::grouped_gemm_packed")
@@ -862,7 +870,7 @@ class Projection:
 
     def __init__(self, w):
         S, n, K = w.shape
-        self.packed = packable(K, n, nat.EPI_NONE)
+        self.packed = prefers_packed(K, n, nat.EPI_NONE)
         self.w = pack_expert_weights.raw(w.contiguous(), nat.EPI_NONE) if self.packed else w.contiguous()
 
     def __call__(self, a, src_row, seg_offsets, total_rows):

@@ -66,7 +66,8 @@ def _ref_gemm(a, src, seg, w, epilogue):
     return out
 
 
-@pytest.mark.parametrize("K", [256, 384, 1024])
+# K = 320 and 448 are odd counts of 64-wide K steps (the extra step that multiplies nothing)
+@pytest.mark.parametrize("K", [256, 320, 384, 448, 1024])
 @pytest.mark.parametrize("epilogue", [0, 1, 2], ids=["swiglu", "relu2", "plain"])
 @pytest.mark.parametrize("gather", [False, True])
 def test_packed_gemm_matches_fp32(K, epilogue, gather):
@@ -126,6 +127,43 @@ def test_packed_gemm_many_tiles(K, epilogue, gather, rows_scale):
         if m.any():
             z = a[a_idx[m]].double() @ w[s_].double().t()
             ref[m] = torch.nn.functional.silu(z[:, :n_out]) * z[:, n_out:] if epilogue == 0 else z
+    assert rel_l2(c[pick].float(), ref) <= BF16_TOL
+
+
+@pytest.mark.parametrize("epilogue", [1, 2], ids=["relu2", "plain"])
+@pytest.mark.parametrize("gather", [False, True])
+def test_packed_gemm_t3_widths_many_tiles(epilogue, gather):
+    # The registered T3 cell's widths: K = 320 (five K steps per tile) for the down projection,
+    # 320 output columns (ten 32-row blocks: the second N tile's last three waves multiply
+    # nothing) for the up projection; 256 segments with ragged counts, two launches equal.
+    from nexttransformer_amd import ops
+    g = torch.Generator().manual_seed(31 + epilogue + 2 * gather)
+    S, K, n_out = 256, 320, 320
+    counts = torch.randint(0, 700, (S,), generator=g)
+    counts[::17] = 0
+    rows = int(counts.sum())
+    seg = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)]).to(torch.int32)
+    a_rows = 30000 if gather else rows
+    a = torch.randn(a_rows, K, generator=g).to(torch.bfloat16)
+    src = torch.randint(0, a_rows, (rows,), generator=g, dtype=torch.int32) if gather else None
+    w = (torch.randn(S, n_out, K, generator=g) * 0.05).to(torch.bfloat16)
+    wp = ops.pack_expert_weights(w.cuda(), epilogue)
+    args = (a.cuda(), None if src is None else src.cuda(), seg.cuda(), wp, epilogue, rows)
+    c = ops.grouped_gemm_packed(*args)
+    c2 = ops.grouped_gemm_packed(*args)
+    torch.cuda.synchronize()
+    c = c.cpu()
+    assert torch.isfinite(c.float()).all() and torch.equal(c, c2.cpu())
+    pick = torch.cat([torch.arange(lo, min(lo + 8, hi)) for lo, hi in
+                      zip(seg[:-1].tolist(), seg[1:].tolist()) if hi > lo]
+                     + [torch.randint(0, rows, (300,), generator=g)])
+    a_idx = src[pick].long() if gather else pick
+    seg_of = torch.searchsorted(seg[1:].long(), pick, right=True)
+    ref = torch.empty(len(pick), n_out, dtype=torch.float64)
+    for s_ in seg_of.unique().tolist():
+        m = seg_of == s_
+        z = a[a_idx[m]].double() @ w[s_].double().t()
+        ref[m] = torch.relu(z).square() if epilogue == 1 else z
     assert rel_l2(c[pick].float(), ref) <= BF16_TOL
 
 
