@@ -258,13 +258,17 @@ def test_grouped_wgrad_shapes_fp32_and_bf16(N, M, gather, splits):
             torch.testing.assert_close(got32[s].double(), ref, rtol=1e-5, atol=1e-4)
 
 
-@pytest.mark.parametrize("activation", [0, 1])
-def test_kept_pre_activations_equal_a_recompute(activation):
+# the last two: a partial N tile (ReLU^2, 320 columns: the T3 cell's up projection) and an odd
+# K-step count with a six-block N tile (K = 320, SwiGLU 96 columns)
+@pytest.mark.parametrize("activation,d,H", [(0, 512, 256), (1, 512, 256), (1, 1280, 320),
+                                            (0, 320, 96)],
+                         ids=["swiglu", "relu2", "relu2-d1280-H320", "swiglu-d320-H96"])
+def test_kept_pre_activations_equal_a_recompute(activation, d, H):
     """The keep launch's h equals the plain packed launch's, and its pre-activations equal an
     EPI_NONE launch over the same rows, bit for bit (same fp32 accumulators, one rounding)."""
     from nexttransformer_amd import _native as nat, ops
-    gen = torch.Generator().manual_seed(41 + activation)
-    E, d, H, T = 8, 512, 256, 700
+    gen = torch.Generator().manual_seed(41 + activation + d)
+    E, T = 8, 700
     F = 2 * H if activation == 0 else H
     up = nat.EPI_SWIGLU if activation == 0 else nat.EPI_RELU2
     w1 = (torch.randn(E, F, d, generator=gen) * 0.05).to(torch.bfloat16).cuda()
