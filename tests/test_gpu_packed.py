@@ -167,6 +167,36 @@ def test_packed_gemm_t3_widths_many_tiles(epilogue, gather):
     assert rel_l2(c[pick].float(), ref) <= BF16_TOL
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_packed_equals_plain_random_shapes(seed):
+    # The packed kernel (EDGE instantiation for odd K-step counts and partial N tiles) and the
+    # 256 x 256 plain-weight kernel add each output's products in the same K order, so their
+    # outputs are equal bit for bit: random K (multiple of 64, >= 256), widths, segment counts.
+    from nexttransformer_amd import ops
+    g = torch.Generator().manual_seed(1000 + seed)
+    epilogue = seed % 3
+    K = 64 * int(torch.randint(4, 21, (1,), generator=g))
+    n_out = 32 * int(torch.randint(1, 21, (1,), generator=g))
+    S = int(torch.randint(1, 40, (1,), generator=g))
+    counts = torch.randint(0, 600, (S,), generator=g)
+    counts[torch.randint(0, S, (max(1, S // 5),), generator=g)] = 0
+    rows = int(counts.sum())
+    if rows == 0:
+        counts[0], rows = 1, 1
+    seg = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)]).to(torch.int32).cuda()
+    R = 2 * n_out if epilogue == 0 else n_out
+    gather = seed % 2 == 0
+    a_rows = 3000 if gather else rows
+    a = torch.randn(a_rows, K, generator=g).to(torch.bfloat16).cuda()
+    src = torch.randint(0, a_rows, (rows,), generator=g, dtype=torch.int32).cuda() if gather else None
+    w = (torch.randn(S, R, K, generator=g) * 0.05).to(torch.bfloat16).cuda()
+    packed = ops.grouped_gemm_packed(a, src, seg, ops.pack_expert_weights(w, epilogue), epilogue,
+                                     rows)
+    plain = ops.grouped_gemm(a, src, seg, w, epilogue, rows)
+    torch.cuda.synchronize()
+    assert torch.equal(packed.view(torch.int16), plain.view(torch.int16)), (K, n_out, S, epilogue)
+
+
 PACKED_CASES = [
     Case("cfg1-shape", 512, 256, 8, 2, 512),
     Case("ragged-T1000-E32-k4", 1000, 1024, 32, 4, 512, seed=1),
