@@ -443,17 +443,21 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
       constexpr int NJd = NJ > 0 ? NJ : 1;        // (divisor; no fragment exists when NJ = 0)
       constexpr int PFd = PF > 0 ? PF : 1;
       if (!ODD) {
-        barrier_nofence();
         // Two workgroups share each CU (b and b + gridDim.x / 2) and the one dispatched first
         // would win instruction arbitration throughout, leaving its partner to finish alone.
         // Instead the two take turns at the higher wave priority, switching every 2^11 ticks
-        // (about 20 us) of the 100 MHz real-time counter, so both progress alike.
+        // (about 20 us) of the 100 MHz real-time counter, so both progress alike. The counter is
+        // read before the barrier, in the same statement as the wait for it, so its latency
+        // overlaps the barrier wait (the barrier's own wait for the LDS reads is the same one).
         if (kWaves == 4) {
           uint64_t now;
-          asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(now));
+          asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier"
+                       : "=s"(now)::"memory");
           const bool high = (((now >> 11) & 1) != 0) != (blockIdx.x >= gridDim.x / 2);
           if (high) __builtin_amdgcn_s_setprio(1);
           else __builtin_amdgcn_s_setprio(0);
+        } else {
+          barrier_nofence();
         }
       }
       // The first PF token fragments go out first, so their latency overlaps the issue of this
