@@ -63,6 +63,7 @@ constexpr int kRPI = 64 / kCH;     // rows per load instruction (8)
 constexpr int kBlockElems = 32 * kBK;  // packed weight block (32 rows x 64 K) = 2048 bf16
 constexpr int kMinK = 4 * kBK;     // the gather table needs four K steps of lead
 constexpr int kTileBlocks = 8;     // packed 32-row weight blocks per N tile (256 weight rows)
+constexpr int kXposeBytes = 2048;  // per-wave LDS scratch of the epilogue's output transpose
 
 // Two workgroup shapes share the kernel. WAVES = 8: 256 tokens per tile, one weight block per
 // wave, one workgroup per CU. WAVES = 4: 128 tokens per tile, two weight blocks per wave (each
@@ -79,9 +80,9 @@ struct Geo {
   static constexpr int kStage = kBM * kRB;          // bytes per LDS stage
   static constexpr int kIdxWaves = kBM / 64;        // waves that load a tile's gather indices
   static constexpr int kPerCU = 8 / WAVES;          // workgroups per CU
-  static constexpr size_t lds(int S) {
-    return (size_t)kSA * kStage + (2 * kBM + kWaves * 64) * sizeof(int) +
-           (size_t)(2 * S + 2) * sizeof(int);
+  static constexpr size_t lds(int S) {  // (two 4-wave workgroups fit a CU up to 512 segments)
+    return (size_t)kSA * kStage + (size_t)kWaves * kXposeBytes +
+           (2 * kBM + kWaves * 64) * sizeof(int) + (size_t)(2 * S + 2) * sizeof(int);
   }
 };
 
@@ -135,7 +136,8 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
   constexpr int kWB = Gm::kWB, kNJ = Gm::kNJ, kIdxWaves = Gm::kIdxWaves;
   constexpr int G = GATHER ? 1 : 0;
   extern __shared__ __align__(16) unsigned char smem[];
-  int* src_tab = reinterpret_cast<int*>(smem + kSA * kStage);  // [2][kBM]
+  unsigned char* xpose = smem + kSA * kStage + wave_id() * kXposeBytes;  // this wave's scratch
+  int* src_tab = reinterpret_cast<int*>(smem + kSA * kStage + kWaves * kXposeBytes);  // [2][kBM]
   int* src_dummy = src_tab + 2 * kBM;                           // [kWaves][64] sink
   int* tile_prefix = src_dummy + kWaves * 64;                   // [S+1]
   int* seg_lo = tile_prefix + (S + 1);                          // [S+1]
@@ -521,59 +523,94 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
     else if (kNJ >= 8 && live_m > kBM / 8) k_loop(std::integral_constant<int, kNJ / 4 ? kNJ / 4 : 1>());
     else k_loop(std::integral_constant<int, 1>());
 
-    // Epilogue: a fixed store count per working wave (none from a wave past the last block: no
-    // later wait counts stores, as they are older than every load a wait names); rows past the
-    // segment or columns past n_out get an out-of-range offset and are dropped by the buffer
-    // range check. Lane (token j, half h)
-    // holds logical block rows 8 h + [0, 8) in elements 0-7 and 16 + 8 h + [0, 8) in 8-15:
-    // for SwiGLU gate and value of output columns 16 nb + 8 h + [0, 8), otherwise columns
-    // 32 nb + 8 h + [0, 8) and 32 nb + 16 + 8 h + [0, 8).
+    // Epilogue. Lane (token j, half h) holds logical block rows 8 h + [0, 8) in elements 0-7 and
+    // 16 + 8 h + [0, 8) in 8-15: for SwiGLU gate and value of output columns 16 nb + 8 h + [0, 8),
+    // otherwise columns 32 nb + 8 h + [0, 8) and 32 nb + 16 + 8 h + [0, 8). Stored straight from
+    // that layout, one instruction would write 32 B of each of 32 rows; instead each wave
+    // transposes its outputs through its LDS scratch (row-major, 16-byte chunks XOR-swizzled by
+    // row so writes and reads are conflict-free), 16 rows (or 32 for SwiGLU) at a time, and every
+    // store instruction writes whole 128-byte (SwiGLU: 64-byte) row segments of the wave's
+    // columns. The store count per wave is fixed (none from a wave past the last block: no later
+    // wait counts stores, as they are older than every load a wait names); rows past the segment
+    // or columns past n_out get an out-of-range offset and are dropped by the buffer range check.
     const int hbit = lane >> 5;
-    if (wave_live)  // (a wave past the last block would store nothing)
-#pragma unroll
-    for (int rb = 0; rb < kWB; ++rb) {
-      const int nb = ct.nt * kTileBlocks + wave * kWB + rb;
+    if (wave_live) {
+      constexpr bool SW = EPI == NT_MOE_EPI_SWIGLU;
+      constexpr int CPR = kWB * (SW ? 2 : 4);  // 16-byte chunks per row of the wave's columns
+      constexpr int RPH = kXposeBytes / (CPR * 16) < 32 ? kXposeBytes / (CPR * 16) : 32;  // rows
+      constexpr int RPS = 64 / CPR;            // per pass through the scratch; per store
+      static_assert(RPH * CPR * 16 <= kXposeBytes && 32 % RPH == 0 && RPH % RPS == 0, "passes");
+      // chunk c of row r: the 8 rows that share a 128-byte LDS line pattern get distinct chunks
+      auto xoff = [](int r, int c) { return r * CPR * 16 + ((c ^ ((r / (8 / CPR)) % CPR)) << 4); };
+      const int col0 = (ct.nt * kTileBlocks + wave * kWB) * (SW ? 16 : 32);
+      const int t = lane & 31;
 #pragma unroll
       for (int j = 0; j < kNJ; ++j) {
-        const int m = ct.m0 + j * 32 + (lane & 31);
-        const bool row_ok = m < ct.seg_end;
 #pragma unroll
-        for (int st = 0; st < Ep<EPI>::kStores; ++st) {
-          int col;
-          float v[8];
-          if (EPI == NT_MOE_EPI_SWIGLU) {
-            col = nb * 16 + 8 * hbit;
+        for (int pass = 0; pass < 32 / RPH; ++pass) {
+          if (t / RPH == pass) {
 #pragma unroll
-            for (int r = 0; r < 8; ++r) {
-              const float a = acc[rb][j][r], u = acc[rb][j][8 + r];
-              v[r] = a * u * __builtin_amdgcn_rcpf(1.f + __expf(-a));
-            }
-          } else {
-            col = nb * 32 + 16 * st + 8 * hbit;
+            for (int rb = 0; rb < kWB; ++rb)
 #pragma unroll
-            for (int r = 0; r < 8; ++r) {
-              const float a = acc[rb][j][8 * st + r];
-              v[r] = EPI == NT_MOE_EPI_RELU2 ? (a > 0.f ? a * a : 0.f) : a;
-            }
+              for (int st = 0; st < Ep<EPI>::kStores; ++st) {
+                float v[8];
+                if (SW) {
+#pragma unroll
+                  for (int r = 0; r < 8; ++r) {
+                    const float a = acc[rb][j][r], u = acc[rb][j][8 + r];
+                    v[r] = a * u * __builtin_amdgcn_rcpf(1.f + __expf(-a));
+                  }
+                } else {
+#pragma unroll
+                  for (int r = 0; r < 8; ++r) {
+                    const float a = acc[rb][j][8 * st + r];
+                    v[r] = EPI == NT_MOE_EPI_RELU2 ? (a > 0.f ? a * a : 0.f) : a;
+                  }
+                }
+                const u32x4 packed = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                      pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+                const int c = SW ? rb * 2 + hbit : rb * 4 + st * 2 + hbit;
+                *reinterpret_cast<u32x4*>(xpose + xoff(t - pass * RPH, c)) = packed;
+              }
           }
-          const u32x4 packed = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
-                                pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
-          const uint32_t voff = (row_ok && nb < NB && col < n_out)
-                                    ? (uint32_t)(((int64_t)m * n_out + col) * 2)
-                                    : 0x80000000u;
-          __builtin_amdgcn_raw_buffer_store_b128(packed, out_rsrc, voff, 0, 0);
-          if constexpr (KEEP) {
-            const bool ok = row_ok && nb < NB && col < n_out;
+          asm volatile("" ::: "memory");  // the wave's LDS operations run in order
+#pragma unroll
+          for (int sidx = 0; sidx < RPH / RPS; ++sidx) {
+            const int r = sidx * RPS + lane / CPR, q = lane % CPR;
+            const u32x4 val = *reinterpret_cast<const u32x4*>(xpose + xoff(r, q));
+            const int m = ct.m0 + j * 32 + pass * RPH + r;
+            const int col = col0 + q * 8;
+            const uint32_t voff = (m < ct.seg_end && col < n_out)
+                                      ? (uint32_t)(((int64_t)m * n_out + col) * 2)
+                                      : 0x80000000u;
+            __builtin_amdgcn_raw_buffer_store_b128(val, out_rsrc, voff, 0, 0);
+          }
+          asm volatile("" ::: "memory");
+        }
+      }
+      if constexpr (KEEP) {  // the fc1 pre-activations, straight from the accumulator layout
+#pragma unroll
+        for (int rb = 0; rb < kWB; ++rb) {
+          const int nb = ct.nt * kTileBlocks + wave * kWB + rb;
+#pragma unroll
+          for (int j = 0; j < kNJ; ++j) {
+            const int m = ct.m0 + j * 32 + t;
             const int64_t prow = (int64_t)m * kPreW * n_out;
 #pragma unroll
-            for (int h = 0; h < (EPI == NT_MOE_EPI_SWIGLU ? 2 : 1); ++h) {
-              const int e0 = EPI == NT_MOE_EPI_SWIGLU ? 8 * h : 8 * st;
-              const u32x4 pv = {pack_bf16x2(acc[rb][j][e0], acc[rb][j][e0 + 1]),
-                                pack_bf16x2(acc[rb][j][e0 + 2], acc[rb][j][e0 + 3]),
-                                pack_bf16x2(acc[rb][j][e0 + 4], acc[rb][j][e0 + 5]),
-                                pack_bf16x2(acc[rb][j][e0 + 6], acc[rb][j][e0 + 7])};
-              const uint32_t poff = ok ? (uint32_t)((prow + h * n_out + col) * 2) : 0x80000000u;
-              __builtin_amdgcn_raw_buffer_store_b128(pv, pre_rsrc, poff, 0, 0);
+            for (int st = 0; st < Ep<EPI>::kStores; ++st) {
+              const int col = SW ? nb * 16 + 8 * hbit : nb * 32 + 16 * st + 8 * hbit;
+              const bool ok = m < ct.seg_end && nb < NB && col < n_out;
+#pragma unroll
+              for (int h = 0; h < (SW ? 2 : 1); ++h) {
+                const int e0 = SW ? 8 * h : 8 * st;
+                const u32x4 pv = {pack_bf16x2(acc[rb][j][e0], acc[rb][j][e0 + 1]),
+                                  pack_bf16x2(acc[rb][j][e0 + 2], acc[rb][j][e0 + 3]),
+                                  pack_bf16x2(acc[rb][j][e0 + 4], acc[rb][j][e0 + 5]),
+                                  pack_bf16x2(acc[rb][j][e0 + 6], acc[rb][j][e0 + 7])};
+                const uint32_t poff =
+                    ok ? (uint32_t)((prow + h * n_out + col) * 2) : 0x80000000u;
+                __builtin_amdgcn_raw_buffer_store_b128(pv, pre_rsrc, poff, 0, 0);
+              }
             }
           }
         }
