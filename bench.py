@@ -360,7 +360,8 @@ def gpu_inputs(case, fp8):
         pk = []
         for group, e in zip(names, (up, nat.EPI_NONE)):
             ok = all(ops.prefers_packed(g[n].shape[2],
-                                        g[n].shape[1] // (2 if e == nat.EPI_SWIGLU else 1), e)
+                                        g[n].shape[1] // (2 if e == nat.EPI_SWIGLU else 1), e,
+                                        repacked_each_step=False)  # packed once, as inference
                      for n in group)
             if ok:
                 for n in group:

@@ -546,32 +546,58 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
       const int t = lane & 31;
 #pragma unroll
       for (int j = 0; j < kNJ; ++j) {
+        // block j's outputs packed first (and its pre-activations stored), so its accumulators
+        // are free before the transpose
+        u32x4 pk[kWB][Ep<EPI>::kStores];
+        const int m_lane = ct.m0 + j * 32 + t;
+#pragma unroll
+        for (int rb = 0; rb < kWB; ++rb)
+#pragma unroll
+          for (int st = 0; st < Ep<EPI>::kStores; ++st) {
+            float v[8];
+            if (SW) {
+#pragma unroll
+              for (int r = 0; r < 8; ++r) {
+                const float a = acc[rb][j][r], u = acc[rb][j][8 + r];
+                v[r] = a * u * __builtin_amdgcn_rcpf(1.f + __expf(-a));
+              }
+            } else {
+#pragma unroll
+              for (int r = 0; r < 8; ++r) {
+                const float a = acc[rb][j][8 * st + r];
+                v[r] = EPI == NT_MOE_EPI_RELU2 ? (a > 0.f ? a * a : 0.f) : a;
+              }
+            }
+            pk[rb][st] = u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                               pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+            if constexpr (KEEP) {  // the fc1 pre-activations, straight from the accumulator layout
+              const int nb = ct.nt * kTileBlocks + wave * kWB + rb;
+              const int col = SW ? nb * 16 + 8 * hbit : nb * 32 + 16 * st + 8 * hbit;
+              const bool ok = m_lane < ct.seg_end && nb < NB && col < n_out;
+              const int64_t prow = (int64_t)m_lane * kPreW * n_out;
+#pragma unroll
+              for (int h = 0; h < (SW ? 2 : 1); ++h) {
+                const int e0 = SW ? 8 * h : 8 * st;
+                const u32x4 pv = {pack_bf16x2(acc[rb][j][e0], acc[rb][j][e0 + 1]),
+                                  pack_bf16x2(acc[rb][j][e0 + 2], acc[rb][j][e0 + 3]),
+                                  pack_bf16x2(acc[rb][j][e0 + 4], acc[rb][j][e0 + 5]),
+                                  pack_bf16x2(acc[rb][j][e0 + 6], acc[rb][j][e0 + 7])};
+                const uint32_t poff =
+                    ok ? (uint32_t)((prow + h * n_out + col) * 2) : 0x80000000u;
+                __builtin_amdgcn_raw_buffer_store_b128(pv, pre_rsrc, poff, 0, 0);
+              }
+            }
+          }
 #pragma unroll
         for (int pass = 0; pass < 32 / RPH; ++pass) {
           if (t / RPH == pass) {
 #pragma unroll
             for (int rb = 0; rb < kWB; ++rb)
 #pragma unroll
-              for (int st = 0; st < Ep<EPI>::kStores; ++st) {
-                float v[8];
-                if (SW) {
-#pragma unroll
-                  for (int r = 0; r < 8; ++r) {
-                    const float a = acc[rb][j][r], u = acc[rb][j][8 + r];
-                    v[r] = a * u * __builtin_amdgcn_rcpf(1.f + __expf(-a));
-                  }
-                } else {
-#pragma unroll
-                  for (int r = 0; r < 8; ++r) {
-                    const float a = acc[rb][j][8 * st + r];
-                    v[r] = EPI == NT_MOE_EPI_RELU2 ? (a > 0.f ? a * a : 0.f) : a;
-                  }
-                }
-                const u32x4 packed = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
-                                      pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
-                const int c = SW ? rb * 2 + hbit : rb * 4 + st * 2 + hbit;
-                *reinterpret_cast<u32x4*>(xpose + xoff(t - pass * RPH, c)) = packed;
-              }
+              for (int st = 0; st < Ep<EPI>::kStores; ++st)
+                *reinterpret_cast<u32x4*>(
+                    xpose + xoff(t - pass * RPH, SW ? rb * 2 + hbit : rb * 4 + st * 2 + hbit)) =
+                    pk[rb][st];
           }
           asm volatile("" ::: "memory");  // the wave's LDS operations run in order
 #pragma unroll
@@ -586,33 +612,6 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
             __builtin_amdgcn_raw_buffer_store_b128(val, out_rsrc, voff, 0, 0);
           }
           asm volatile("" ::: "memory");
-        }
-      }
-      if constexpr (KEEP) {  // the fc1 pre-activations, straight from the accumulator layout
-#pragma unroll
-        for (int rb = 0; rb < kWB; ++rb) {
-          const int nb = ct.nt * kTileBlocks + wave * kWB + rb;
-#pragma unroll
-          for (int j = 0; j < kNJ; ++j) {
-            const int m = ct.m0 + j * 32 + t;
-            const int64_t prow = (int64_t)m * kPreW * n_out;
-#pragma unroll
-            for (int st = 0; st < Ep<EPI>::kStores; ++st) {
-              const int col = SW ? nb * 16 + 8 * hbit : nb * 32 + 16 * st + 8 * hbit;
-              const bool ok = m < ct.seg_end && nb < NB && col < n_out;
-#pragma unroll
-              for (int h = 0; h < (SW ? 2 : 1); ++h) {
-                const int e0 = SW ? 8 * h : 8 * st;
-                const u32x4 pv = {pack_bf16x2(acc[rb][j][e0], acc[rb][j][e0 + 1]),
-                                  pack_bf16x2(acc[rb][j][e0 + 2], acc[rb][j][e0 + 3]),
-                                  pack_bf16x2(acc[rb][j][e0 + 4], acc[rb][j][e0 + 5]),
-                                  pack_bf16x2(acc[rb][j][e0 + 6], acc[rb][j][e0 + 7])};
-                const uint32_t poff =
-                    ok ? (uint32_t)((prow + h * n_out + col) * 2) : 0x80000000u;
-                __builtin_amdgcn_raw_buffer_store_b128(pv, pre_rsrc, poff, 0, 0);
-              }
-            }
-          }
         }
       }
     }

@@ -386,14 +386,16 @@ class MoELayer(nn.Module):
             # The packed-weight GEMM (fragment-ordered weights streamed into registers) for a
             # projection when its K and width qualify for every expert kind (routed, shared) and
             # the weights live on the GPU; fp8 always. (The T3 cell: the up projection packed,
-            # K = 1280; the down projection plain, K = 320.)
+            # K = 1280; the down projection, K = 320, packed for inference, plain in training.)
             widths = [r.expert_width] + ([r.shared_expert_width] if self.shared_experts else [])
             on_gpu = self.router.weight.is_cuda
+            # training (keep_plain) repacks after every update; inference packs once
             pk_up = fp8 or (on_gpu and all(ops.prefers_packed(
-                dp, _round_up(h, align), nat.EPI_SWIGLU if gated else nat.EPI_RELU2)
-                for h in widths))
+                dp, _round_up(h, align), nat.EPI_SWIGLU if gated else nat.EPI_RELU2,
+                repacked_each_step=keep_plain) for h in widths))
             pk_down = fp8 or (on_gpu and all(
-                ops.prefers_packed(_round_up(h, align), dp, nat.EPI_NONE) for h in widths))
+                ops.prefers_packed(_round_up(h, align), dp, nat.EPI_NONE,
+                                   repacked_each_step=keep_plain) for h in widths))
 
             def stack(experts, hidden, pools=(None, None)):
                 hp = _round_up(hidden, align)

@@ -336,12 +336,14 @@ def packable(K, n_out, epilogue):
     return K >= 256 and K % 64 == 0 and n_out % (16 if epilogue == nat.EPI_SWIGLU else 32) == 0
 
 
-def prefers_packed(K, n_out, epilogue):
-    """Whether the layer packs a projection: packable with an even count of 64-wide K steps. An
-    odd count (K = 320, the T3 cell's down projection and fc1 dgrad) runs a sixth step per tile
-    that multiplies nothing and measured within 2 % of the 256 x 256 plain-weight kernel, less
-    than the repack that a training step pays when the weights change."""
-    return packable(K, n_out, epilogue) and K % 128 == 0
+def prefers_packed(K, n_out, epilogue, repacked_each_step=True):
+    """Whether the layer packs a projection. Weights packed once (inference): whenever packable.
+    Weights repacked after every update (training): only with an even count of 64-wide K steps.
+    An odd count (K = 320, the T3 cell's down projection and fc1 dgrad) runs a sixth step per
+    tile that multiplies nothing; there the packed kernel measured 176 us against the 256 x 256
+    plain-weight kernel's 210 us, less than the ~80 us repack of the [256, 1280, 320] weights
+    that each training step would add."""
+    return packable(K, n_out, epilogue) and (K % 128 == 0 or not repacked_each_step)
 
 
 @_custom_op("ntmoe::grouped_gemm_packed")
