@@ -237,6 +237,21 @@ int nt_moe_convert_expert_weights(const float* w, int64_t num_matrices, int32_t 
                                   nt_moe_stream_t stream);
 
 /*
+ * The same single read of the fp32 masters, with two more optional outputs in the packed GEMM's
+ * fragment order (the layout nt_moe_pack_expert_weights_bf16 writes): packed = w packed for
+ * `epilogue` (for SWIGLU, rows = 2 n_out, gate and value rows paired), packed_t = w^T
+ * [num_matrices, cols, rows] packed as a plain projection (EPI_NONE). Bit-identical to
+ * nt_moe_convert_expert_weights followed by nt_moe_pack_expert_weights_bf16, without the second
+ * pass over the bf16 copy that every weight update would otherwise pay. Any output may be NULL.
+ * rows and cols multiples of 64; 16-byte aligned buffers. No counterpart in the reference beyond
+ * the per-product cast it prepares (megatron_moe.py:74-75).
+ */
+int nt_moe_convert_expert_weights_packed(const float* w, int64_t num_matrices, int32_t rows,
+                                         int32_t cols, uint16_t* out, uint16_t* out_t,
+                                         uint16_t* packed, int32_t epilogue, uint16_t* packed_t,
+                                         nt_moe_stream_t stream);
+
+/*
  * Packed-weight variant of the grouped GEMM. nt_moe_pack_expert_weights_bf16 rearranges
  * w [num_segments, rows, K] once (same bytes, fragment order: 32-row x 64-K blocks in which
  * each lane's 16-byte operand chunk is contiguous with its neighbours', rows inside a block

@@ -593,6 +593,26 @@ int nt_moe_convert_expert_weights(const float* w, int64_t num_matrices, int32_t 
                   "convert_expert_weights");
 }
 
+int nt_moe_convert_expert_weights_packed(const float* w, int64_t num_matrices, int32_t rows,
+                                         int32_t cols, uint16_t* out, uint16_t* out_t,
+                                         uint16_t* packed, int32_t epilogue, uint16_t* packed_t,
+                                         nt_moe_stream_t stream) {
+  NT_REQUIRE(num_matrices >= 0 && rows > 0 && rows % 64 == 0 && cols > 0 && cols % 64 == 0,
+             "convert_expert_weights_packed: rows and cols must be positive multiples of 64, "
+             "got %d x %d", rows, cols);
+  NT_REQUIRE(epilogue == NT_MOE_EPI_SWIGLU || epilogue == NT_MOE_EPI_RELU2 ||
+                 epilogue == NT_MOE_EPI_NONE,
+             "convert_expert_weights_packed: unknown epilogue %d", epilogue);
+  if (num_matrices == 0 || (!out && !out_t && !packed && !packed_t)) return ok();
+  NT_REQUIRE(w && aligned16(w) && (!out || aligned16(out)) && (!out_t || aligned16(out_t)) &&
+                 (!packed || aligned16(packed)) && (!packed_t || aligned16(packed_t)),
+             "convert_expert_weights_packed: null or unaligned buffer");
+  return launched(launch_convert_weights(w, num_matrices, rows, cols, out, out_t,
+                                         reinterpret_cast<hipStream_t>(stream), packed,
+                                         epilogue == NT_MOE_EPI_SWIGLU ? rows / 2 : 0, packed_t),
+                  "convert_expert_weights_packed");
+}
+
 int nt_moe_pack_expert_weights_bf16(const uint16_t* w, int64_t num_segments, int32_t rows,
                                     int32_t K, int32_t epilogue, uint16_t* packed,
                                     nt_moe_stream_t stream) {

@@ -137,7 +137,8 @@ hipError_t launch_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int6
                                            uint16_t* c, hipStream_t stream);
 int packed_gemm_min_k();
 hipError_t launch_convert_weights(const float* w, int64_t S, int R, int K, uint16_t* out,
-                                  uint16_t* out_t, hipStream_t stream);
+                                  uint16_t* out_t, hipStream_t stream, uint16_t* pk = nullptr,
+                                  int pk_swiglu_n = 0, uint16_t* pk_t = nullptr);
 hipError_t launch_grouped_gemm_bf16_t256(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                                          const int32_t* src_row, const int32_t* seg_offsets,
                                          int num_segments, int64_t total_rows, const uint16_t* w,

@@ -3,8 +3,9 @@
 // MasterLinear keeps fp32 masters and casts them to the activation dtype for every product
 // (megatron_moe.py:58-78, backbone.py:45-50); the backward's dgrad products need the transposes
 // (autograd of F.linear). After every optimizer update all of them are stale at once, so one
-// kernel reads each master exactly once and writes both the bf16 copy w [S, R, K] and the bf16
-// transpose w^T [S, K, R] (either may be skipped): a workgroup moves a 64 x 64 tile, the
+// kernel reads each master exactly once and writes any of the bf16 copy w [S, R, K], the bf16
+// transpose w^T [S, K, R], and both in the packed GEMM's fragment order (w with its epilogue's
+// row pairing, w^T as a plain projection), so no separate pack pass follows: a workgroup moves a 64 x 64 tile, the
 // transpose through LDS (row pitch 65 floats, so the column reads hit 64 different banks), every
 // global read and write a run of consecutive 16-byte (read) or 8-byte (write) pieces per row.
 #include "common.h"
@@ -14,10 +15,35 @@ namespace {
 
 constexpr int kCT = 64;  // tile edge
 
+// Packed (fragment-order) position of the 16-byte chunk holding K elements [kc, kc + 8) of row
+// `row` of a [S, R, K] weight stack, as the packed GEMM reads it: block (s, nb, kb) of 32 rows x
+// 64 K, chunk q * 64 + l with l = 32 h + block_row(i) for logical row i of the block and
+// K = kb * 64 + 32 h + 8 q. Logical row i of block nb is row 32 nb + i, or for SwiGLU
+// (swiglu_n = n_out > 0) gate row 16 nb + i (i < 16) and value row n_out + 16 nb + i - 16.
+__device__ __forceinline__ int64_t packed_chunk(int64_t s, int row, int kc, int R, int K,
+                                                int swiglu_n) {
+  int nb, i;
+  if (swiglu_n > 0) {
+    const bool val = row >= swiglu_n;
+    const int rr = val ? row - swiglu_n : row;
+    nb = rr >> 4;
+    i = (rr & 15) + (val ? 16 : 0);
+  } else {
+    nb = row >> 5;
+    i = row & 31;
+  }
+  const int kb = kc >> 6, kk = kc & 63, h = kk >> 5, q = (kk & 31) >> 3;
+  const int l = 32 * h + (i ^ (((i >> 2) ^ (i >> 3)) & 1) * 12);  // block_row(i), an involution
+  return ((s * (R / 32) + nb) * (int64_t)(K / 64) + kb) * 256 + q * 64 + l;
+}
+
 __global__ __launch_bounds__(256) void convert_weights_kernel(const float* __restrict__ w,
                                                               int64_t S, int R, int K,
                                                               uint16_t* __restrict__ out,
-                                                              uint16_t* __restrict__ out_t) {
+                                                              uint16_t* __restrict__ out_t,
+                                                              uint16_t* __restrict__ pk,
+                                                              int pk_swiglu_n,
+                                                              uint16_t* __restrict__ pk_t) {
   __shared__ float tile[kCT][kCT + 1];
   const int tiles_k = K / kCT, tiles_r = R / kCT;
   const int64_t b = blockIdx.x;
@@ -37,26 +63,50 @@ __global__ __launch_bounds__(256) void convert_weights_kernel(const float* __res
 #pragma unroll
     for (int j = 0; j < 4; ++j) tile[ty + 16 * i][4 * tx + j] = v[j];
   }
-  if (!out_t) return;
+  if (!out_t && !pk && !pk_t) return;
   __syncthreads();
-  uint16_t* dst = out_t + s * R * (int64_t)K;
+  if (out_t) {
+    uint16_t* dst = out_t + s * R * (int64_t)K;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int kk = ty + 16 * i;  // row of w^T within the tile
-    const u32x2 o = {pack_bf16x2(tile[4 * tx][kk], tile[4 * tx + 1][kk]),
-                     pack_bf16x2(tile[4 * tx + 2][kk], tile[4 * tx + 3][kk])};
-    *reinterpret_cast<u32x2*>(dst + (int64_t)(k0 + kk) * R + r0 + 4 * tx) = o;
+    for (int i = 0; i < 4; ++i) {
+      const int kk = ty + 16 * i;  // row of w^T within the tile
+      const u32x2 o = {pack_bf16x2(tile[4 * tx][kk], tile[4 * tx + 1][kk]),
+                       pack_bf16x2(tile[4 * tx + 2][kk], tile[4 * tx + 3][kk])};
+      *reinterpret_cast<u32x2*>(dst + (int64_t)(k0 + kk) * R + r0 + 4 * tx) = o;
+    }
+  }
+  // Packed w and packed w^T: the tile's 64 x 8 chunks of each, one 16-byte chunk per thread
+  // and pass, consecutive threads on consecutive rows (runs of consecutive packed chunks).
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int p = threadIdx.x + 256 * it, a = p & 63, c = p >> 6;
+    if (pk) {  // row r0 + a, K [k0 + 8 c, + 8)
+      const u32x4 o = {pack_bf16x2(tile[a][8 * c], tile[a][8 * c + 1]),
+                       pack_bf16x2(tile[a][8 * c + 2], tile[a][8 * c + 3]),
+                       pack_bf16x2(tile[a][8 * c + 4], tile[a][8 * c + 5]),
+                       pack_bf16x2(tile[a][8 * c + 6], tile[a][8 * c + 7])};
+      *reinterpret_cast<u32x4*>(pk + packed_chunk(s, r0 + a, k0 + 8 * c, R, K, pk_swiglu_n) * 8) =
+          o;
+    }
+    if (pk_t) {  // w^T [S, K, R]: row k0 + a, K [r0 + 8 c, + 8)
+      const u32x4 o = {pack_bf16x2(tile[8 * c][a], tile[8 * c + 1][a]),
+                       pack_bf16x2(tile[8 * c + 2][a], tile[8 * c + 3][a]),
+                       pack_bf16x2(tile[8 * c + 4][a], tile[8 * c + 5][a]),
+                       pack_bf16x2(tile[8 * c + 6][a], tile[8 * c + 7][a])};
+      *reinterpret_cast<u32x4*>(pk_t + packed_chunk(s, k0 + a, r0 + 8 * c, K, R, 0) * 8) = o;
+    }
   }
 }
 
 }  // namespace
 
 hipError_t launch_convert_weights(const float* w, int64_t S, int R, int K, uint16_t* out,
-                                  uint16_t* out_t, hipStream_t stream) {
+                                  uint16_t* out_t, hipStream_t stream, uint16_t* pk,
+                                  int pk_swiglu_n, uint16_t* pk_t) {
   const int64_t blocks = S * (int64_t)(R / kCT) * (K / kCT);
-  if (blocks == 0 || (!out && !out_t)) return hipSuccess;
+  if (blocks == 0 || (!out && !out_t && !pk && !pk_t)) return hipSuccess;
   hipLaunchKernelGGL(convert_weights_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, w, S,
-                     R, K, out, out_t);
+                     R, K, out, out_t, pk, pk_swiglu_n, pk_t);
   return hipGetLastError();
 }
 

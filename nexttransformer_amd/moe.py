@@ -356,7 +356,10 @@ class MoELayer(nn.Module):
             self._bw = ops.backward_weights(w["w1_plain"], w["w2_plain"], w["shared_w1_plain"],
                                             w["shared_w2_plain"], w["router_t"],
                                             w1_t=w["w1_t"], w2_t=w["w2_t"],
-                                            shared_w2_t=w["shared_w2_t"])
+                                            shared_w2_t=w["shared_w2_t"],
+                                            w1_t_packed=w["w1_t_packed"],
+                                            w2_t_packed=w["w2_t_packed"],
+                                            shared_w2_t_packed=w["shared_w2_t_packed"])
             self._bw_key = self._pack_key
         return self._bw
 
@@ -397,22 +400,26 @@ class MoELayer(nn.Module):
                 ops.prefers_packed(_round_up(h, align), dp, nat.EPI_NONE,
                                    repacked_each_step=keep_plain) for h in widths))
 
-            def stack(experts, hidden, pools=(None, None)):
+            def stack(experts, hidden, pools=(None, None), need_w1=False):
                 hp = _round_up(hidden, align)
                 if not fp8 and hp == hidden and dp == r.width and self.router.weight.is_cuda:
-                    # one pass over the fp32 masters: the bf16 copy (and, for the backward, its
-                    # transpose)
-                    w1, w1t = ops.convert_expert_weights.raw(
-                        _stacked(pools[0], [e.linear_fc1.weight for e in experts]), True,
-                        keep_plain)
-                    w2, w2t = ops.convert_expert_weights.raw(
-                        _stacked(pools[1], [e.linear_fc2.weight for e in experts]), True,
-                        keep_plain)
-                    plain.append((w1, w2, w1t if keep_plain else None,
-                                  w2t if keep_plain else None))
+                    # one pass over each fp32 master stack writes what the kernels read: the
+                    # packed or plain weights and, for the backward, the transposes (packed
+                    # when their dgrad projection takes the packed GEMM)
                     up = nat.EPI_SWIGLU if gated else nat.EPI_RELU2
-                    return (ops.pack_expert_weights.raw(w1, up) if pk_up else w1, None,
-                            ops.pack_expert_weights.raw(w2, nat.EPI_NONE) if pk_down else w2, None)
+                    rows1 = (2 if gated else 1) * hidden
+                    t1 = keep_plain and ops.prefers_packed(rows1, r.width, nat.EPI_NONE)
+                    t2 = keep_plain and ops.prefers_packed(r.width, hidden, nat.EPI_NONE)
+                    w1, w1t, w1p, w1tp = ops.convert_pack_expert_weights.raw(
+                        _stacked(pools[0], [e.linear_fc1.weight for e in experts]), up,
+                        not pk_up or need_w1, keep_plain and not t1, pk_up, t1)
+                    w2, w2t, w2p, w2tp = ops.convert_pack_expert_weights.raw(
+                        _stacked(pools[1], [e.linear_fc2.weight for e in experts]), nat.EPI_NONE,
+                        not pk_down, keep_plain and not t2, pk_down, t2)
+                    some = lambda t: t if t.numel() else None
+                    plain.append((some(w1), some(w2), some(w1t), some(w2t), some(w1tp),
+                                  some(w2tp)))
+                    return (w1p if pk_up else w1, None, w2p if pk_down else w2, None)
                 if hp == hidden and dp == r.width:
                     w1 = torch.stack([e.linear_fc1.weight.detach() for e in experts]).to(dtype)
                     w2 = torch.stack([e.linear_fc2.weight.detach() for e in experts]).to(dtype)
@@ -432,7 +439,7 @@ class MoELayer(nn.Module):
                 if not fp8:
                     up = nat.EPI_SWIGLU if gated else nat.EPI_RELU2
                     w1, w2 = w1.contiguous(), w2.contiguous()
-                    plain.append((w1, w2, None, None))
+                    plain.append((w1, w2, None, None, None, None))
                     return (ops.pack_expert_weights.raw(w1, up) if pk_up else w1, None,
                             ops.pack_expert_weights.raw(w2, nat.EPI_NONE) if pk_down else w2, None)
                 w1q, w1s = ops.quantize_fp8_blockwise(w1.contiguous())
@@ -453,12 +460,13 @@ class MoELayer(nn.Module):
                                          (self._fc1_pool, self._fc2_pool))
             if self.shared_experts is not None:
                 (packed["shared_w1"], packed["shared_w1_scale"], packed["shared_w2"],
-                 packed["shared_w2_scale"]) = stack([self.shared_experts], r.shared_expert_width)
+                 packed["shared_w2_scale"]) = stack([self.shared_experts], r.shared_expert_width,
+                                                     need_w1=True)
             if keep_plain and not fp8:
-                (packed["w1_plain"], packed["w2_plain"], packed["w1_t"],
-                 packed["w2_t"]) = plain[0]
-                (packed["shared_w1_plain"], packed["shared_w2_plain"], _,
-                 packed["shared_w2_t"]) = plain[1] if len(plain) > 1 else (None,) * 4
+                (packed["w1_plain"], packed["w2_plain"], packed["w1_t"], packed["w2_t"],
+                 packed["w1_t_packed"], packed["w2_t_packed"]) = plain[0]
+                (packed["shared_w1_plain"], packed["shared_w2_plain"], _, packed["shared_w2_t"],
+                 _, packed["shared_w2_t_packed"]) = plain[1] if len(plain) > 1 else (None,) * 6
             self._packed = packed
             self._pack_key = key
         return self._packed

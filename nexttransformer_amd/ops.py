@@ -331,6 +331,37 @@ def _(w, want_out, want_t):
             w.new_empty((S, K, R) if want_t else (0,), dtype=torch.bfloat16))
 
 
+@_custom_op("ntmoe::convert_pack_expert_weights")
+def convert_pack_expert_weights(w: Tensor, epilogue: int, want_out: bool, want_t: bool,
+                                want_packed: bool, want_packed_t: bool
+                                ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """fp32 [S, R, K] -> (bf16 w, bf16 w^T [S, K, R], w packed for `epilogue`, w^T packed as a
+    plain projection), each or an empty tensor, from one read of w; the packed ones equal
+    pack_expert_weights of the bf16 copies bit for bit."""
+    _on_gpu(w)
+    _require(w.dtype == torch.float32 and w.dim() == 3 and w.is_contiguous(),
+             "convert_pack_expert_weights: w must be contiguous fp32 [S, R, K]")
+    S, R, K = w.shape
+    mk = lambda want, shape: torch.empty(shape if want else (0,), device=w.device,
+                                         dtype=torch.bfloat16)
+    out, out_t = mk(want_out, (S, R, K)), mk(want_t, (S, K, R))
+    pk, pk_t = mk(want_packed, (S, R, K)), mk(want_packed_t, (S, K, R))
+    st = nat.load().nt_moe_convert_expert_weights_packed(
+        ptr(w), S, R, K, ptr(out) if want_out else None, ptr(out_t) if want_t else None,
+        ptr(pk) if want_packed else None, int(epilogue), ptr(pk_t) if want_packed_t else None,
+        _stream(w.device))
+    nat.check(st, "ntmoe::convert_pack_expert_weights")
+    return out, out_t, pk, pk_t
+
+
+@convert_pack_expert_weights.register_fake
+def _(w, epilogue, want_out, want_t, want_packed, want_packed_t):
+    S, R, K = w.shape
+    mk = lambda want, shape: w.new_empty(shape if want else (0,), dtype=torch.bfloat16)
+    return (mk(want_out, (S, R, K)), mk(want_t, (S, K, R)), mk(want_packed, (S, R, K)),
+            mk(want_packed_t, (S, K, R)))
+
+
 def packable(K, n_out, epilogue):
     """Whether a [*, n_out or 2 n_out, K] weight stack qualifies for the packed GEMM."""
     return K >= 256 and K % 64 == 0 and n_out % (16 if epilogue == nat.EPI_SWIGLU else 32) == 0
@@ -870,7 +901,10 @@ class Projection:
     """One dgrad / recompute GEMM's weights, c[r] = a_r . W_s^T with W [S, n, K] bf16: packed for
     the packed GEMM when the shape qualifies, else the plain grouped GEMM's operand."""
 
-    def __init__(self, w):
+    def __init__(self, w, prepacked=None):
+        if prepacked is not None:  # already in the packed layout (convert_pack_expert_weights)
+            self.packed, self.w = True, prepacked
+            return
         S, n, K = w.shape
         self.packed = prefers_packed(K, n, nat.EPI_NONE)
         self.w = pack_expert_weights.raw(w.contiguous(), nat.EPI_NONE) if self.packed else w.contiguous()
@@ -894,17 +928,25 @@ class BackwardWeights:
     """
 
     def __init__(self, w1, w2, shared_w1=None, shared_w2=None, w_router_t=None, w1_t=None,
-                 w2_t=None, shared_w2_t=None):
+                 w2_t=None, shared_w2_t=None, w1_t_packed=None, w2_t_packed=None,
+                 shared_w2_t_packed=None):
         self.w1_plain, self.w2_plain = w1, w2
         self.shared_w1, self.shared_w2 = shared_w1, shared_w2
         self.w_router_t = w_router_t
         # transposes already made (convert_expert_weights), else made here on first use
         self._t = dict(w1=w1_t, w2=w2_t, shared_w2=shared_w2_t)
+        # transposes already packed (convert_pack_expert_weights), used as they are
+        self._tp = dict(w1=w1_t_packed, w2=w2_t_packed, shared_w2=shared_w2_t_packed)
         self._cache = {}
 
     def _transposed(self, name, w):
         t = self._t.get(name)
         return t if t is not None else w.transpose(1, 2).contiguous()
+
+    def _projection_t(self, name, w):
+        """The dgrad projection over w^T: from its packed form when given, else from w^T."""
+        tp = self._tp.get(name)
+        return Projection(None, tp) if tp is not None else Projection(self._transposed(name, w))
 
     def _get(self, name, make):
         if name not in self._cache:
@@ -917,18 +959,18 @@ class BackwardWeights:
 
     @property
     def w1t(self):
-        return self._get("w1t", lambda: Projection(self._transposed("w1", self.w1_plain)))
+        return self._get("w1t", lambda: self._projection_t("w1", self.w1_plain))
 
     @property
     def w2t(self):
-        return self._get("w2t", lambda: Projection(self._transposed("w2", self.w2_plain)))
+        return self._get("w2t", lambda: self._projection_t("w2", self.w2_plain))
 
     @property
     def shared(self):
         if self.shared_w1 is None:
             return None
         return self._get("shared", lambda: dict(
-            w2t=Projection(self._transposed("shared_w2", self.shared_w2))))
+            w2t=self._projection_t("shared_w2", self.shared_w2)))
 
     @property
     def shared_w1_proj(self):

@@ -326,6 +326,27 @@ def test_convert_expert_weights_is_the_cast_and_its_transpose():
     assert torch.equal(only_t, out_t)
 
 
+@pytest.mark.parametrize("epilogue,R,K", [(0, 192, 320), (1, 320, 256), (2, 128, 384)],
+                         ids=["swiglu-R192-K320", "relu2-R320-K256", "plain-R128-K384"])
+def test_convert_pack_equals_convert_then_pack(epilogue, R, K):
+    """One pass over fp32 masters gives the plain copy, its transpose, the copy packed for the
+    epilogue and the transpose packed as a plain projection, equal bit for bit to
+    convert_expert_weights followed by pack_expert_weights (SwiGLU with n_out = 96: a 64-row tile
+    straddles the gate / value boundary)."""
+    from nexttransformer_amd import _native as nat, ops
+    g = torch.Generator().manual_seed(61 + epilogue)
+    w = torch.randn(3, R, K, generator=g).cuda()
+    out, out_t = ops.convert_expert_weights(w, True, True)
+    a, at, p, pt = ops.convert_pack_expert_weights(w, epilogue, True, True, True, True)
+    ref_p = ops.pack_expert_weights(out, epilogue)
+    ref_pt = ops.pack_expert_weights(out_t, nat.EPI_NONE)
+    only = ops.convert_pack_expert_weights(w, epilogue, False, False, True, False)
+    torch.cuda.synchronize()
+    eq = lambda x, y: torch.equal(x.view(torch.int16), y.view(torch.int16))
+    assert eq(a, out) and eq(at, out_t) and eq(p, ref_p) and eq(pt, ref_pt) and eq(only[2], ref_p)
+    assert only[0].numel() == 0 and only[1].numel() == 0 and only[3].numel() == 0
+
+
 def test_module_keeps_masters_in_one_buffer_and_falls_back_when_replaced():
     """The experts' fp32 masters are slices of one buffer (the weight cast reads it without a
     stack); an expert whose weight tensor is replaced is still used, through a stacked copy."""
