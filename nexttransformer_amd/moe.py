@@ -388,17 +388,22 @@ class MoELayer(nn.Module):
             dtype = torch.float32 if fp8 else torch.bfloat16
             # The packed-weight GEMM (fragment-ordered weights streamed into registers) for a
             # projection when its K and width qualify for every expert kind (routed, shared) and
-            # the weights live on the GPU; fp8 always. (The T3 cell: the up projection packed,
-            # K = 1280; the down projection, K = 320, packed for inference, plain in training.)
+            # the weights live on the GPU; fp8 always. (The T3 cell: both projections packed,
+            # the down projection's K = 320 on the kernel's odd K-step path.)
             widths = [r.expert_width] + ([r.shared_expert_width] if self.shared_experts else [])
             on_gpu = self.router.weight.is_cuda
-            # training (keep_plain) repacks after every update; inference packs once
+            # Training (keep_plain) rebuilds these after every update. Where the conversion
+            # pass writes the packed layout itself (bf16, no padding, on the GPU) packing costs
+            # nothing extra; elsewhere it is a second pass, worth it only for even K-step counts.
+            fused = (not fp8 and on_gpu and dp == r.width
+                     and all(_round_up(h, align) == h for h in widths))
+            extra_pass = keep_plain and not fused
             pk_up = fp8 or (on_gpu and all(ops.prefers_packed(
                 dp, _round_up(h, align), nat.EPI_SWIGLU if gated else nat.EPI_RELU2,
-                repacked_each_step=keep_plain) for h in widths))
+                repacked_each_step=extra_pass) for h in widths))
             pk_down = fp8 or (on_gpu and all(
                 ops.prefers_packed(_round_up(h, align), dp, nat.EPI_NONE,
-                                   repacked_each_step=keep_plain) for h in widths))
+                                   repacked_each_step=extra_pass) for h in widths))
 
             def stack(experts, hidden, pools=(None, None), need_w1=False):
                 hp = _round_up(hidden, align)
@@ -408,8 +413,10 @@ class MoELayer(nn.Module):
                     # when their dgrad projection takes the packed GEMM)
                     up = nat.EPI_SWIGLU if gated else nat.EPI_RELU2
                     rows1 = (2 if gated else 1) * hidden
-                    t1 = keep_plain and ops.prefers_packed(rows1, r.width, nat.EPI_NONE)
-                    t2 = keep_plain and ops.prefers_packed(r.width, hidden, nat.EPI_NONE)
+                    t1 = keep_plain and ops.prefers_packed(rows1, r.width, nat.EPI_NONE,
+                                                           repacked_each_step=False)
+                    t2 = keep_plain and ops.prefers_packed(r.width, hidden, nat.EPI_NONE,
+                                                           repacked_each_step=False)
                     w1, w1t, w1p, w1tp = ops.convert_pack_expert_weights.raw(
                         _stacked(pools[0], [e.linear_fc1.weight for e in experts]), up,
                         not pk_up or need_w1, keep_plain and not t1, pk_up, t1)
