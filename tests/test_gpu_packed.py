@@ -197,6 +197,42 @@ def test_packed_equals_plain_random_shapes(seed):
     assert torch.equal(packed.view(torch.int16), plain.view(torch.int16)), (K, n_out, S, epilogue)
 
 
+_EIGHT_WAVE_CHECK = r"""
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+from nexttransformer_amd import ops
+g = torch.Generator().manual_seed(5)
+for epilogue, K, n_out in [(0, 1024, 512), (1, 512, 256), (2, 512, 1024)]:
+    counts = torch.tensor([700, 0, 1300, 90, 2500])
+    seg = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)]).to(torch.int32).cuda()
+    rows = int(counts.sum())
+    R = 2 * n_out if epilogue == 0 else n_out
+    a = torch.randn(3000, K, generator=g).to(torch.bfloat16).cuda()
+    src = torch.randint(0, 3000, (rows,), generator=g, dtype=torch.int32).cuda()
+    w = (torch.randn(5, R, K, generator=g) * 0.05).to(torch.bfloat16).cuda()
+    p = ops.grouped_gemm_packed(a, src, seg, ops.pack_expert_weights(w, epilogue), epilogue, rows)
+    q = ops.grouped_gemm(a, src, seg, w, epilogue, rows)
+    torch.cuda.synchronize()
+    assert torch.equal(p.view(torch.int16), q.view(torch.int16)), (epilogue, K, n_out)
+print("eight-wave ok")
+"""
+
+
+def test_eight_wave_shape_matches_plain():
+    # NT_MOE_PACKED_WAVES=8 (read once per process, so in a child process): one 8-wave
+    # workgroup per CU with 256-token tiles, its own epilogue transpose geometry (one weight
+    # block per wave); outputs equal the plain-weight kernel's bit for bit.
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = str(Path(__file__).resolve().parents[1])
+    env = dict(os.environ, NT_MOE_PACKED_WAVES="8")
+    r = subprocess.run([sys.executable, "-c", _EIGHT_WAVE_CHECK, root], env=env,
+                       capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0 and "eight-wave ok" in r.stdout, r.stdout + r.stderr
+
+
 PACKED_CASES = [
     Case("cfg1-shape", 512, 256, 8, 2, 512),
     Case("ragged-T1000-E32-k4", 1000, 1024, 32, 4, 512, seed=1),
