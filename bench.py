@@ -4,6 +4,9 @@
 
 A step is one full MoE layer forward (router -> histogram/scan -> permute plan -> grouped
 expert GEMMs -> combine + aux loss) over one batch of synthetic input already resident in HBM.
+Before the W warm-up steps, untimed forwards run for --settle-ms of wall time (default 300 ms):
+the GPU raises its clocks only under sustained load, and without them a short run such as
+--steps 20 --warmup 5 times its forwards 8-11 % slower than a settled one (measured side by side).
 Default workload: config 2 (T=16384 = 8 x 2048, d=1024, 32 experts, top-4 softmax, SwiGLU H=512,
 bf16, dropless). Configs 1-4 run the bf16 path; config 5 (T=64, d=4096, 128 experts, top-8,
 H=1536) runs the fp8 path (e4m3 weights with 128 x 128 block scales, activations quantised per
@@ -102,6 +105,11 @@ def parse():
                    help="time the up-projection launch with HIP events in every N-th timed "
                         "forward (each event record idles the stream about 6 us)")
     p.add_argument("--warmup", type=int, default=50)
+    p.add_argument("--settle-ms", type=float, default=300.0,
+                   help="before the warm-up steps, run forwards for at least this long (wall "
+                        "time): the GPU raises its clocks only after some milliseconds of load, "
+                        "so without it a short run (--steps 20 --warmup 5) times the first "
+                        "forwards at low clocks, 8-11 %% slower than a settled run")
     p.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5, 6],
                    help="1-5: the benchmark configurations; 6: the registered T3 expert cell "
                         "(moe-T3-L20 shapes) on 16384 tokens")
@@ -550,6 +558,14 @@ def main():
         return
 
     state = None
+    settle_n = 0
+    if args.settle_ms > 0:
+        t_settle = time.perf_counter()
+        while (time.perf_counter() - t_settle) * 1e3 < args.settle_ms:
+            for _ in range(10):
+                forward()
+            settle_n += 10
+            torch.cuda.synchronize()
     for _ in range(max(1, args.warmup)):
         _, _, state = forward()
     torch.cuda.synchronize()
@@ -674,6 +690,7 @@ def main():
         "expert_load_max_over_mean": round(load_ratio, 3),
         "stages_ms": stage,
         "launch": "eager" if graphs is None else "hip_graph_replay",
+        "settle": {"ms": args.settle_ms, "forwards": settle_n},
         "graph_replay_matches_eager": replay_ok,
     }
     if not args.no_cpu_baseline:

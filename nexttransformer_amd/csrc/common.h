@@ -136,6 +136,14 @@ hipError_t launch_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int6
                                            const uint16_t* wp, int K, int n_out, int epilogue,
                                            uint16_t* c, hipStream_t stream);
 int packed_gemm_min_k();
+// The ping-pong packed GEMM (grouped_gemm_pp.hip): same operands and results as the packed
+// kernel; pre (the fc1 pre-activations, SWIGLU / RELU2 only) may be null.
+bool pp_gemm_supported(int K, int num_segments);
+hipError_t launch_grouped_gemm_bf16_pp(const uint16_t* a, int64_t ld_a, int64_t a_rows,
+                                       const int32_t* src_row, const int32_t* seg_offsets,
+                                       int num_segments, int64_t total_rows, const uint16_t* wp,
+                                       int K, int n_out, int epilogue, uint16_t* c, uint16_t* pre,
+                                       hipStream_t stream);
 hipError_t launch_convert_weights(const float* w, int64_t S, int R, int K, uint16_t* out,
                                   uint16_t* out_t, hipStream_t stream, uint16_t* pk = nullptr,
                                   int pk_swiglu_n = 0, uint16_t* pk_t = nullptr);

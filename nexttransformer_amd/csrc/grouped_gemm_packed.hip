@@ -668,6 +668,15 @@ hipError_t launch_packed(const uint16_t* a, int64_t ld_a, int64_t a_rows, const 
   return hipGetLastError();
 }
 
+// Whether the ping-pong kernel serves the packed entry points (NT_MOE_GEMM_PP=1).
+bool use_pp() {
+  static const bool v = [] {
+    const char* s = getenv("NT_MOE_GEMM_PP");
+    return s && atoi(s) == 1;
+  }();
+  return v;
+}
+
 // Workgroup shape of the packed kernel: 4 (two workgroups per CU) unless NT_MOE_PACKED_WAVES=8.
 int packed_waves() {
   static const int w = [] {
@@ -704,6 +713,9 @@ hipError_t launch_grouped_gemm_bf16_packed(const uint16_t* a, int64_t ld_a, int6
                                            const uint16_t* wp, int K, int n_out, int epilogue,
                                            uint16_t* c, hipStream_t stream) {
   if (total_rows == 0) return hipSuccess;
+  if (use_pp() && pp_gemm_supported(K, num_segments))
+    return launch_grouped_gemm_bf16_pp(a, ld_a, a_rows, src_row, seg_offsets, num_segments,
+                                       total_rows, wp, K, n_out, epilogue, c, nullptr, stream);
   const bool edge = packed_edge(K, n_out, epilogue);
 #define NT_PW(EPI, W, EDGE)                                                                   \
   return src_row ? launch_packed<EPI, true, W, false, EDGE>(a, ld_a, a_rows, src_row,         \
@@ -738,6 +750,9 @@ hipError_t launch_grouped_gemm_bf16_packed_keep(const uint16_t* a, int64_t ld_a,
                                                 int n_out, int epilogue, uint16_t* c,
                                                 uint16_t* pre, hipStream_t stream) {
   if (total_rows == 0) return hipSuccess;
+  if (use_pp() && pp_gemm_supported(K, num_segments))
+    return launch_grouped_gemm_bf16_pp(a, ld_a, a_rows, src_row, seg_offsets, num_segments,
+                                       total_rows, wp, K, n_out, epilogue, c, pre, stream);
   const bool edge = packed_edge(K, n_out, epilogue);
 #define NT_PKE(EPI, EDGE)                                                                    \
   return src_row ? launch_packed<EPI, true, 4, true, EDGE>(a, ld_a, a_rows, src_row,         \

@@ -233,6 +233,58 @@ def test_eight_wave_shape_matches_plain():
     assert r.returncode == 0 and "eight-wave ok" in r.stdout, r.stdout + r.stderr
 
 
+_PP_CHECK = r"""
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+from nexttransformer_amd import _native as nat, ops
+g = torch.Generator().manual_seed(7)
+n = 0
+for counts in ([0, 300, 1, 256, 0, 513, 40], [512, 512, 512, 512], [3000, 17, 0, 1200]):
+    for K in (256, 320, 1024):
+        for epilogue, n_out in ((0, 192), (0, 512), (1, 448), (1, 320), (2, 448), (2, 1024)):
+            for gather in (False, True):
+                ct = torch.tensor(counts)
+                seg = torch.cat([torch.zeros(1, dtype=torch.long), ct.cumsum(0)]).to(torch.int32).cuda()
+                rows, S = int(ct.sum()), len(counts)
+                R = 2 * n_out if epilogue == 0 else n_out
+                a_rows = 3500 if gather else rows
+                a = torch.randn(a_rows, K, generator=g).to(torch.bfloat16).cuda()
+                src = (torch.randint(0, a_rows, (rows,), generator=g, dtype=torch.int32).cuda()
+                       if gather else None)
+                w = (torch.randn(S, R, K, generator=g) * 0.05).to(torch.bfloat16).cuda()
+                wp = ops.pack_expert_weights(w, epilogue)
+                p = ops.grouped_gemm_packed(a, src, seg, wp, epilogue, rows)
+                q = ops.grouped_gemm(a, src, seg, w, epilogue, rows)
+                torch.cuda.synchronize()
+                assert torch.equal(p.view(torch.int16), q.view(torch.int16)), (counts, K, epilogue, n_out, gather)
+                if epilogue != 2:  # the fc1 pre-activations equal the plain product's bf16 bits
+                    c, pre = ops.grouped_gemm_packed_keep(a, src, seg, wp, epilogue, rows)
+                    z = ops.grouped_gemm(a, src, seg, w, nat.EPI_NONE, rows)
+                    torch.cuda.synchronize()
+                    assert torch.equal(c.view(torch.int16), q.view(torch.int16))
+                    assert torch.equal(pre.view(torch.int16), z.view(torch.int16)), (counts, K, epilogue)
+                n += 1
+print("ping-pong ok", n)
+"""
+
+
+def test_ping_pong_kernel_matches_plain():
+    # NT_MOE_GEMM_PP=1 (read once per process, so in a child process): the packed entry points
+    # run the two-group ping-pong kernel (256 x 256 tiles, both operands staged in LDS). Its
+    # outputs and kept pre-activations equal the plain-weight kernel's bit for bit on empty,
+    # single-row, exact and multi-tile segments, partial N tiles (last tiles of 2, 4 and 6 weight
+    # blocks), odd K-step counts, with and without the row gather.
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = str(Path(__file__).resolve().parents[1])
+    env = dict(os.environ, NT_MOE_GEMM_PP="1")
+    r = subprocess.run([sys.executable, "-c", _PP_CHECK, root], env=env,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and "ping-pong ok" in r.stdout, r.stdout + r.stderr
+
+
 PACKED_CASES = [
     Case("cfg1-shape", 512, 256, 8, 2, 512),
     Case("ragged-T1000-E32-k4", 1000, 1024, 32, 4, 512, seed=1),
