@@ -31,9 +31,21 @@ a master changes (tracked by the tensors' version counters, which in-place optim
 bump).
 
 Under autograd the layer runs its training path (_MoETrain: the forward keeps what the HIP
-backward reads, and the gradients reach hidden and every fp32 master) for bf16 experts whose
-widths are multiples of 64; other configurations raise RuntimeError there instead of returning a
-result without a graph. There is no CPU path.
+backward reads, and the gradients reach hidden and every fp32 master) for bf16 experts of any
+width (widths that are not multiples of 64 run zero-padded); fp8 experts raise RuntimeError there
+instead of returning a result without a graph. There is no CPU path.
+
+Expert weight gradients (the `expert_grad` mode): with "accumulate" (the default) the backward
+adds the routed experts' gradients into their .grad itself, whatever the caller asked autograd
+for -- also under torch.autograd.grad(out, hidden) or loss.backward(inputs=[hidden]) -- and
+per-parameter gradient hooks do not fire for them; this saves autograd's per-tensor work (about
+a millisecond per backward at 256 experts). With "autograd" the expert masters are ordinary
+inputs of the layer's autograd function: torch.autograd.grad can name them, `inputs=` is
+honoured and hooks fire.
+
+Weight caches: the bf16 / packed / fp8 operands are rebuilt when a master's address or version
+counter changes. An update that does not bump the counter (a write through .data, or into the
+storage from outside PyTorch) must be followed by invalidate_weights().
 """
 import math
 
@@ -46,6 +58,7 @@ from nexttransformer_amd.moe_recipe import MoERecipe
 
 SEED_LAYER_STRIDE = 100003  # megatron_moe.py:113-120: seed + 100003 * layer_number + index
 AUX_GRAD_MODES = ("inject", "loss")
+EXPERT_GRAD_MODES = ("accumulate", "autograd")
 
 # Scale of the injected aux-loss gradient (MCore's MoEAuxLossAutoScaler main-loss scale), set by
 # set_aux_loss_scale() before backward and read when the backward runs.
@@ -155,11 +168,14 @@ class _MoETrain(torch.autograd.Function):
     inputs after x are router.weight and the shared expert's fp32 masters, so autograd hands
     each its own gradient; the bf16 operands the kernels read are the layer's cached copies of
     the masters (MasterLinear casts its master per call, megatron_moe.py:58-78; the cache is
-    rebuilt when a master changes). The routed experts' masters (two per expert) are not inputs:
-    autograd's per-input bookkeeping costs a few microseconds per tensor (over a millisecond per
-    step at 256 experts), so the backward sets their .grad itself from one fp32 stack per
-    projection (MoELayer._accumulate_expert_grads); `anchor`, an empty tensor that requires
-    grad, keeps the backward in the graph when nothing else does."""
+    rebuilt when a master changes). With expert_grad "accumulate" (the default) the routed
+    experts' masters (two per expert) are not inputs: autograd's per-input bookkeeping costs a
+    few microseconds per tensor (over a millisecond per step at 256 experts), so the backward
+    adds their gradients to .grad itself, from one fp32 stack per projection
+    (MoELayer._accumulate_expert_grads); with "autograd" they are inputs like the others.
+    `anchor`, an empty tensor that requires grad, keeps the backward in the graph when nothing
+    else does. x and the weights may be zero-padded to widths the kernels take (MoELayer.
+    packed_weights); the gradients handed back have the masters' shapes."""
 
     @staticmethod
     def forward(ctx, x, cfg, anchor, *masters):
@@ -190,10 +206,15 @@ class _MoETrain(torch.autograd.Function):
                              aux_coeff=cfg["aux_coeff"], z_coeff=cfg["z_coeff"],
                              weight_grads_fp32=True)
         ctx.state = ctx.x = ctx.w = None
-        pooled = layer._masters(pooled_only=True)  # fc1, fc2 of expert 0, then expert 1, ...
-        layer._accumulate_expert_grads(pooled[0::2], g["w1"])
-        layer._accumulate_expert_grads(pooled[1::2], g["w2"])
+        g = layer._unpadded_grads(g)
         grads = [g["x"], None, None, g["router"]]
+        if cfg["expert_autograd"]:  # fc1, fc2 of expert 0, then expert 1, ... as inputs
+            for a, b in zip(g["w1"].unbind(0), g["w2"].unbind(0)):
+                grads += [a, b]
+        else:
+            pooled = layer._masters(pooled_only=True)  # fc1, fc2 of expert 0, then expert 1, ...
+            layer._accumulate_expert_grads(pooled[0::2], g["w1"])
+            layer._accumulate_expert_grads(pooled[1::2], g["w2"])
         if g["shared_w1"] is not None:
             grads += [g["shared_w1"][0], g["shared_w2"][0]]
         return tuple(grads)
@@ -206,11 +227,13 @@ class MoELayer(nn.Module):
     """
 
     def __init__(self, recipe, layer_number: int, pg_collection=None, *, device=None,
-                 aux_grad="inject"):
+                 aux_grad="inject", expert_grad="accumulate"):
         super().__init__()
         recipe = MoERecipe.from_any(recipe)
         if aux_grad not in AUX_GRAD_MODES:
             raise ValueError(f"aux_grad must be one of {AUX_GRAD_MODES}")
+        if expert_grad not in EXPERT_GRAD_MODES:
+            raise ValueError(f"expert_grad must be one of {EXPERT_GRAD_MODES}")
         if layer_number < 1:
             raise ValueError("layer_number counts from one")
         if _ep_size(pg_collection) != 1:
@@ -225,6 +248,7 @@ class MoELayer(nn.Module):
         self.recipe = recipe
         self.layer_number = layer_number
         self.aux_grad = aux_grad
+        self.expert_grad = expert_grad
         gated = recipe.activation == "swiglu"
         self.router = Router(recipe.routed_experts, recipe.width, device)
         self.experts = LocalExperts(recipe.routed_experts, recipe.width, recipe.expert_width,
@@ -244,8 +268,6 @@ class MoELayer(nn.Module):
         self.last_aux_parts = None
         self._pack_key = None
         self._packed = None
-        self._bw_key = None
-        self._bw = None
         self.reset_parameters()
 
     # -- initialisation --------------------------------------------------------------------
@@ -272,8 +294,16 @@ class MoELayer(nn.Module):
         w = torch.empty(self.router.weight.shape, dtype=torch.float32, device="cpu")
         nn.init.normal_(w, std=r.router_init_std, generator=_seeded(base + r.routed_experts + 1))
         self.router.weight.copy_(w)
+        self.invalidate_weights()
+
+    def invalidate_weights(self):
+        """Drops the cached kernel operands (bf16 / packed / fp8 copies of the masters and the
+        backward's transposes), so the next forward rebuilds them from the masters. The cache
+        follows each master's address and version counter, which in-place updates bump
+        (torch.optim steps, copy_ / add_ under no_grad); an update that bypasses the counter
+        (writes through .data, or into the storage from outside PyTorch) must call this."""
         self._pack_key = None
-        self._bw_key = None
+        self._packed = None
 
     # -- expert weight gradients -----------------------------------------------------------
 
@@ -350,18 +380,48 @@ class MoELayer(nn.Module):
 
     @torch.no_grad()
     def backward_weights(self, w):
-        """The backward's GEMM operands for the cached weights `w` (packed_weights(keep_plain=
-        True)), built once per weight version (each operand on first use)."""
-        if self._bw_key is not self._pack_key or self._bw is None:
-            self._bw = ops.backward_weights(w["w1_plain"], w["w2_plain"], w["shared_w1_plain"],
+        """The backward's GEMM operands for the weights `w` (packed_weights(keep_plain=True))
+        a forward used, kept in `w` itself, so a backward always uses operands built from its
+        own forward's weights (each operand on first use)."""
+        if "_bw" not in w:
+            w["_bw"] = ops.backward_weights(w["w1_plain"], w["w2_plain"], w["shared_w1_plain"],
                                             w["shared_w2_plain"], w["router_t"],
                                             w1_t=w["w1_t"], w2_t=w["w2_t"],
                                             shared_w2_t=w["shared_w2_t"],
                                             w1_t_packed=w["w1_t_packed"],
                                             w2_t_packed=w["w2_t_packed"],
                                             shared_w2_t_packed=w["shared_w2_t_packed"])
-            self._bw_key = self._pack_key
-        return self._bw
+        return w["_bw"]
+
+    def _unpadded_grads(self, g):
+        """moe_backward's gradients of the zero-padded operands (x [T, dp], router [E, dp],
+        fc1 [E, (2) Hp, dp], fc2 [E, dp, Hp], the shared expert's likewise) cut back to the
+        masters' shapes: the padding entries are constants, so the masters' gradients are the
+        padded gradients' entries at the masters' positions (for SwiGLU, fc1's value half starts
+        at row Hp)."""
+        r = self.recipe
+        d = r.width
+        gated = r.activation == "swiglu"
+
+        def fc1(t, hidden):
+            hp = t.shape[1] // (2 if gated else 1)
+            if hp == hidden and t.shape[2] == d:
+                return t
+            if gated:
+                return torch.cat([t[:, :hidden, :d], t[:, hp:hp + hidden, :d]], 1)
+            return t[:, :hidden, :d].contiguous()
+
+        def fc2(t, hidden):
+            return t if tuple(t.shape[1:]) == (d, hidden) else t[:, :d, :hidden].contiguous()
+
+        out = dict(g)
+        if g["router"].shape[1] != d:
+            out["router"] = g["router"][:, :d].contiguous()
+        out["w1"], out["w2"] = fc1(g["w1"], r.expert_width), fc2(g["w2"], r.expert_width)
+        if g["shared_w1"] is not None:
+            out["shared_w1"] = fc1(g["shared_w1"], r.shared_expert_width)
+            out["shared_w2"] = fc2(g["shared_w2"], r.shared_expert_width)
+        return out
 
     @torch.no_grad()
     def packed_weights(self, keep_plain=False):
@@ -518,22 +578,31 @@ class MoELayer(nn.Module):
 
 
     def _forward_train(self, hidden):
-        """Forward with gradients to hidden and every master (bf16 experts)."""
+        """Forward with gradients to hidden and every master (bf16 experts). Widths that are not
+        multiples of 64 (the reference's debug recipe: d = 32, expert width 8) run zero-padded,
+        as the inference forward does; the gradients come back in the masters' shapes."""
         r = self.recipe
-        widths = [r.width, r.expert_width] + (
-            [r.shared_expert_width] if self.shared_experts is not None else [])
-        if r.expert_dtype == "fp8" or any(w % 64 for w in widths):
-            raise RuntimeError("the MoE backward covers bf16 experts whose widths are multiples "
-                               "of 64; run this configuration under torch.no_grad()")
+        if r.expert_dtype == "fp8":
+            raise RuntimeError("the MoE backward covers bf16 experts; run fp8 experts under "
+                               "torch.no_grad()")
         if not self.router.weight.is_cuda:
             raise ValueError("the MoE layer runs on the GPU only (no CPU path)")
-        x = hidden.reshape(-1, r.width).to(torch.bfloat16).contiguous()
+        x = hidden.reshape(-1, r.width).to(torch.bfloat16)
+        dp = _round_up(r.width, 64)
+        if dp != r.width:
+            x = nn.functional.pad(x, (0, dp - r.width))
+        x = x.contiguous()
         inject = self.aux_grad == "inject"
+        autograd_experts = self.expert_grad == "autograd"
         cfg = dict(layer=self, top_k=r.top_k, score_fn=_SCORE[r.score_function],
                    activation=_ACT[r.activation], aux_coeff=r.aux_loss_coeff,
-                   z_coeff=r.z_loss_coeff, inject=inject and self.training)
+                   z_coeff=r.z_loss_coeff, inject=inject and self.training,
+                   expert_autograd=autograd_experts)
         anchor = torch.empty(0, device=x.device, requires_grad=True)
-        out, aux = _MoETrain.apply(x, cfg, anchor, *self._masters(skip_pooled=True))
+        masters = self._masters(skip_pooled=not autograd_experts)
+        out, aux = _MoETrain.apply(x, cfg, anchor, *masters)
+        if dp != r.width:
+            out = out[:, :r.width]
         self.last_load = cfg["counts"].to(torch.int64)
         self.last_aux_parts = aux.detach()
         # "inject": the gradient comes from the backward itself, so the returned value is

@@ -924,7 +924,8 @@ class BackwardWeights:
       first        the token-side first row's operand: [W1s^T | Wr_hi^T | Wr_lo^T | Wr_hi^T]
                    (K padded to 64), so that one GEMM over [dfc1s | g_hi | g_hi | g_lo] gives the
                    shared expert's input gradient plus grad_logits . Wr in fp32 (the router's
-                   input gradient; g = grad_logits, hi/lo its exact bf16 split) rounded once
+                   input gradient; g = grad_logits, hi/lo its two-term bf16 split, hi + lo
+                   within about 2^-17 |g| of g) rounded once
     """
 
     def __init__(self, w1, w2, shared_w1=None, shared_w2=None, w_router_t=None, w1_t=None,
@@ -933,6 +934,17 @@ class BackwardWeights:
         self.w1_plain, self.w2_plain = w1, w2
         self.shared_w1, self.shared_w2 = shared_w1, shared_w2
         self.w_router_t = w_router_t
+
+        def plain_shape(plain, *transposed):  # [S, rows, cols] of the weight the forward used
+            if plain is not None:
+                return tuple(plain.shape)
+            t = next((t for t in transposed if t is not None), None)
+            return None if t is None else (t.shape[0], t.shape[2], t.shape[1])
+        # the weight gradients' shapes (what an empty batch returns zeros of)
+        self.shapes = dict(w1=plain_shape(w1, w1_t, w1_t_packed),
+                           w2=plain_shape(w2, w2_t, w2_t_packed),
+                           shared_w1=plain_shape(shared_w1),
+                           shared_w2=plain_shape(shared_w2, shared_w2_t, shared_w2_t_packed))
         # transposes already made (convert_expert_weights), else made here on first use
         self._t = dict(w1=w1_t, w2=w2_t, shared_w2=shared_w2_t)
         # transposes already packed (convert_pack_expert_weights), used as they are
@@ -1019,7 +1031,8 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
     grad_logits . Wr, comes from one grouped GEMM over the concatenated K of BackwardWeights'
     `first` operand), and every weight gradient on grouped_wgrad: dy^T h and d_fc1^T x over each
     expert's rows (x gathered through src_row), the shared expert's over all T rows and the
-    router's grad_logits^T x (fp32: the exact bf16 split of grad_logits, fp32 output), the last
+    router's grad_logits^T x (fp32 output over the two-term bf16 split of grad_logits, which
+    carries g to about 2^-17 |g|; the router gradients are checked against fp64), the last
     two split along T in fixed order. `mark(name)` as in moe_forward.
     """
     mark = mark or (lambda name: None)
@@ -1028,11 +1041,12 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
     k = top_k
     A = T * k
     sh = bw.shared_w1 is not None
-    if T == 0:
-        z = lambda t: None if t is None else torch.zeros_like(t)
+    if T == 0:  # no rows: every gradient is zero
+        wdt = torch.float32 if weight_grads_fp32 else torch.bfloat16
+        z = lambda shape: None if shape is None else torch.zeros(shape, device=x.device, dtype=wdt)
         return dict(x=torch.zeros_like(x), router=torch.zeros(E, d, device=x.device),
-                    w1=z(bw.w1_plain), w2=z(bw.w2_plain), shared_w1=z(bw.shared_w1),
-                    shared_w2=z(bw.shared_w2))
+                    w1=z(bw.shapes["w1"]), w2=z(bw.shapes["w2"]),
+                    shared_w1=z(bw.shapes["shared_w1"]), shared_w2=z(bw.shapes["shared_w2"]))
     src, offsets = state["src_row"], state["offsets"]
     cdest, ids = state["combine_dest"], state["ids"]
     g = grad_out.to(torch.bfloat16).contiguous()

@@ -93,6 +93,20 @@ def test_aux_only_layer_gradients(score_fn):
         z = z_coeff * torch.logsumexp(L, -1).square().mean()
         ((ga[0] + ga[1]) * lb + (ga[0] + ga[2]) * z).backward()
         assert rel_l2(res["router"].cpu(), wr.grad) <= 1e-4, ga
+        # the same router gradient in float64: the two-term bf16 split of grad_logits keeps it
+        # at fp32 accuracy (each element within about 2^-17 of |g|), far inside 2e-5
+        x64 = cpu["x"].double()
+        w64 = cpu["router"].double().clone().requires_grad_()
+        L = x64 @ w64.t()
+        if score_fn == 0:
+            p = L.softmax(-1)
+        else:
+            s = torch.sigmoid(L)
+            p = s / s.sum(-1, keepdim=True)
+        lb = aux_coeff * case.E / (case.k * case.T ** 2) * (p.sum(0) * counts.double()).sum()
+        z = z_coeff * torch.logsumexp(L, -1).square().mean()
+        ((ga[0] + ga[1]) * lb + (ga[0] + ga[2]) * z).backward()
+        assert rel_l2(res["router"].cpu().double(), w64.grad) <= 2e-5, ga
         assert rel_l2(res["x"].float().cpu(), xr.grad) <= 1e-2, ga  # dx is stored in bf16
         assert float(res["w1"].float().abs().max()) == 0.0
 
@@ -217,11 +231,20 @@ def test_adapter_from_reference_recipe_matches_oracle():
     assert torch.equal(ffn.engine.last_load.cpu(), want["counts"].long())
 
 
+# the reference's debug recipe (moe_recipe.py:128-133: width 32, 2 heads, 8 experts, top-2,
+# expert width 8; ReLU^2 with one shared expert of width 8) trains zero-padded to 64
+DEBUG_RECIPE = dict(layers=3, width=32, heads=2, vocab_size=64, sequence_len=8, routed_experts=8,
+                    top_k=2, expert_width=8, global_batch_tokens=32)
+
+
 @pytest.mark.parametrize("kw", [
     dict(),
     dict(activation="swiglu", score_function="sigmoid", shared_experts=0, expert_width=128,
          allow_any_expert_width=True),
-], ids=["relu2-shared", "swiglu-sigmoid"])
+    DEBUG_RECIPE,
+    dict(DEBUG_RECIPE, activation="swiglu", expert_width=24, allow_any_expert_width=True,
+         shared_expert_width=40),
+], ids=["relu2-shared", "swiglu-sigmoid", "debug-recipe", "debug-swiglu-odd-widths"])
 def test_module_training_gradients_match_fp32_autograd(kw):
     """Every parameter's .grad and hidden.grad from MoELayer (loss mode) against fp32 autograd
     of the layer restated in PyTorch with the same selection: checks the training glue (expert
@@ -266,3 +289,74 @@ def test_module_training_gradients_match_fp32_autograd(kw):
         assert rel_l2(m.shared_experts.linear_fc1.weight.grad.cpu(), ref[4][0]) <= 2e-2
         assert rel_l2(m.shared_experts.linear_fc2.weight.grad.cpu(), ref[5][0]) <= 2e-2
     assert all(p.grad.dtype == torch.float32 for p in m.parameters())
+
+
+def test_module_empty_batch_trains():
+    """A batch of no tokens in training mode: the forward returns an empty output and the
+    backward zero gradients of the masters' shapes (fp32), for both expert-gradient modes."""
+    from nexttransformer_amd.moe import MoELayer
+    for mode in ("accumulate", "autograd"):
+        m = MoELayer(_recipe(), 2, expert_grad=mode)
+        m.train()
+        hidden = torch.zeros(0, m.recipe.width, device="cuda", dtype=torch.bfloat16,
+                             requires_grad=True)
+        out, aux = m(hidden)
+        assert out.shape == (0, m.recipe.width)
+        (out.float().sum() + aux).backward()
+        assert hidden.grad is not None and hidden.grad.shape == hidden.shape
+        for name, p in m.named_parameters():
+            assert p.grad is not None and p.grad.shape == p.shape, (mode, name)
+            assert p.grad.dtype == torch.float32 and float(p.grad.abs().max()) == 0.0, (mode, name)
+
+
+def test_expert_grad_modes():
+    """expert_grad="autograd" hands the routed experts' gradients to autograd: the same values as
+    the default mode's .grad, torch.autograd.grad can name the expert weights, and
+    backward(inputs=[hidden]) leaves them alone (which the default mode does not)."""
+    from nexttransformer_amd.moe import MoELayer
+    r = _recipe(activation="swiglu", shared_experts=1, expert_width=128,
+                allow_any_expert_width=True)
+    a = MoELayer(r, 2, aux_grad="loss")
+    _randomise_fc2(a, 5)
+    b = MoELayer(r, 2, aux_grad="loss", expert_grad="autograd")
+    b.load_state_dict(a.state_dict())
+    g = torch.Generator().manual_seed(6)
+    hidden = torch.randn(300, r.width, generator=g).to(torch.bfloat16).cuda()
+    G = torch.randn(300, r.width, generator=g).to(torch.bfloat16).cuda()
+    loss = lambda m, h: (m(h)[0].float() * G.float()).sum() + m.last_aux_loss
+    loss(a, hidden).backward()
+    fc1 = [e.linear_fc1.weight for e in b.experts.local_experts]
+    grads = torch.autograd.grad(loss(b, hidden), fc1)
+    for ea, gb in zip(a.experts.local_experts, grads):
+        assert torch.equal(ea.linear_fc1.weight.grad, gb)
+    # backward restricted to hidden: autograd mode leaves the experts' .grad unset
+    h = hidden.clone().requires_grad_()
+    loss(b, h).backward(inputs=[h])
+    assert h.grad is not None
+    assert all(w.grad is None for w in fc1)
+
+
+def test_invalidate_weights_after_data_write():
+    """The operand cache follows version counters: an optimizer step is picked up by itself; a
+    write through .data (which bypasses the counter) after invalidate_weights()."""
+    from nexttransformer_amd.moe import MoELayer
+    r = _recipe()
+    m = MoELayer(r, 2, aux_grad="loss")
+    _randomise_fc2(m, 9)
+    ref = MoELayer(r, 2, aux_grad="loss")
+    g = torch.Generator().manual_seed(10)
+    hidden = torch.randn(200, r.width, generator=g).to(torch.bfloat16).cuda().requires_grad_()
+
+    def same_as_fresh_copy():
+        ref.load_state_dict(m.state_dict())
+        ref.invalidate_weights()
+        return torch.equal(m(hidden)[0].view(torch.int16), ref(hidden)[0].view(torch.int16))
+
+    m(hidden)[0].float().sum().backward()  # builds the cache
+    opt = torch.optim.SGD(m.parameters(), lr=0.5)
+    opt.step()
+    assert same_as_fresh_copy()
+    w = m.experts.local_experts[0].linear_fc2.weight
+    w.data.add_(0.25)
+    m.invalidate_weights()
+    assert same_as_fresh_copy()
