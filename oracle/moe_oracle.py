@@ -314,9 +314,3 @@ def moe_forward_fp8(x, router, w1q, w1s, w2q, w2s, k, *, score_fn=SOFTMAX, activ
     lb, z = aux_losses(logits, counts, k, aux_coeff, z_coeff, score_fn)
     return dict(out=out, aux=lb + z, lb=lb, z=z, logits=logits, ids=ids, weights=topw,
                 counts=counts, offsets=offsets, src_row=src, dest=dest, x_q=xq, x_scale=xs)
-
-
-def tflops(T, d, E, k, H, shared_H=0):
-    """Algorithmic FLOP of one forward: router 2TdE + routed 6TkdH + shared 6TdHs."""
-    return 2 * T * d * E + 6 * T * k * d * H + 6 * T * d * shared_H
-
