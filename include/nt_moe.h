@@ -149,6 +149,26 @@ int nt_moe_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
                       uint16_t* x_perm, nt_moe_stream_t stream);
 
 /*
+ * Router and route plan in one call: the outputs of nt_moe_router_fwd followed by those of
+ * nt_moe_route_plan without x_perm, identical bits. When ceil(T/64) * E <= 16384 in two launches
+ * instead of three: the router's top-k also counts each 64-token block's assignments per expert
+ * into the workspace, and the plan kernel ranks each block's assignments itself (no histogram
+ * launch); larger shapes make exactly the router and route-plan launches. Replaces
+ * NativeRouter.gating + TopKRouter (megatron_moe.py:95-100, 43) followed by
+ * mapping.T.nonzero() / mapping.sum(0) (megatron_moe.py:142-144).
+ *   workspace  nt_moe_router_plan_workspace_bytes(T, d, E, k) bytes (never smaller)
+ * Other arguments as in nt_moe_router_fwd and nt_moe_route_plan.
+ */
+size_t nt_moe_router_plan_workspace_bytes(int64_t T, int32_t d, int32_t E, int32_t k);
+int nt_moe_router_plan(const uint16_t* x, int64_t ld_x, const float* w_router_t,
+                       const float* logit_bias, int64_t T, int32_t d, int32_t E, int32_t k,
+                       int32_t score_fn, float* logits, int32_t* topk_ids, float* topk_w,
+                       float* prob_partial, float* z_partial, int32_t* counts, int32_t* offsets,
+                       int32_t* src_row, float* perm_w, int32_t* combine_dest,
+                       float* combine_w, void* workspace, size_t workspace_bytes,
+                       nt_moe_stream_t stream);
+
+/*
  * nt_moe_route_plan without a workspace argument: the same outputs, the same kernels, with
  * their scratch (ranks and per-block counts) in a static device array of the library instead.
  * No counterpart in the reference; it is for callers that cannot allocate device memory (code

@@ -37,6 +37,9 @@ SIGNATURES = {
                               _p, _p]),
     "nt_moe_route_plan": (_i32, [_p, _i64, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _sz, _p,
                                  _p, _p, _p, _p, _p]),
+    "nt_moe_router_plan_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32]),
+    "nt_moe_router_plan": (_i32, [_p, _i64, _p, _p, _i64, _i32, _i32, _i32, _i32, _p, _p, _p, _p,
+                                  _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p]),
     "nt_moe_route_plan_noalloc": (_i32, [_p, _i64, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p,
                                          _p, _p, _p, _p, _p]),
     "nt_moe_grouped_gemm_bf16_packed_keep": (_i32, [_p, _i64, _i64, _p, _p, _i32, _i64, _p, _i32,

@@ -394,6 +394,73 @@ int nt_moe_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
 
 namespace {
 
+// The one-launch plan reads the whole per-64-token-block counts table in every workgroup; past
+// this many entries the histogram + plan kernels (a table four times smaller) are faster
+// (measured at T = 16384, E = 256 and T = 32768, E = 64).
+constexpr int64_t kCountsPlanMax = 16384;
+
+bool plan_from_counts(int64_t T, int E) {
+  return ((T + NT_MOE_ROUTE_BLOCK - 1) / NT_MOE_ROUTE_BLOCK) * E <= kCountsPlanMax;
+}
+
+}  // namespace
+
+size_t nt_moe_router_plan_workspace_bytes(int64_t T, int32_t d, int32_t E, int32_t k) {
+  if (T <= 0 || d <= 0 || E <= 0 || k <= 0) return 0;
+  const int64_t nblk64 = (T + NT_MOE_ROUTE_BLOCK - 1) / NT_MOE_ROUTE_BLOCK;
+  const size_t plan = plan_from_counts(T, E) ? align256((size_t)nblk64 * E * 4)
+                                             : route_ws_bytes(T, k, E);
+  return align256(router_workspace_need(T, d, E)) + plan;
+}
+
+int nt_moe_router_plan(const uint16_t* x, int64_t ld_x, const float* w_router_t,
+                       const float* logit_bias, int64_t T, int32_t d, int32_t E, int32_t k,
+                       int32_t score_fn, float* logits, int32_t* topk_ids, float* topk_w,
+                       float* prob_partial, float* z_partial, int32_t* counts, int32_t* offsets,
+                       int32_t* src_row, float* perm_w, int32_t* combine_dest,
+                       float* combine_w, void* workspace, size_t workspace_bytes,
+                       nt_moe_stream_t stream) {
+  int rc = check_route_shape(T, k, E);
+  if (rc) return rc;
+  NT_REQUIRE(d > 0 && d % 8 == 0, "router_plan: d must be a positive multiple of 8, got %d", d);
+  NT_REQUIRE(ld_x >= d && ld_x % 8 == 0, "router_plan: ld_x must be >= d and a multiple of 8");
+  NT_REQUIRE(score_fn == NT_MOE_SCORE_SOFTMAX || score_fn == NT_MOE_SCORE_SIGMOID,
+             "router_plan: unknown score_fn %d", score_fn);
+  NT_REQUIRE(counts && offsets, "router_plan: null buffer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (T == 0)  // counts and offsets are zero: the scan over no blocks
+    return launched(launch_histogram_scan(nullptr, 0, k, E, counts, offsets, nullptr, nullptr, st),
+                    "router_plan");
+  NT_REQUIRE(x && w_router_t && topk_ids && topk_w && prob_partial && z_partial && src_row &&
+                 combine_dest && combine_w && workspace,
+             "router_plan: null buffer");
+  NT_REQUIRE(aligned16(x), "router_plan: x must be 16-byte aligned");
+  const size_t need = nt_moe_router_plan_workspace_bytes(T, d, E, k);
+  if (workspace_bytes < need)
+    return fail(NT_MOE_ENOSPC, "router_plan: workspace %zu < %zu bytes", workspace_bytes, need);
+  const size_t router_part = align256(router_workspace_need(T, d, E));
+  void* plan_ws = reinterpret_cast<char*>(workspace) + router_part;
+  const bool from_counts = plan_from_counts(T, E);
+  hipError_t err = launch_router(x, ld_x, w_router_t, logit_bias, T, d, E, k, score_fn, logits,
+                                 topk_ids, topk_w, prob_partial, z_partial,
+                                 router_part ? reinterpret_cast<float*>(workspace) : nullptr,
+                                 router_part, st,
+                                 from_counts ? reinterpret_cast<int32_t*>(plan_ws) : nullptr);
+  if (err != hipSuccess) return launched(err, "router_plan (router)");
+  if (from_counts)
+    return launched(launch_plan_from_counts(topk_ids, topk_w, T, k, E,
+                                            reinterpret_cast<int32_t*>(plan_ws), counts, offsets,
+                                            src_row, perm_w, combine_dest, combine_w, st),
+                    "router_plan (plan)");
+  RouteWorkspace ws = route_ws(plan_ws, T, k);
+  return launched(launch_route_plan(nullptr, 0, topk_ids, topk_w, T, d, k, E, counts, offsets,
+                                    ws.ranks, ws.block_counts, src_row, perm_w, combine_dest,
+                                    combine_w, nullptr, st),
+                  "router_plan (plan)");
+}
+
+namespace {
+
 // The route plan's scratch for nt_moe_route_plan_noalloc: NT_MOE_NOALLOC_MAX_ASSIGNMENTS ranks,
 // then NT_MOE_NOALLOC_MAX_BLOCK_COUNTS per-block expert counts (2 MiB). Each GPU holds its own
 // copy at its own address until the process ends. Host code never passes the array's name to a

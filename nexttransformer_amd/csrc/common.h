@@ -15,6 +15,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 constexpr int kRouteBlock = NT_MOE_ROUTE_BLOCK;  // tokens per router / histogram block
@@ -52,7 +53,7 @@ hipError_t launch_router(const uint16_t* x, int64_t ld_x, const float* wt, const
                          int64_t T, int d, int E, int k, int score_fn, float* logits,
                          int32_t* topk_ids, float* topk_w, float* prob_partial,
                          float* z_partial, float* workspace, size_t workspace_bytes,
-                         hipStream_t stream);
+                         hipStream_t stream, int32_t* block_counts = nullptr);
 hipError_t launch_topk_from_logits(const float* logits, int64_t T, int E, int k,
                                    int score_fn, int32_t* topk_ids, float* topk_w,
                                    float* prob_partial, float* z_partial, hipStream_t stream);
@@ -61,6 +62,12 @@ size_t router_workspace_need(int64_t T, int d, int E);
 hipError_t launch_histogram_scan(const int32_t* topk_ids, int64_t T, int k, int E,
                                  int32_t* counts, int32_t* offsets, int32_t* ranks,
                                  int32_t* block_counts, hipStream_t stream);
+// The route plan from the router's per-64-token-block expert counts (ceil(T/64) x E, written by
+// launch_router's block_counts): plan_kernel without the histogram launch. E <= 256.
+hipError_t launch_plan_from_counts(const int32_t* topk_ids, const float* topk_w, int64_t T, int k,
+                                   int E, const int32_t* block_counts64, int32_t* counts,
+                                   int32_t* offsets, int32_t* src_row, float* perm_w,
+                                   int32_t* combine_dest, float* combine_w, hipStream_t stream);
 hipError_t launch_permute(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
                           const float* topk_w, int64_t T, int d, int k, int E,
                           const int32_t* ranks, const int32_t* block_base,

@@ -285,6 +285,146 @@ __global__ __launch_bounds__(256) void plan_kernel(
   }
 }
 
+// plan_kernel with the counts table at the router's 64-token granularity (block_counts64[b][e]:
+// assignments of tokens [64 b, 64 b + 64) to expert e, written by the router's top-k), so the
+// histogram launch is not needed: each workgroup ranks its own 256 tokens' assignments in LDS
+// (histogram_kernel's bit masks, one wave per 64 tokens) and takes its expert bases from the
+// table -- every column summed over the whole table, in the same fixed shape in every
+// workgroup, with the blocks before its first token as its prefix. All integer: the same
+// destinations as histogram_kernel + plan_kernel.
+__global__ __launch_bounds__(256) void plan_c64_kernel(
+    const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int64_t T, int k,
+    int E, int nblk64, const int32_t* __restrict__ block_counts64, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ src_row, float* __restrict__ perm_w,
+    int32_t* __restrict__ combine_dest, float* __restrict__ combine_w) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint64_t* mask = reinterpret_cast<uint64_t*>(smem);              // [4][E]
+  int32_t* wave_prefix = reinterpret_cast<int32_t*>(mask + 4 * E);  // [4][E]
+  __shared__ int32_t pre_s[1024], tot_s[1024];  // [G][E] partial column sums, G * E <= 1024
+  __shared__ int32_t base_s[NT_MOE_MAX_EXPERTS];
+  __shared__ int32_t wave_tot[4];
+  const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
+  const int blk = blockIdx.x;
+  const int64_t t = (int64_t)blk * kHistBlock + tid;
+  const bool live = t < T;
+  for (int i = tid; i < 4 * E; i += blockDim.x) mask[i] = 0ull;
+  int ev[NT_MOE_MAX_TOPK];
+  float wv[NT_MOE_MAX_TOPK];
+#pragma unroll
+  for (int j = 0; j < NT_MOE_MAX_TOPK; ++j) {
+    ev[j] = 0x7fffffff;
+    wv[j] = 0.f;
+    if (live && j < k) {
+      ev[j] = topk_ids[t * k + j];
+      wv[j] = topk_w[t * k + j];
+    }
+  }
+  // Column sums of the table: groups of E / 4 threads, each thread four consecutive experts
+  // (16-byte loads; E % 4 == 0, else one expert per thread); group g sums blocks g, g + G, ...
+  const int pre_end = 4 * blk;  // 64-token blocks before this workgroup's first token
+  int G;
+  if (E % 4 == 0) {
+    const int E4 = E / 4;
+    G = 256 / E4;
+    const int g = tid / E4, e4 = tid - g * E4;
+    if (g < G) {
+      i32x4 pre = {0, 0, 0, 0}, tot = {0, 0, 0, 0};
+#pragma unroll 16
+      for (int b = g; b < nblk64; b += G) {
+        const i32x4 c = *reinterpret_cast<const i32x4*>(block_counts64 + (int64_t)b * E + 4 * e4);
+        tot += c;
+        if (b < pre_end) pre += c;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        pre_s[g * E + 4 * e4 + q] = pre[q];
+        tot_s[g * E + 4 * e4 + q] = tot[q];
+      }
+    }
+  } else {
+    G = 256 / E;
+    const int g = tid / E, e = tid - g * E;
+    if (g < G) {
+      int pre = 0, tot = 0;
+#pragma unroll 8
+      for (int b = g; b < nblk64; b += G) {
+        const int c = block_counts64[(int64_t)b * E + e];
+        tot += c;
+        pre += b < pre_end ? c : 0;
+      }
+      pre_s[tid] = pre;
+      tot_s[tid] = tot;
+    }
+  }
+  __syncthreads();  // masks cleared
+#pragma unroll
+  for (int j = 0; j < NT_MOE_MAX_TOPK; ++j)
+    if (j < k && (unsigned)ev[j] < (unsigned)E)
+      atomicOr(reinterpret_cast<unsigned long long*>(&mask[w * E + ev[j]]), 1ull << lane);
+  __syncthreads();
+  int before = 0, total = 0;  // thread tid owns expert tid
+  if (tid < E) {
+    for (int q = 0; q < G; ++q) {
+      before += pre_s[q * E + tid];
+      total += tot_s[q * E + tid];
+    }
+    int run = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      wave_prefix[q * E + tid] = run;
+      run += __popcll(mask[q * E + tid]);
+    }
+  }
+  const int incl = group_inclusive_scan(total, 64);
+  if (lane == 63) wave_tot[w] = incl;
+  __syncthreads();
+  int carry = 0;
+  for (int q = 0; q < w; ++q) carry += wave_tot[q];
+  const int excl = carry + incl - total;  // offsets[tid]
+  if (tid < E) {
+    base_s[tid] = excl + before;
+    if (blk == 0) {
+      counts[tid] = total;
+      offsets[tid] = excl;
+    }
+  }
+  if (blk == 0 && tid == 0) offsets[E] = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
+  __syncthreads();
+
+  if (!live) return;
+  const int64_t A = T * k;
+  const uint64_t below = (1ull << lane) - 1ull;
+  int dv[NT_MOE_MAX_TOPK];
+#pragma unroll
+  for (int j = 0; j < NT_MOE_MAX_TOPK; ++j) {
+    dv[j] = 0;
+    if (j < k) {
+      if ((unsigned)ev[j] < (unsigned)E) {
+        const int ej = ev[j];
+        int dest = base_s[ej] + wave_prefix[w * E + ej] + __popcll(mask[w * E + ej] & below);
+        dest = dest < 0 ? 0 : (dest >= A ? (int)(A - 1) : dest);
+        src_row[dest] = (int32_t)t;
+        if (perm_w) perm_w[dest] = wv[j];
+        dv[j] = dest;
+      } else {
+        ev[j] = 0x7ffffffe;  // ignored id: sorts last, row 0 as a harmless target
+      }
+    }
+  }
+  // Ascending expert order; equal keys (only ignored ids) keep their slot order.
+#pragma unroll
+  for (int j = 0; j < NT_MOE_MAX_TOPK; ++j) {
+    if (j < k) {
+      int pos = 0;
+#pragma unroll
+      for (int i = 0; i < NT_MOE_MAX_TOPK; ++i)
+        pos += (ev[i] < ev[j] || (ev[i] == ev[j] && i < j)) ? 1 : 0;
+      combine_dest[t * k + pos] = dv[j];
+      combine_w[t * k + pos] = wv[j];
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_histogram_scan(const int32_t* topk_ids, int64_t T, int k, int E,
@@ -340,6 +480,21 @@ hipError_t launch_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* top
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL(plan_kernel, dim3((unsigned)nblk), dim3(256), 0, stream, topk_ids, topk_w, T,
                      k, E, (int)nblk, ranks, block_counts, counts, offsets, src_row, perm_w,
+                     combine_dest, combine_w);
+  return hipGetLastError();
+}
+
+// The route plan from the router's per-64-token-block counts (one launch); E <= 256.
+hipError_t launch_plan_from_counts(const int32_t* topk_ids, const float* topk_w, int64_t T, int k,
+                                   int E, const int32_t* block_counts64, int32_t* counts,
+                                   int32_t* offsets, int32_t* src_row, float* perm_w,
+                                   int32_t* combine_dest, float* combine_w, hipStream_t stream) {
+  if (T == 0 || E > 256) return hipErrorInvalidValue;
+  const int64_t nblk = ceil_div(T, kHistBlock);
+  const int nblk64 = ceil_div(T, kRouteBlock);
+  const size_t lds = (size_t)4 * E * (sizeof(uint64_t) + sizeof(int32_t));
+  hipLaunchKernelGGL(plan_c64_kernel, dim3((unsigned)nblk), dim3(256), lds, stream, topk_ids,
+                     topk_w, T, k, E, nblk64, block_counts64, counts, offsets, src_row, perm_w,
                      combine_dest, combine_w);
   return hipGetLastError();
 }

@@ -46,7 +46,9 @@ constexpr int kBufferWord3 = 0x00020000;
 
 __host__ __device__ inline int lg_tile_bytes(int E) { return kRouteBlock * (E + 1) * 4; }
 __host__ __device__ inline int zt_offset(int E) { return (lg_tile_bytes(E) + 15) & ~15; }
-inline size_t router_lds_bytes(int E) { return zt_offset(E) + kRouteBlock * sizeof(float); }
+// After the logits tile: zt (64 floats), then the block's per-expert assignment counts (E ints).
+__host__ __device__ inline int cnt_offset(int E) { return zt_offset(E) + kRouteBlock * 4; }
+__host__ __device__ inline size_t router_lds_bytes(int E) { return cnt_offset(E) + (size_t)E * 4; }
 
 // LDS stages of the fused kernel: for each feature range, 64 features of x (64 tokens, rows
 // padded to kXPitch bf16) and of the router weights for all expert blocks, stored so that a
@@ -86,8 +88,13 @@ template <int KMAX, int LPT = 4>
 __device__ __forceinline__ void topk_and_scores(float* lg, float* zt, int64_t t0, int64_t T, int E, int k,
                                 int score_fn, int32_t* __restrict__ topk_ids,
                                 float* __restrict__ topk_w, float* __restrict__ prob_partial,
-                                float* __restrict__ z_partial) {
+                                float* __restrict__ z_partial, int32_t* __restrict__ block_counts) {
   static_assert(LPT == 1 || LPT == 2 || LPT == 4 || LPT == 8 || LPT == 16, "lanes per token");
+  // The block's per-expert assignment counts (for the route plan): LDS integer adds, so the
+  // result does not depend on their order.
+  int* cnt = reinterpret_cast<int*>(reinterpret_cast<unsigned char*>(zt) + kRouteBlock * 4);
+  if (block_counts)
+    for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
   const int ldl = E + 1;
   const int tt = threadIdx.x / LPT;   // token within the block
   const int sub = threadIdx.x % LPT;  // which of the LPT expert strides this lane scans
@@ -174,6 +181,11 @@ __device__ __forceinline__ void topk_and_scores(float* lg, float* zt, int64_t t0
   }
   if (sub == 0) zt[tt] = lse * lse;
   __syncthreads();
+  if (block_counts && t < T) {
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j)
+      if (j < k && j % LPT == sub) atomicAdd(&cnt[oi[j]], 1);
+  }
 
   // Per-block column sums in a fixed order (deterministic): P consecutive lanes per expert,
   // lane p summing tokens p, p + P, ..., then a butterfly over the P lanes; P is the largest
@@ -196,6 +208,10 @@ __device__ __forceinline__ void topk_and_scores(float* lg, float* zt, int64_t t0
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
     if (threadIdx.x == 0) z_partial[blk] = s;
+  }
+  if (block_counts) {
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) block_counts[blk * E + e] = cnt[e];
   }
 }
 
@@ -388,7 +404,8 @@ __global__ __launch_bounds__(128 * EB * R) void router_mfma_kernel(
     const uint16_t* __restrict__ x, int64_t ld_x, const float* __restrict__ wt,
     const float* __restrict__ bias, int64_t T, int d, int E, int k, int score_fn,
     float* __restrict__ logits, int32_t* __restrict__ topk_ids, float* __restrict__ topk_w,
-    float* __restrict__ prob_partial, float* __restrict__ z_partial) {
+    float* __restrict__ prob_partial, float* __restrict__ z_partial,
+    int32_t* __restrict__ block_counts) {
   using RB = RouterBlock<EB, R>;
   extern __shared__ __align__(16) unsigned char smem[];
   float* lg = reinterpret_cast<float*>(smem + RB::stage_bytes());
@@ -407,7 +424,7 @@ __global__ __launch_bounds__(128 * EB * R) void router_mfma_kernel(
   __syncthreads();
   if (logits) write_logits_out(lg, t0, T, E, logits);
   topk_and_scores<KMAX, 2 * EB * R>(lg, zt, t0, T, E, k, score_fn, topk_ids, topk_w,
-                                    prob_partial, z_partial);
+                                    prob_partial, z_partial, block_counts);
 }
 
 inline size_t router_mfma_lds_bytes(int EB, int R, int E) {
@@ -504,7 +521,7 @@ struct StreamGeo {
   static_assert(kXCopies * EBW == 8, "x copies per stage");
   static constexpr size_t ring_bytes() { return (size_t)kSRing * kSTile; }
   static constexpr size_t lds_bytes(int E) {
-    return ring_bytes() + (size_t)zt_offset(E) + kRouteBlock * sizeof(float);
+    return ring_bytes() + router_lds_bytes(E);
   }
 };
 
@@ -513,7 +530,8 @@ __global__ __launch_bounds__(64 * EBW) void router_stream_kernel(
     const uint16_t* __restrict__ x, int64_t ld_x, const float* __restrict__ wt,
     const float* __restrict__ bias, int64_t T, int d, int E, int k, int score_fn,
     float* __restrict__ logits, int32_t* __restrict__ topk_ids, float* __restrict__ topk_w,
-    float* __restrict__ prob_partial, float* __restrict__ z_partial) {
+    float* __restrict__ prob_partial, float* __restrict__ z_partial,
+    int32_t* __restrict__ block_counts) {
   using G = StreamGeo<EBW>;
   extern __shared__ __align__(16) unsigned char smem[];
   float* lg = reinterpret_cast<float*>(smem + G::ring_bytes());
@@ -645,7 +663,143 @@ __global__ __launch_bounds__(64 * EBW) void router_stream_kernel(
   __syncthreads();
   if (logits) write_logits_out(lg, t0, T, E, logits);
   topk_and_scores<KMAX, EBW>(lg, zt, t0, T, E, k, score_fn, topk_ids, topk_w, prob_partial,
-                             z_partial);
+                             z_partial, block_counts);
+}
+
+// ---- Chunk-per-wave router -----------------------------------------------------------------
+// For up to 32 experts and up to 8 chunks (d <= 1024), one workgroup per 64-token block: wave j
+// computes chunk sum c_j of all 64 tokens (two chains, one per 32-token half, sharing each
+// router weight operand) from token rows it stages itself, so no wave waits for another until
+// every chunk sum is done. Per wave: the block's rows of its 128 features (two [64 rows][128 B]
+// tiles, 16 KB, the streamed kernel's swizzled layout, written by its own 16-byte direct-to-LDS
+// buffer loads) and its 64 router weight operands per lane (straight into registers); the chains
+// run as soon as the wave's own first tile and weights have landed. The chunk sums then go to
+// LDS over the wave's own tiles and the fixed-order sum ((c_0 + c_1) + c_2) + ... (+ bias) fills
+// the logits tile, ranked as in the other fused kernels.
+template <int NW>
+struct ChunkGeo {
+  static constexpr int kWaveBytes = 2 * kSTile;  // two [64 rows][128 B] tiles per wave
+  static constexpr int kCsPitch = 33;            // floats per row of a wave's chunk-sum tile
+  static_assert(kRouteBlock * kCsPitch * 4 <= kWaveBytes, "chunk sums fit the wave's tiles");
+  static constexpr size_t lds_bytes(int E) { return (size_t)NW * kWaveBytes + router_lds_bytes(E); }
+};
+
+template <int NW, int KMAX>
+__global__ __launch_bounds__(64 * NW) void router_chunk_kernel(
+    const uint16_t* __restrict__ x, int64_t ld_x, const float* __restrict__ wt,
+    const float* __restrict__ bias, int64_t T, int d, int E, int k, int score_fn,
+    float* __restrict__ logits, int32_t* __restrict__ topk_ids, float* __restrict__ topk_w,
+    float* __restrict__ prob_partial, float* __restrict__ z_partial,
+    int32_t* __restrict__ block_counts) {
+  using G = ChunkGeo<NW>;
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* lg = reinterpret_cast<float*>(smem + NW * G::kWaveBytes);
+  float* zt = reinterpret_cast<float*>(smem + NW * G::kWaveBytes + zt_offset(E));
+  const int lane = lane_id(), wave = wave_id();
+  const int64_t t0 = (int64_t)blockIdx.x * kRouteBlock;
+  const int nchunk = (d + kRouterChunk - 1) / kRouterChunk;
+  unsigned char* xs = smem + wave * G::kWaveBytes;
+  const int ec = lane & 31;
+  if (wave < nchunk) {
+    const int f0 = wave * kRouterChunk;
+    const int fe = f0 + kRouterChunk < d ? f0 + kRouterChunk : d;
+    // Token rows [t0, t0 + rows): a row past T or a feature past the last row's end reads 0
+    // (buffer range check); features past fe are never multiplied.
+    const int rows = T - t0 < kRouteBlock ? (int)(T - t0) : kRouteBlock;
+    const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(x + t0 * ld_x), 0, (int)(((int64_t)(rows - 1) * ld_x + d) * 2), kBufferWord3);
+    // Copy i of tile h: rows 8 i + lane / 8, LDS slot lane % 8 holding chunk slot ^ ((row >> 1) & 7)
+    // of features [f0 + 64 h, +64).
+    auto issue_tile = [&](int h) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int row = 8 * i + (lane >> 3);
+        const int voff = (int)(row * ld_x * 2) + (((lane & 7) ^ ((row >> 1) & 7)) << 4) +
+                         (f0 + 64 * h) * 2;
+        buffer_copy_lds16(xrsrc, xs + h * kSTile + i * 1024, voff);
+      }
+    };
+    const int ecl = ec < E ? ec : E - 1;
+    const int hk = lane >> 5;  // feature parity this lane supplies
+    const __amdgpu_buffer_rsrc_t wrsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)wt, 0, (int)((int64_t)d * E * 4), kBufferWord3);
+    const int voff_w = (hk * E + ecl) * 4;
+    // Operands of tile h: pair 4 q + j is features f0 + 64 h + 8 q + 2 j + hk (pairs past d read
+    // the last pair, unused).
+    auto issue_w = [&](int h, float (&wr)[32]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int f = f0 + 64 * h + 8 * q + 2 * j;
+          wr[4 * q + j] = load_w_asm(wrsrc, voff_w, (f < d - 2 ? f : d - 2) * E * 4);
+        }
+    };
+    const uint32_t sel = hk ? 0x07060C0Cu : 0x05040C0Cu;
+    const int row0 = lane & 31, row1 = 32 + (lane & 31);
+    const int sw0 = (row0 >> 1) & 7, sw1 = (row1 >> 1) & 7;
+    floatx16 c0 = {}, c1 = {};
+    auto compute = [&](int h, const float (&wr)[32]) __attribute__((always_inline)) {
+      const int left = fe - (f0 + 64 * h);
+      const int ng = left >= 64 ? 8 : (left > 0 ? left / 8 : 0);
+      const unsigned char* tile = xs + h * kSTile;
+      u32x4 x0[8], x1[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        x0[q] = *reinterpret_cast<const u32x4*>(tile + row0 * kSRow + ((q ^ sw0) << 4));
+        x1[q] = *reinterpret_cast<const u32x4*>(tile + row1 * kSRow + ((q ^ sw1) << 4));
+      }
+      auto group = [&](int q) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a0 = __builtin_bit_cast(float, __builtin_amdgcn_perm(x0[q][j], 0u, sel));
+          const float a1 = __builtin_bit_cast(float, __builtin_amdgcn_perm(x1[q][j], 0u, sel));
+          c0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, wr[4 * q + j], c0, 0, 0, 0);
+          c1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, wr[4 * q + j], c1, 0, 0, 0);
+        }
+      };
+      if (ng == 8) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) group(q);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (q < ng) group(q);
+      }
+    };
+    float wlo[32], whi[32];
+    issue_tile(0);
+    issue_w(0, wlo);
+    issue_tile(1);
+    issue_w(1, whi);
+    // Tile 0 and its weights are the first 40 operations: at most the 40 after them outstanding.
+    stage_wait<40>(wlo);
+    compute(0, wlo);
+    stage_wait<0>(whi);
+    compute(1, whi);
+    // Chunk sums over this wave's own tiles (its LDS reads of them are complete: a wave's LDS
+    // operations run in order).
+    float* cs = reinterpret_cast<float*>(xs);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      cs[acc_row(i, lane) * G::kCsPitch + ec] = c0[i];
+      cs[(32 + acc_row(i, lane)) * G::kCsPitch + ec] = c1[i];
+    }
+  }
+  __syncthreads();
+  // logit = ((c_0 + c_1) + c_2) + ... (+ bias) into the tile lg[64][E+1].
+  for (int idx = threadIdx.x; idx < kRouteBlock * E; idx += blockDim.x) {
+    const int r = idx / E, e = idx - r * E;
+    float v = reinterpret_cast<const float*>(smem)[r * G::kCsPitch + e];
+    for (int c = 1; c < nchunk; ++c)
+      v = v + reinterpret_cast<const float*>(smem + c * G::kWaveBytes)[r * G::kCsPitch + e];
+    if (bias) v = v + bias[e];
+    lg[r * (E + 1) + e] = v;
+  }
+  __syncthreads();
+  if (logits) write_logits_out(lg, t0, T, E, logits);
+  topk_and_scores<KMAX, NW>(lg, zt, t0, T, E, k, score_fn, topk_ids, topk_w, prob_partial,
+                            z_partial, block_counts);
 }
 
 // Split: the chunk sum c_j (blockIdx.y = j) of a 64-token x 32-expert block (blockIdx.z) ->
@@ -713,7 +867,8 @@ __global__ __launch_bounds__(1024) void router_topk_kernel(
     const float* __restrict__ partials, int nchunk, const float* __restrict__ bias, int64_t T,
     int E, int k, int score_fn,
     float* __restrict__ logits, int32_t* __restrict__ topk_ids, float* __restrict__ topk_w,
-    float* __restrict__ prob_partial, float* __restrict__ z_partial) {
+    float* __restrict__ prob_partial, float* __restrict__ z_partial,
+    int32_t* __restrict__ block_counts) {
   extern __shared__ __align__(16) unsigned char smem[];
   float* lg = reinterpret_cast<float*>(smem);
   float* zt = reinterpret_cast<float*>(smem + zt_offset(E));
@@ -775,7 +930,7 @@ __global__ __launch_bounds__(1024) void router_topk_kernel(
   }
   __syncthreads();
   topk_and_scores<KMAX, 16>(lg, zt, t0, T, E, k, score_fn, topk_ids, topk_w, prob_partial,
-                        z_partial);
+                            z_partial, block_counts);
 }
 
 int kmax_for(int k) { return k <= 2 ? 2 : (k <= 4 ? 4 : 8); }
@@ -797,7 +952,8 @@ int router_ranges(int d, int E) {
 }
 
 // NT_MOE_ROUTER_MODE=fused|split|stream overrides the size heuristic (for tuning runs): fused =
-// the fused kernel (up to 128 experts), split = chunk planes, stream = the streamed kernel
+// the fused range kernel (up to 128 experts, never the chunk-per-wave one), split = chunk
+// planes, stream = the streamed kernel
 // (129-256 experts).
 int router_mode_override() {
   static int mode = [] {
@@ -814,47 +970,47 @@ int router_mode_override() {
 template <int KMAX>
 hipError_t launch_topk_k(const float* partials, int nchunk, const float* bias, int64_t T, int E,
                          int k, int score_fn, float* logits, int32_t* ids, float* w, float* pp,
-                         float* zp, hipStream_t stream) {
+                         float* zp, int32_t* bc, hipStream_t stream) {
   dim3 grid(ceil_div(T, kRouteBlock));
   hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(router_topk_kernel<KMAX>),
                                      router_lds_bytes(E));
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL((router_topk_kernel<KMAX>), grid, dim3(1024), router_lds_bytes(E), stream,
-                     partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp);
+                     partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, bc);
   return hipGetLastError();
 }
 
 hipError_t launch_topk_any(const float* partials, int nchunk, const float* bias, int64_t T,
                            int E, int k, int score_fn, float* logits, int32_t* ids, float* w,
-                           float* pp, float* zp, hipStream_t stream) {
+                           float* pp, float* zp, int32_t* bc, hipStream_t stream) {
   switch (kmax_for(k)) {
-    case 2: return launch_topk_k<2>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
-    case 4: return launch_topk_k<4>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
-    default: return launch_topk_k<8>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    case 2: return launch_topk_k<2>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
+    case 4: return launch_topk_k<4>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
+    default: return launch_topk_k<8>(partials, nchunk, bias, T, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
   }
 }
 
 template <int EB, int R, int KMAX>
 hipError_t launch_mfma_k(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
                          int64_t T, int d, int E, int k, int score_fn, float* logits,
-                         int32_t* ids, float* w, float* pp, float* zp, hipStream_t stream) {
+                         int32_t* ids, float* w, float* pp, float* zp, int32_t* bc, hipStream_t stream) {
   auto kern = router_mfma_kernel<EB, R, KMAX>;
   const size_t lds = router_mfma_lds_bytes(EB, R, E);
   hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL(kern, dim3(ceil_div(T, kRouteBlock)), dim3(128 * EB * R), lds, stream, x,
-                     ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp);
+                     ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc);
   return hipGetLastError();
 }
 
 template <int EB, int R>
 hipError_t launch_mfma_r(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
                          int64_t T, int d, int E, int k, int score_fn, float* logits,
-                         int32_t* ids, float* w, float* pp, float* zp, hipStream_t stream) {
+                         int32_t* ids, float* w, float* pp, float* zp, int32_t* bc, hipStream_t stream) {
   switch (kmax_for(k)) {
-    case 2: return launch_mfma_k<EB, R, 2>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
-    case 4: return launch_mfma_k<EB, R, 4>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
-    default: return launch_mfma_k<EB, R, 8>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    case 2: return launch_mfma_k<EB, R, 2>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
+    case 4: return launch_mfma_k<EB, R, 4>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
+    default: return launch_mfma_k<EB, R, 8>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
   }
 }
 
@@ -892,25 +1048,61 @@ int router_path(int64_t T, int d, int E) {
 template <int KMAX>
 hipError_t launch_stream_k(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
                            int64_t T, int d, int E, int k, int score_fn, float* logits,
-                           int32_t* ids, float* w, float* pp, float* zp, hipStream_t stream) {
+                           int32_t* ids, float* w, float* pp, float* zp, int32_t* bc, hipStream_t stream) {
   auto kern = router_stream_kernel<8, KMAX>;
   const size_t lds = StreamGeo<8>::lds_bytes(E);
   hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL(kern, dim3(ceil_div(T, kRouteBlock)), dim3(StreamGeo<8>::kThreads), lds,
-                     stream, x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp);
+                     stream, x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc);
   return hipGetLastError();
+}
+
+template <int NW, int KMAX>
+hipError_t launch_chunk_k(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
+                          int64_t T, int d, int E, int k, int score_fn, float* logits,
+                          int32_t* ids, float* w, float* pp, float* zp, int32_t* bc, hipStream_t stream) {
+  auto kern = router_chunk_kernel<NW, KMAX>;
+  const size_t lds = ChunkGeo<NW>::lds_bytes(E);
+  hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(kern, dim3(ceil_div(T, kRouteBlock)), dim3(64 * NW), lds, stream, x, ld_x,
+                     wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc);
+  return hipGetLastError();
+}
+
+template <int NW>
+hipError_t launch_chunk_w(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
+                          int64_t T, int d, int E, int k, int score_fn, float* logits,
+                          int32_t* ids, float* w, float* pp, float* zp, int32_t* bc, hipStream_t stream) {
+  switch (kmax_for(k)) {
+    case 2: return launch_chunk_k<NW, 2>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
+    case 4: return launch_chunk_k<NW, 4>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
+    default: return launch_chunk_k<NW, 8>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
+  }
+}
+
+// The chunk-per-wave kernel: up to 32 experts and 8 chunks, one wave per chunk (2, 4 or 8).
+bool chunk_router_fits(int d, int E) { return E <= 32 && ceil_div(d, kRouterChunk) <= 8; }
+
+hipError_t launch_chunk(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
+                        int64_t T, int d, int E, int k, int score_fn, float* logits,
+                        int32_t* ids, float* w, float* pp, float* zp, int32_t* bc, hipStream_t stream) {
+  const int nchunk = ceil_div(d, kRouterChunk);
+  if (nchunk <= 2) return launch_chunk_w<2>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
+  if (nchunk <= 4) return launch_chunk_w<4>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
+  return launch_chunk_w<8>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
 }
 
 // The streamed kernel for 129-256 experts (eight 32-expert blocks).
 hipError_t launch_stream(const uint16_t* x, int64_t ld_x, const float* wt, const float* bias,
                          int64_t T, int d, int E, int k, int score_fn, float* logits,
-                         int32_t* ids, float* w, float* pp, float* zp, hipStream_t stream) {
+                         int32_t* ids, float* w, float* pp, float* zp, int32_t* bc, hipStream_t stream) {
   if (E > 256) return hipErrorInvalidValue;
   switch (kmax_for(k)) {
-    case 2: return launch_stream_k<2>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
-    case 4: return launch_stream_k<4>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
-    default: return launch_stream_k<8>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, stream);
+    case 2: return launch_stream_k<2>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
+    case 4: return launch_stream_k<4>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
+    default: return launch_stream_k<8>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, ids, w, pp, zp, bc, stream);
   }
 }
 
@@ -929,7 +1121,7 @@ hipError_t launch_router(const uint16_t* x, int64_t ld_x, const float* wt, const
                          int64_t T, int d, int E, int k, int score_fn, float* logits,
                          int32_t* topk_ids, float* topk_w, float* prob_partial,
                          float* z_partial, float* workspace, size_t workspace_bytes,
-                         hipStream_t stream) {
+                         hipStream_t stream, int32_t* block_counts) {
   const int nchunk = ceil_div(d, kRouterChunk);
   const int path = router_path(T, d, E);
   const size_t plane = (size_t)T * (size_t)E * sizeof(float);
@@ -948,14 +1140,14 @@ hipError_t launch_router(const uint16_t* x, int64_t ld_x, const float* wt, const
       err = hipGetLastError();
       if (err != hipSuccess) return err;
       return launch_topk_any(workspace, 1, nullptr, T, E, k, score_fn, logits, topk_ids, topk_w,
-                             prob_partial, z_partial, stream);
+                             prob_partial, z_partial, block_counts, stream);
     }
     return launch_topk_any(workspace, nchunk, bias, T, E, k, score_fn, logits, topk_ids, topk_w,
-                           prob_partial, z_partial, stream);
+                           prob_partial, z_partial, block_counts, stream);
   }
   if (path == kStream || (path == kPlanes && E > 128 && E <= 256))
     return launch_stream(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, topk_ids, topk_w,
-                         prob_partial, z_partial, stream);
+                         prob_partial, z_partial, block_counts, stream);
   float* lbuf = logits ? logits : (workspace && workspace_bytes >= plane ? workspace : nullptr);
   if ((path != kFused || E > 128) && lbuf && nchunk <= 16) {
     const int ranges = logit_ranges(d);
@@ -973,18 +1165,22 @@ hipError_t launch_router(const uint16_t* x, int64_t ld_x, const float* wt, const
     err = hipGetLastError();
     if (err != hipSuccess) return err;
     return launch_topk_any(lbuf, 1, nullptr, T, E, k, score_fn, nullptr, topk_ids, topk_w,
-                           prob_partial, z_partial, stream);
+                           prob_partial, z_partial, block_counts, stream);
   }
   if (E <= 128) {  // the fused kernel: its path, or planes / logits without their buffers
+    // (the chunk-per-wave kernel where it fits, unless NT_MOE_ROUTER_MODE=fused)
+    if (chunk_router_fits(d, E) && router_mode_override() != 1)
+      return launch_chunk(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, topk_ids, topk_w,
+                          prob_partial, z_partial, block_counts, stream);
     const int eb = expert_blocks(E), ranges = router_ranges(d, E);
 #define NT_MFMA(EB, R) \
-  if (eb == EB && ranges == R) return launch_mfma_r<EB, R>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, topk_ids, topk_w, prob_partial, z_partial, stream);
+  if (eb == EB && ranges == R) return launch_mfma_r<EB, R>(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, topk_ids, topk_w, prob_partial, z_partial, block_counts, stream);
     NT_MFMA(1, 1) NT_MFMA(1, 2) NT_MFMA(1, 4) NT_MFMA(2, 1) NT_MFMA(4, 1)
 #undef NT_MFMA
   }
   if (E <= 256)
     return launch_stream(x, ld_x, wt, bias, T, d, E, k, score_fn, logits, topk_ids, topk_w,
-                         prob_partial, z_partial, stream);
+                         prob_partial, z_partial, block_counts, stream);
   return hipErrorInvalidValue;  // more than 256 experts need the workspace or a logits buffer
 }
 
@@ -992,7 +1188,7 @@ hipError_t launch_topk_from_logits(const float* logits, int64_t T, int E, int k,
                                    int score_fn, int32_t* topk_ids, float* topk_w,
                                    float* prob_partial, float* z_partial, hipStream_t stream) {
   return launch_topk_any(logits, 1, nullptr, T, E, k, score_fn, nullptr, topk_ids, topk_w,
-                         prob_partial, z_partial, stream);
+                         prob_partial, z_partial, nullptr, stream);
 }
 
 }  // namespace ntmoe

@@ -170,6 +170,61 @@ def _(ids, weights, num_experts, x, want_x_perm):
             f((A, d) if want_x_perm else (0,), dtype=torch.bfloat16))
 
 
+@_custom_op("ntmoe::router_plan")
+def router_plan(x: Tensor, w_router_t: Tensor, bias: Optional[Tensor], k: int, score_fn: int,
+                want_logits: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor,
+                                            Tensor, Tensor, Tensor, Tensor]:
+    """router followed by route_plan (without x_perm) in one C-ABI call and two launches: the
+    same tensors, the same bits -- (logits, ids, weights, prob_partial, z_partial, counts,
+    offsets, src_row, perm_w, combine_dest, combine_w)."""
+    _on_gpu(x, w_router_t, bias)
+    _require(x.dtype == torch.bfloat16 and x.dim() == 2, "router_plan: x must be bf16 [T, d]")
+    _require(x.stride(1) == 1, "router_plan: x rows must be contiguous")
+    _require(w_router_t.dtype == torch.float32 and w_router_t.is_contiguous(),
+             "router_plan: w_router_t must be contiguous fp32 [d, E]")
+    T, d = x.shape
+    _require(w_router_t.shape[0] == d, "router_plan: w_router_t must be [d, E]")
+    E = w_router_t.shape[1]
+    if bias is not None:
+        _require(bias.dtype == torch.float32 and bias.shape == (E,) and bias.is_contiguous(),
+                 "router_plan: bias must be contiguous fp32 [E]")
+    dev = x.device
+    A = T * k
+    f32, i32 = torch.float32, torch.int32
+    logits = torch.empty((T, E) if want_logits else (0,), device=dev, dtype=f32)
+    ids = torch.empty(T, k, device=dev, dtype=i32)
+    w = torch.empty(T, k, device=dev, dtype=f32)
+    pp = torch.empty(_nblk(T), E, device=dev, dtype=f32)
+    zp = torch.empty(_nblk(T), device=dev, dtype=f32)
+    counts = torch.empty(E, device=dev, dtype=i32)
+    offsets = torch.empty(E + 1, device=dev, dtype=i32)
+    src = torch.empty(A, device=dev, dtype=i32)
+    perm_w = torch.empty(A, device=dev, dtype=f32)
+    cdest = torch.empty(T, k, device=dev, dtype=i32)
+    cw = torch.empty(T, k, device=dev, dtype=f32)
+    lib = nat.load()
+    ws_bytes = lib.nt_moe_router_plan_workspace_bytes(T, d, E, k)
+    ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    st = lib.nt_moe_router_plan(ptr(x), x.stride(0), ptr(w_router_t), ptr(bias), T, d, E, k,
+                                score_fn, ptr(logits) if want_logits else None, ptr(ids), ptr(w),
+                                ptr(pp), ptr(zp), ptr(counts), ptr(offsets), ptr(src),
+                                ptr(perm_w), ptr(cdest), ptr(cw), ptr(ws), ws_bytes, _stream(dev))
+    nat.check(st, "ntmoe::router_plan")
+    return logits, ids, w, pp, zp, counts, offsets, src, perm_w, cdest, cw
+
+
+@router_plan.register_fake
+def _(x, w_router_t, bias, k, score_fn, want_logits):
+    T, E = x.shape[0], w_router_t.shape[1]
+    A = T * k
+    f = x.new_empty
+    f32, i32 = torch.float32, torch.int32
+    return (f((T, E) if want_logits else (0,), dtype=f32), f((T, k), dtype=i32),
+            f((T, k), dtype=f32), f((_nblk(T), E), dtype=f32), f((_nblk(T),), dtype=f32),
+            f((E,), dtype=i32), f((E + 1,), dtype=i32), f((A,), dtype=i32), f((A,), dtype=f32),
+            f((T, k), dtype=i32), f((T, k), dtype=f32))
+
+
 # ---------------------------------------------------------------------------------------------
 # grouped expert FFN
 
@@ -648,10 +703,16 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
                      perm_w=empty(0, dtype=f32), combine_dest=empty(0, top_k),
                      combine_w=empty(0, top_k, dtype=f32))
         return x.new_empty(0, x.shape[1]), torch.zeros(3, device=dev, dtype=f32), state
-    logits, ids, w, pp, zp = router.raw(x, w_router_t, logit_bias, top_k, score_fn, want_logits)
-    mark("router")
-    counts, offsets, src, perm_w, cdest, cw, x_perm = route_plan.raw(
-        ids, w, E, x if permute_rows else None, permute_rows)
+    if permute_rows:
+        logits, ids, w, pp, zp = router.raw(x, w_router_t, logit_bias, top_k, score_fn,
+                                            want_logits)
+        mark("router")
+        counts, offsets, src, perm_w, cdest, cw, x_perm = route_plan.raw(ids, w, E, x, True)
+    else:  # one call, two launches: the router's top-k counts for the plan
+        (logits, ids, w, pp, zp, counts, offsets, src, perm_w, cdest,
+         cw) = router_plan.raw(x, w_router_t, logit_bias, top_k, score_fn, want_logits)
+        x_perm = None
+        mark("router")
     mark("route_plan")
     up_epi = nat.EPI_SWIGLU if activation == nat.ACT_SWIGLU else nat.EPI_RELU2
     if w1.dtype == torch.uint8:

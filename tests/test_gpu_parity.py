@@ -152,6 +152,49 @@ def test_streamed_router_bit_exact(case):
     torch.testing.assert_close(zp.cpu().double().sum(), lse2, rtol=1e-5, atol=1e-5)
 
 
+# router_plan (router + plan in one call, the router's top-k counting each 64-token block's
+# assignments): the chunk-per-wave kernel (E <= 32, d <= 1024), the fused range, logits + top-k
+# and planes paths, the streamed kernel, ragged last blocks, E not dividing 256, and the T3 cell.
+ROUTER_PLAN = SMALL + MID + STREAM + [
+    Case("t3-T16384-d1280-E256-k8", 16384, 1280, 256, 8, 64, seed=24),
+    Case("E64-T16400-d2048-k8-zipf", 16400, 2048, 64, 8, 64, zipf_bias=1.2, seed=25),
+    Case("E128-T8192-d2048-k8-sigmoid", 8192, 2048, 128, 8, 64, score_fn=1, seed=26),
+]
+
+
+@pytest.mark.parametrize("case", ROUTER_PLAN, ids=lambda c: c.name)
+def test_router_plan_equals_router_then_route_plan(case):
+    """Every output of the one-call router + plan bit-identical to router followed by
+    route_plan (the histogram path), on the same inputs."""
+    from nexttransformer_amd import ops
+    x, router, bias = make_router_inputs(case)
+    dev = torch.device("cuda")
+    x, wt = x.to(dev), router.t().contiguous().to(dev)
+    bias = None if bias is None else bias.to(dev)
+    ref = ops.router(x, wt, bias, case.k, case.score_fn, True)
+    ref = ref + ops.route_plan(ref[1], ref[2], case.E, None, False)[:6]
+    got = ops.router_plan(x, wt, bias, case.k, case.score_fn, True)
+    torch.cuda.synchronize()
+    names = ("logits", "ids", "weights", "prob_partial", "z_partial", "counts", "offsets",
+             "src_row", "perm_w", "combine_dest", "combine_w")
+    for name, a, b in zip(names, got, ref):
+        assert a.shape == b.shape, name
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), name
+    assert int(got[5].sum()) == case.T * case.k
+
+
+def test_router_plan_empty_batch():
+    from nexttransformer_amd import ops
+    dev = torch.device("cuda")
+    x = torch.empty(0, 256, device=dev, dtype=torch.bfloat16)
+    wt = torch.randn(256, 16, device=dev)
+    out = ops.router_plan(x, wt, None, 2, 0, False)
+    torch.cuda.synchronize()
+    assert out[1].shape == (0, 2) and out[7].shape == (0,)
+    assert torch.equal(out[5].cpu(), torch.zeros(16, dtype=torch.int32))
+    assert torch.equal(out[6].cpu(), torch.zeros(17, dtype=torch.int32))
+
+
 def test_topk_on_reference_logits_and_ties():
     """Top-k on the reference's own F.linear logits, plus constructed ties (lower index wins)."""
     from nexttransformer_amd import ops
