@@ -321,9 +321,38 @@ __global__ __launch_bounds__(256) void plan_c64_kernel(
   }
   // Column sums of the table: groups of E / 4 threads, each thread four consecutive experts
   // (16-byte loads; E % 4 == 0, else one expert per thread); group g sums blocks g, g + G, ...
+  // When E / 4 divides 64 the groups of a wave are combined by shuffles first, so the LDS
+  // partials are one per wave.
   const int pre_end = 4 * blk;  // 64-token blocks before this workgroup's first token
   int G;
-  if (E % 4 == 0) {
+  const bool shfl = E % 4 == 0 && 64 % (E / 4) == 0;
+  if (shfl) {
+    const int E4 = E / 4;  // a power of two <= 64
+    const int GT = 256 / E4;
+    const int g = tid / E4, e4 = tid - g * E4;
+    i32x4 pre = {0, 0, 0, 0}, tot = {0, 0, 0, 0};
+#pragma unroll 16
+    for (int b = g; b < nblk64; b += GT) {
+      const i32x4 c = *reinterpret_cast<const i32x4*>(block_counts64 + (int64_t)b * E + 4 * e4);
+      tot += c;
+      if (b < pre_end) pre += c;
+    }
+    for (int m = E4; m < 64; m <<= 1) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        pre[q] += __shfl_xor(pre[q], m);
+        tot[q] += __shfl_xor(tot[q], m);
+      }
+    }
+    G = 4;  // one partial per wave
+    if (lane < E4) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        pre_s[w * E + 4 * lane + q] = pre[q];
+        tot_s[w * E + 4 * lane + q] = tot[q];
+      }
+    }
+  } else if (E % 4 == 0) {
     const int E4 = E / 4;
     G = 256 / E4;
     const int g = tid / E4, e4 = tid - g * E4;
