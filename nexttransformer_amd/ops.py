@@ -684,7 +684,8 @@ def moe_forward(x, w_router_t, w1, w2, *, top_k, score_fn=nat.SCORE_SOFTMAX,
     block scales (w*_scale, from quantize_fp8_blockwise); the token rows and the intermediate
     h are then quantised per row and both projections run on the fp8 grouped GEMM.
     `mark(name)`, when given, is called after each stage is enqueued (used to place timing
-    events on the stream). keep (bf16 experts): the state also holds what moe_backward reads
+    events on the stream; without permute_rows the router and the route plan are one call, so
+    the "router" stage holds both and "route_plan" is empty). keep (bf16 experts): the state also holds what moe_backward reads
     (h, y, the shared expert's h, the router's aux partials and the fc1 pre-activations of
     the routed and the shared expert from their up projections' launches, with packed weights
     or plain ones that plain_keep_supported takes; otherwise moe_backward recomputes them).
