@@ -151,9 +151,9 @@ int nt_moe_route_plan(const uint16_t* x, int64_t ld_x, const int32_t* topk_ids,
 /*
  * Router and route plan in one call: the outputs of nt_moe_router_fwd followed by those of
  * nt_moe_route_plan without x_perm, identical bits. When ceil(T/64) * E <= 16384 in two launches
- * instead of three: the router's top-k also counts each 64-token block's assignments per expert
- * into the workspace, and the plan kernel ranks each block's assignments itself (no histogram
- * launch); larger shapes make exactly the router and route-plan launches. Replaces
+ * instead of three: the router's top-k also writes each 64-token block's assignments per expert
+ * and each assignment's rank within its block into the workspace, so the plan needs no
+ * histogram launch; larger shapes make exactly the router and route-plan launches. Replaces
  * NativeRouter.gating + TopKRouter (megatron_moe.py:95-100, 43) followed by
  * mapping.T.nonzero() / mapping.sum(0) (megatron_moe.py:142-144).
  *   workspace  nt_moe_router_plan_workspace_bytes(T, d, E, k) bytes (never smaller)

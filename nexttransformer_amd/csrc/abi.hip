@@ -407,9 +407,10 @@ bool plan_from_counts(int64_t T, int E) {
 
 size_t nt_moe_router_plan_workspace_bytes(int64_t T, int32_t d, int32_t E, int32_t k) {
   if (T <= 0 || d <= 0 || E <= 0 || k <= 0) return 0;
-  const int64_t nblk64 = (T + NT_MOE_ROUTE_BLOCK - 1) / NT_MOE_ROUTE_BLOCK;
-  const size_t plan = plan_from_counts(T, E) ? align256((size_t)nblk64 * E * 4)
-                                             : route_ws_bytes(T, k, E);
+  // the router's counts table and ranks (route_ranks_offset), or the route plan's workspace
+  const size_t plan = plan_from_counts(T, E)
+                          ? align256((size_t)(route_ranks_offset(T, E) + T * (int64_t)k) * 4)
+                          : route_ws_bytes(T, k, E);
   return align256(router_workspace_need(T, d, E)) + plan;
 }
 

@@ -62,6 +62,12 @@ size_t router_workspace_need(int64_t T, int d, int E);
 hipError_t launch_histogram_scan(const int32_t* topk_ids, int64_t T, int k, int E,
                                  int32_t* counts, int32_t* offsets, int32_t* ranks,
                                  int32_t* block_counts, hipStream_t stream);
+// The router's route-plan outputs (launch_router's block_counts): the per-64-token-block expert
+// counts [ceil(T/64)][E], then, from this offset (ints), each assignment's rank within its block
+// among the tokens that chose its expert [T * k].
+__host__ __device__ inline int64_t route_ranks_offset(int64_t T, int E) {
+  return ((T + kRouteBlock - 1) / kRouteBlock * E + 63) / 64 * 64;
+}
 // The route plan from the router's per-64-token-block expert counts (ceil(T/64) x E, written by
 // launch_router's block_counts): plan_kernel without the histogram launch. E <= 256.
 hipError_t launch_plan_from_counts(const int32_t* topk_ids, const float* topk_w, int64_t T, int k,

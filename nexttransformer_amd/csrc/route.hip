@@ -285,38 +285,38 @@ __global__ __launch_bounds__(256) void plan_kernel(
   }
 }
 
-// plan_kernel with the counts table at the router's 64-token granularity (block_counts64[b][e]:
-// assignments of tokens [64 b, 64 b + 64) to expert e, written by the router's top-k), so the
-// histogram launch is not needed: each workgroup ranks its own 256 tokens' assignments in LDS
-// (histogram_kernel's bit masks, one wave per 64 tokens) and takes its expert bases from the
-// table -- every column summed over the whole table, in the same fixed shape in every
-// workgroup, with the blocks before its first token as its prefix. All integer: the same
-// destinations as histogram_kernel + plan_kernel.
+// plan_kernel from the router's outputs at its 64-token granularity: block_counts64[b][e]
+// (assignments of tokens [64 b, 64 b + 64) to expert e) and each assignment's rank within its
+// 64-token block (route_ranks_offset), both written by the router's top-k, so the histogram
+// launch is not needed. One workgroup per 256 tokens (its four 64-token blocks, one per wave):
+// every column of the table summed over the whole table and over the blocks before its own, in
+// the same fixed shape in every workgroup, plus the counts of its own earlier 64-token blocks.
+// All integer: the same destinations as histogram_kernel + plan_kernel.
 __global__ __launch_bounds__(256) void plan_c64_kernel(
     const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int64_t T, int k,
     int E, int nblk64, const int32_t* __restrict__ block_counts64, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ src_row, float* __restrict__ perm_w,
     int32_t* __restrict__ combine_dest, float* __restrict__ combine_w) {
-  extern __shared__ __align__(16) unsigned char smem[];
-  uint64_t* mask = reinterpret_cast<uint64_t*>(smem);              // [4][E]
-  int32_t* wave_prefix = reinterpret_cast<int32_t*>(mask + 4 * E);  // [4][E]
   __shared__ int32_t pre_s[1024], tot_s[1024];  // [G][E] partial column sums, G * E <= 1024
   __shared__ int32_t base_s[NT_MOE_MAX_EXPERTS];
+  __shared__ int32_t sub_s[4][NT_MOE_MAX_EXPERTS];  // earlier 64-token blocks of this workgroup
   __shared__ int32_t wave_tot[4];
   const int tid = threadIdx.x, lane = lane_id(), w = wave_id();
   const int blk = blockIdx.x;
   const int64_t t = (int64_t)blk * kHistBlock + tid;
   const bool live = t < T;
-  for (int i = tid; i < 4 * E; i += blockDim.x) mask[i] = 0ull;
-  int ev[NT_MOE_MAX_TOPK];
+  const int32_t* __restrict__ ranks64 = block_counts64 + route_ranks_offset(T, E);
+  int ev[NT_MOE_MAX_TOPK], rv[NT_MOE_MAX_TOPK];
   float wv[NT_MOE_MAX_TOPK];
 #pragma unroll
   for (int j = 0; j < NT_MOE_MAX_TOPK; ++j) {
     ev[j] = 0x7fffffff;
+    rv[j] = 0;
     wv[j] = 0.f;
     if (live && j < k) {
       ev[j] = topk_ids[t * k + j];
       wv[j] = topk_w[t * k + j];
+      rv[j] = ranks64[t * k + j];  // in bounds; used only for valid ids
     }
   }
   // Column sums of the table: groups of E / 4 threads, each thread four consecutive experts
@@ -385,23 +385,23 @@ __global__ __launch_bounds__(256) void plan_c64_kernel(
       tot_s[tid] = tot;
     }
   }
-  __syncthreads();  // masks cleared
+  // this workgroup's own 64-token blocks, exclusive prefix over them per expert
+  if (tid < E) {
+    int run = 0;
 #pragma unroll
-  for (int j = 0; j < NT_MOE_MAX_TOPK; ++j)
-    if (j < k && (unsigned)ev[j] < (unsigned)E)
-      atomicOr(reinterpret_cast<unsigned long long*>(&mask[w * E + ev[j]]), 1ull << lane);
+    for (int q = 0; q < 4; ++q) {
+      const int b = pre_end + q;
+      const int c = b < nblk64 ? block_counts64[(int64_t)b * E + tid] : 0;
+      sub_s[q][tid] = run;
+      run += c;
+    }
+  }
   __syncthreads();
   int before = 0, total = 0;  // thread tid owns expert tid
   if (tid < E) {
     for (int q = 0; q < G; ++q) {
       before += pre_s[q * E + tid];
       total += tot_s[q * E + tid];
-    }
-    int run = 0;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      wave_prefix[q * E + tid] = run;
-      run += __popcll(mask[q * E + tid]);
     }
   }
   const int incl = group_inclusive_scan(total, 64);
@@ -422,7 +422,6 @@ __global__ __launch_bounds__(256) void plan_c64_kernel(
 
   if (!live) return;
   const int64_t A = T * k;
-  const uint64_t below = (1ull << lane) - 1ull;
   int dv[NT_MOE_MAX_TOPK];
 #pragma unroll
   for (int j = 0; j < NT_MOE_MAX_TOPK; ++j) {
@@ -430,7 +429,7 @@ __global__ __launch_bounds__(256) void plan_c64_kernel(
     if (j < k) {
       if ((unsigned)ev[j] < (unsigned)E) {
         const int ej = ev[j];
-        int dest = base_s[ej] + wave_prefix[w * E + ej] + __popcll(mask[w * E + ej] & below);
+        int dest = base_s[ej] + sub_s[w][ej] + rv[j];
         dest = dest < 0 ? 0 : (dest >= A ? (int)(A - 1) : dest);
         src_row[dest] = (int32_t)t;
         if (perm_w) perm_w[dest] = wv[j];
@@ -521,8 +520,7 @@ hipError_t launch_plan_from_counts(const int32_t* topk_ids, const float* topk_w,
   if (T == 0 || E > 256) return hipErrorInvalidValue;
   const int64_t nblk = ceil_div(T, kHistBlock);
   const int nblk64 = ceil_div(T, kRouteBlock);
-  const size_t lds = (size_t)4 * E * (sizeof(uint64_t) + sizeof(int32_t));
-  hipLaunchKernelGGL(plan_c64_kernel, dim3((unsigned)nblk), dim3(256), lds, stream, topk_ids,
+  hipLaunchKernelGGL(plan_c64_kernel, dim3((unsigned)nblk), dim3(256), 0, stream, topk_ids,
                      topk_w, T, k, E, nblk64, block_counts64, counts, offsets, src_row, perm_w,
                      combine_dest, combine_w);
   return hipGetLastError();

@@ -46,9 +46,10 @@ constexpr int kBufferWord3 = 0x00020000;
 
 __host__ __device__ inline int lg_tile_bytes(int E) { return kRouteBlock * (E + 1) * 4; }
 __host__ __device__ inline int zt_offset(int E) { return (lg_tile_bytes(E) + 15) & ~15; }
-// After the logits tile: zt (64 floats), then the block's per-expert assignment counts (E ints).
+// After the logits tile: zt (64 floats), then the block's per-expert assignment masks (E
+// 64-bit words, bit tt set when token tt of the block chose the expert).
 __host__ __device__ inline int cnt_offset(int E) { return zt_offset(E) + kRouteBlock * 4; }
-__host__ __device__ inline size_t router_lds_bytes(int E) { return cnt_offset(E) + (size_t)E * 4; }
+__host__ __device__ inline size_t router_lds_bytes(int E) { return cnt_offset(E) + (size_t)E * 8; }
 
 // LDS stages of the fused kernel: for each feature range, 64 features of x (64 tokens, rows
 // padded to kXPitch bf16) and of the router weights for all expert blocks, stored so that a
@@ -90,11 +91,15 @@ __device__ __forceinline__ void topk_and_scores(float* lg, float* zt, int64_t t0
                                 float* __restrict__ topk_w, float* __restrict__ prob_partial,
                                 float* __restrict__ z_partial, int32_t* __restrict__ block_counts) {
   static_assert(LPT == 1 || LPT == 2 || LPT == 4 || LPT == 8 || LPT == 16, "lanes per token");
-  // The block's per-expert assignment counts (for the route plan): LDS integer adds, so the
-  // result does not depend on their order.
-  int* cnt = reinterpret_cast<int*>(reinterpret_cast<unsigned char*>(zt) + kRouteBlock * 4);
+  // The block's assignments per expert, for the route plan: a 64-bit mask per expert (bit tt
+  // for token tt; LDS ORs, so the result does not depend on their order) gives the counts
+  // (popcount) and each assignment's rank among the block's tokens that chose its expert
+  // (popcount of the lower bits) -- block_counts[blk][e] and, after the table,
+  // ranks[t k + j] (route_ranks_offset).
+  unsigned long long* msk =
+      reinterpret_cast<unsigned long long*>(reinterpret_cast<unsigned char*>(zt) + kRouteBlock * 4);
   if (block_counts)
-    for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) msk[e] = 0ull;
   const int ldl = E + 1;
   const int tt = threadIdx.x / LPT;   // token within the block
   const int sub = threadIdx.x % LPT;  // which of the LPT expert strides this lane scans
@@ -184,7 +189,7 @@ __device__ __forceinline__ void topk_and_scores(float* lg, float* zt, int64_t t0
   if (block_counts && t < T) {
 #pragma unroll
     for (int j = 0; j < KMAX; ++j)
-      if (j < k && j % LPT == sub) atomicAdd(&cnt[oi[j]], 1);
+      if (j < k && j % LPT == sub) atomicOr(&msk[oi[j]], 1ull << tt);
   }
 
   // Per-block column sums in a fixed order (deterministic): P consecutive lanes per expert,
@@ -211,7 +216,14 @@ __device__ __forceinline__ void topk_and_scores(float* lg, float* zt, int64_t t0
   }
   if (block_counts) {
     __syncthreads();
-    for (int e = threadIdx.x; e < E; e += blockDim.x) block_counts[blk * E + e] = cnt[e];
+    for (int e = threadIdx.x; e < E; e += blockDim.x) block_counts[blk * E + e] = __popcll(msk[e]);
+    if (t < T) {
+      int32_t* ranks = block_counts + route_ranks_offset(T, E);
+      const unsigned long long below = (1ull << tt) - 1ull;
+#pragma unroll
+      for (int j = 0; j < KMAX; ++j)
+        if (j < k && j % LPT == sub) ranks[t * k + j] = __popcll(msk[oi[j]] & below);
+    }
   }
 }
 
