@@ -251,8 +251,17 @@ __global__ __launch_bounds__(256, 2) void grouped_wgrad_tr_kernel(
   int* idx_ring = reinterpret_cast<int*>(smem + kTRing * G::kStage);  // [kTIdx][kTK]
   const int ntn = (N + TN - 1) / TN, ntm = (M + TM - 1) / TM;
   const int per_seg = ntn * ntm;
-  const int split = blockIdx.x / (num_segments * per_seg);
-  const int rest = blockIdx.x - split * num_segments * per_seg;
+  // Workgroup b runs on XCD b % 8: give each XCD a contiguous range of the tile list, so the
+  // tiles that share a segment's slabs (all of a segment's tiles, which read the same rows) run
+  // at about the same time behind one L2 and each slab comes from HBM once.
+  int blk;
+  {
+    const int nb = (int)gridDim.x, q = nb / 8, r = nb % 8;
+    const int xcd = (int)blockIdx.x % 8, slot = (int)blockIdx.x / 8;
+    blk = xcd * q + (xcd < r ? xcd : r) + slot;
+  }
+  const int split = blk / (num_segments * per_seg);
+  const int rest = blk - split * num_segments * per_seg;
   const int s = rest / per_seg;
   const int tile = rest - s * per_seg;
   const int n0 = (tile / ntm) * TN, m0 = (tile % ntm) * TM;
