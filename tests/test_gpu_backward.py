@@ -258,6 +258,37 @@ def test_grouped_wgrad_shapes_fp32_and_bf16(N, M, gather, splits):
             torch.testing.assert_close(got32[s].double(), ref, rtol=1e-5, atol=1e-4)
 
 
+@pytest.mark.parametrize("gather,splits", [(False, 1), (True, 1), (True, 2)])
+def test_grouped_wgrad_walks_many_tiles(gather, splits):
+    """More tiles than the persistent grid holds (64 segments x 16 tiles of 128 x 256, up to
+    twice that with split K), so each workgroup runs several tiles back to back with the copy
+    pipeline crossing tile boundaries: empty segments between non-empty ones, one-row and
+    one-slab segments, segments of many slabs; fp32 output against float64."""
+    from nexttransformer_amd import ops
+    gen = torch.Generator().manual_seed(7 + 2 * gather + splits)
+    S, N, M = 64, 512, 1024
+    sizes = torch.randint(0, 160, (S,), generator=gen)
+    sizes[torch.randperm(S, generator=gen)[:12]] = 0
+    sizes[3], sizes[4], sizes[5], sizes[6] = 1, 32, 33, 300
+    total = int(sizes.sum())
+    offsets = torch.cat([torch.zeros(1, dtype=torch.int64), sizes.cumsum(0)]).to(torch.int32)
+    a = torch.randn(total, N, generator=gen).to(torch.bfloat16)
+    b_rows = 211 if gather else total
+    b = torch.randn(b_rows, M, generator=gen).to(torch.bfloat16)
+    src = torch.randint(0, b_rows, (total,), generator=gen, dtype=torch.int32) if gather else None
+    got = ops.grouped_wgrad(a.cuda(), b.cuda(), None if src is None else src.cuda(),
+                            offsets.cuda(), total, splits, out_fp32=True).cpu()
+    bb = (b[src.long()] if gather else b).double()
+    ad = a.double()
+    for s in range(S):
+        lo, hi = int(offsets[s]), int(offsets[s + 1])
+        if hi == lo:
+            assert torch.equal(got[s], torch.zeros(N, M)), s
+        else:
+            torch.testing.assert_close(got[s].double(), ad[lo:hi].t() @ bb[lo:hi], rtol=1e-5,
+                                       atol=1e-4, msg=f"segment {s} ({hi - lo} rows)")
+
+
 # the last two: a partial N tile (ReLU^2, 320 columns: the T3 cell's up projection) and an odd
 # K-step count with a six-block N tile (K = 320, SwiGLU 96 columns)
 @pytest.mark.parametrize("activation,d,H", [(0, 512, 256), (1, 512, 256), (1, 1280, 320),
