@@ -616,7 +616,10 @@ __global__ __launch_bounds__(64 * EBW) void router_stream_kernel(
   const uint32_t sel = hk ? 0x07060C0Cu : 0x05040C0Cu;
   const int row0 = lane & 31, row1 = 32 + (lane & 31);
   const int sw0 = (row0 >> 1) & 7, sw1 = (row1 >> 1) & 7;
-  auto compute = [&](int st, const float (&wr)[32], floatx16& c0, floatx16& c1)
+  // The stage's chains, with the next stage's weight loads (wn) issued four at a time after each
+  // group of eight MFMAs: issued together at the stage's start they filled the wave's memory
+  // queue and held back its first MFMAs.
+  auto compute = [&](int st, const float (&wr)[32], float (&wn)[32], floatx16& c0, floatx16& c1)
                      __attribute__((always_inline)) {
     const int left = d - st * 64;
     const int ng = left >= 64 ? 8 : left / 8;
@@ -639,31 +642,47 @@ __global__ __launch_bounds__(64 * EBW) void router_stream_kernel(
         c1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, wr[4 * q + j], c1, 0, 0, 0);
       }
     };
+    auto next_w = [&](int q) __attribute__((always_inline)) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int f = (st + 1) * 64 + 8 * q + 2 * j;
+        wn[4 * q + j] = load_w_asm(wrsrc, voff_w, (f < d - 2 ? f : d - 2) * E * 4);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
     if (ng == 8) {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) group(q);
+      for (int q = 0; q < 8; ++q) {
+        group(q);
+        next_w(q);
+      }
     } else {
 #pragma unroll
-      for (int q = 0; q < 8; ++q)
+      for (int q = 0; q < 8; ++q) {
         if (q < ng) group(q);
+        next_w(q);
+      }
     }
   };
-  // Stage st: issue the weights of st + 1 and the x copies of st + 2, wait until x(st) and W(st)
-  // are complete (at most the loads issued after W(st) outstanding: x(st + 1), W(st + 1),
-  // x(st + 2); vector memory operations retire in order), then the chains. Past the last stage
-  // these loads read in-bounds data nobody uses.
+  // Stage st: issue the x copies of st + 2, wait until x(st) and W(st) are complete (at most the
+  // operations issued after W(st) outstanding: x(st + 1) and x(st + 2) for stage 0, whose
+  // weights were loaded before the loop, and x(st + 2) later, W(st) having been issued during
+  // stage st - 1's chains after x(st + 1); vector memory operations retire in order), then the
+  // chains, which issue W(st + 1). Past the last stage these loads read in-bounds data nobody
+  // uses.
   auto stage = [&](int st, float (&wcur)[32], float (&wnext)[32], floatx16& c0, floatx16& c1)
                    __attribute__((always_inline)) {
-    issue_w(st + 1, wnext);
     issue_x(st + 2, (st + 2) % kSRing);
-    stage_wait<2 * G::kXCopies + 32>(wcur);
+    if (st == 0) stage_wait<2 * G::kXCopies>(wcur);
+    else stage_wait<G::kXCopies>(wcur);
     // Barrier without a memory fence (a fence would wait for the prefetches too): every wave's
     // copies of stage st have landed (its own vmcnt wait above), and every wave's reads of the
     // slot refilled next stage are complete (lgkmcnt).
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    compute(st, wcur, c0, c1);
+    compute(st, wcur, wnext, c0, c1);
   };
 
   float wa[32], wb[32];
