@@ -49,6 +49,15 @@
 namespace ntmoe {
 namespace {
 
+// f(integral_constant<int, i>) for i = 0 .. N-1, each index a constant expression.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>());
+    static_for<I + 1, N>(f);
+  }
+}
+
 typedef __attribute__((address_space(1))) void gvoid;
 typedef __attribute__((address_space(3))) void lvoid;
 
@@ -474,30 +483,81 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
       for (int n = 0; n < PF; ++n) fr[n] = frag(n);
       asm volatile("" ::: "memory");
       if (kt + 1 == nks && tile_ok(ti + 1)) w_base(tile_at(ti + 1), wb_next);
-      load_b(wb, wb_next, kt + 1, bn);  // past the last tile: re-reads of its first step
-      asm volatile("" ::: "memory");
-      if (!ODD) {
-        produce();
+      // The step's vector memory operations -- B(g + 1) as kWB x 4 loads of 1 KB, then on even
+      // steps the two token-row stages (produce) -- go out spread between the MFMA groups, in
+      // that order: issued together ahead of the MFMAs they filled the wave's memory queue and
+      // held back its first products (config 2 up projection 139 -> 132 us, down 85 -> 78 us).
+      // EDGE: the two stages follow the last group; EDGE without the gather, whose registers
+      // are at the limit, keeps the loads ahead of the MFMAs.
+      constexpr bool kSpread = GATHER || !EDGE;
+      if constexpr (kSpread) {
+        const uint16_t* bsrc[kWB];
+#pragma unroll
+        for (int rb = 0; rb < kWB; ++rb)  // past the last tile: re-reads of its first step
+          bsrc[rb] = kt + 1 >= nks
+                         ? wb_next[rb]
+                         : wb[rb] + (int64_t)(kt + 1 < nk ? kt + 1 : nk - 1) * kBlockElems;
+        constexpr int kItems = kWB * 4 + (ODD || EDGE ? 0 : 2);
+        auto item = [&](auto i_c) __attribute__((always_inline)) {
+          constexpr int i = decltype(i_c)::value;
+          if constexpr (i < kWB * 4) {
+            asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3"
+                         : "=v"(bn[i / 4][i % 4])
+                         : "v"(b_lane), "s"(bsrc[i / 4]), "n"((i % 4) * 1024)
+                         : "memory");
+          } else {
+            produce();
+            asm volatile("" ::: "memory");
+          }
+        };
+        if constexpr (NM == 0) static_for<0, kItems>(item);
+        static_for<0, NM>([&](auto n_c) __attribute__((always_inline)) {
+          constexpr int n = decltype(n_c)::value;
+#pragma unroll
+          for (int rb = 0; rb < kWB; ++rb)
+            acc[rb][n % NJd] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8, bc[rb][n / NJd]), fr[n % PFd], acc[rb][n % NJd], 0,
+                0, 0);
+          if constexpr (n + PF < NM) fr[n % PFd] = frag(n + PF);
+          // this group's share of the memory operations, after its MFMAs and fragment read
+          __builtin_amdgcn_sched_barrier(0);
+          static_for<n * kItems / NM, (n + 1) * kItems / NM>(item);
+          __builtin_amdgcn_sched_barrier(0);
+        });
+        if constexpr (EDGE && !ODD) {
+          produce();
+          asm volatile("" ::: "memory");
+          produce();
+          asm volatile("" ::: "memory");
+        }
+      } else {
+        load_b(wb, wb_next, kt + 1, bn);  // past the last tile: re-reads of its first step
         asm volatile("" ::: "memory");
-        produce();
-        asm volatile("" ::: "memory");
-      }
+        if (!ODD) {
+          produce();
+          asm volatile("" ::: "memory");
+          produce();
+          asm volatile("" ::: "memory");
+        }
 #pragma unroll
-      for (int n = 0; n < NM; ++n) {
+        for (int n = 0; n < NM; ++n) {
 #pragma unroll
-        for (int rb = 0; rb < kWB; ++rb)
-          acc[rb][n % NJd] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(bf16x8, bc[rb][n / NJd]), fr[n % PFd], acc[rb][n % NJd], 0, 0, 0);
-        if (n + PF < NM) fr[n % PFd] = frag(n + PF);
-      }
-      // Keep PF fragment reads in flight: (kWB MFMAs, 1 read) groups, then the last PF groups'
-      // MFMAs. Without this the scheduler pulls each read next to its MFMA and waits on it.
+          for (int rb = 0; rb < kWB; ++rb)
+            acc[rb][n % NJd] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8, bc[rb][n / NJd]), fr[n % PFd], acc[rb][n % NJd], 0,
+                0, 0);
+          if (n + PF < NM) fr[n % PFd] = frag(n + PF);
+        }
+        // Keep PF fragment reads in flight: (kWB MFMAs, 1 read) groups, then the last PF
+        // groups' MFMAs. Without this the scheduler pulls each read next to its MFMA and waits
+        // on it.
 #pragma unroll
-      for (int n = 0; n < NM - PF; ++n) {
-        __builtin_amdgcn_sched_group_barrier(0x008, kWB, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        for (int n = 0; n < NM - PF; ++n) {
+          __builtin_amdgcn_sched_group_barrier(0x008, kWB, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if constexpr (PF > 0) __builtin_amdgcn_sched_group_barrier(0x008, kWB * PF, 0);
       }
-      if constexpr (PF > 0) __builtin_amdgcn_sched_group_barrier(0x008, kWB * PF, 0);
       // Even step: the two stages and index loads issued after B(g + 1) may stay in flight.
       wait_b(std::integral_constant<int, ODD ? 0 : 2 * (kAQ + G)>(), bn);
       ++g;
