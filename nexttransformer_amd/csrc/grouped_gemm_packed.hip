@@ -519,9 +519,14 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
                 __builtin_bit_cast(bf16x8, bc[rb][n / NJd]), fr[n % PFd], acc[rb][n % NJd], 0,
                 0, 0);
           if constexpr (n + PF < NM) fr[n % PFd] = frag(n + PF);
-          // this group's share of the memory operations, after its MFMAs and fragment read
+          // this group's share of the memory operations, after its MFMAs and fragment read:
+          // the weight loads over the first half of the groups, the stages at 1/2 and 3/4
           __builtin_amdgcn_sched_barrier(0);
-          static_for<n * kItems / NM, (n + 1) * kItems / NM>(item);
+          static_for<0, kItems>([&](auto i_c) __attribute__((always_inline)) {
+            constexpr int i = decltype(i_c)::value;
+            constexpr int at = i < kWB * 4 ? i * (NM / 2) / (kWB * 4) : NM / 2 + (i - kWB * 4) * (NM / 4);
+            if constexpr (at == n) item(i_c);
+          });
           __builtin_amdgcn_sched_barrier(0);
         });
         if constexpr (EDGE && !ODD) {
