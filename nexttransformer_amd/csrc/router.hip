@@ -793,7 +793,10 @@ __global__ __launch_bounds__(64 * NW) void router_chunk_kernel(
     const int row0 = lane & 31, row1 = 32 + (lane & 31);
     const int sw0 = (row0 >> 1) & 7, sw1 = (row1 >> 1) & 7;
     floatx16 c0 = {}, c1 = {};
-    auto compute = [&](int h, const float (&wr)[32]) __attribute__((always_inline)) {
+    // Tile h's chains; with issue, tile 1's weight loads (into wn) go out four at a time after
+    // each group of eight MFMAs (issued together ahead of them they held back the products).
+    auto compute = [&](int h, const float (&wr)[32], float (&wn)[32], bool issue)
+                       __attribute__((always_inline)) {
       const int left = fe - (f0 + 64 * h);
       const int ng = left >= 64 ? 8 : (left > 0 ? left / 8 : 0);
       const unsigned char* tile = xs + h * kSTile;
@@ -812,25 +815,41 @@ __global__ __launch_bounds__(64 * NW) void router_chunk_kernel(
           c1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, wr[4 * q + j], c1, 0, 0, 0);
         }
       };
+      auto next_w = [&](int q) __attribute__((always_inline)) {
+        if (issue) {
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int f = f0 + 64 + 8 * q + 2 * j;
+            wn[4 * q + j] = load_w_asm(wrsrc, voff_w, (f < d - 2 ? f : d - 2) * E * 4);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
       if (ng == 8) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) group(q);
+        for (int q = 0; q < 8; ++q) {
+          group(q);
+          next_w(q);
+        }
       } else {
 #pragma unroll
-        for (int q = 0; q < 8; ++q)
+        for (int q = 0; q < 8; ++q) {
           if (q < ng) group(q);
+          next_w(q);
+        }
       }
     };
     float wlo[32], whi[32];
     issue_tile(0);
     issue_w(0, wlo);
     issue_tile(1);
-    issue_w(1, whi);
-    // Tile 0 and its weights are the first 40 operations: at most the 40 after them outstanding.
-    stage_wait<40>(wlo);
-    compute(0, wlo);
+    // Tile 0 and its weights are the first 40 operations: at most tile 1's 8 copies after them
+    // outstanding. Tile 1's weights go out during tile 0's chains.
+    stage_wait<8>(wlo);
+    compute(0, wlo, whi, true);
     stage_wait<0>(whi);
-    compute(1, whi);
+    compute(1, whi, whi, false);
     // Chunk sums over this wave's own tiles (its LDS reads of them are complete: a wave's LDS
     // operations run in order).
     float* cs = reinterpret_cast<float*>(xs);
