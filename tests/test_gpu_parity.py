@@ -213,6 +213,36 @@ def test_topk_on_reference_logits_and_ties():
     assert ids[:64].cpu().tolist() == [[0, 1, 2, 3]] * 64
 
 
+def test_topk_256_experts_threshold_path_and_ties():
+    """256 experts, top-8: 16 logits per lane, where the top-k inserts only the logits at or
+    above the smallest lane maximum. Constructed rows: all tied, ties in pairs, many ties, the
+    whole top 8 in one lane's share (experts 16 i), -0.0 beside +0.0, -inf everywhere but a few
+    experts, and the reference's own logits."""
+    from nexttransformer_amd import ops
+    gen = torch.Generator().manual_seed(21)
+    T, E, k = 512, 256, 8
+    x = torch.randn(T, 256, generator=gen).to(torch.bfloat16)
+    w = torch.randn(E, 256, generator=gen) * 0.05
+    logits = orc.router_logits_reference(x, w)
+    logits[:64] = 0.0
+    logits[64:128, ::2] = 1.0
+    logits[128:192] = torch.randint(0, 3, (64, E), generator=gen).float()
+    logits[192:256] = -1.0
+    logits[192:256, 0:256:16] = 10.0 + torch.arange(16).float()  # one lane's share
+    logits[256:320] = 0.0
+    logits[256:320, 1::2] = float("-0.0")
+    logits[320:384] = float("-inf")
+    logits[320:384, 7] = 1.0
+    logits[320:384, 200] = 2.0
+    for score_fn in (0, 1):
+        ids, wts, _, _ = ops.topk_from_logits(logits.cuda(), k, score_fn)
+        ref_ids, ref_w = orc.topk(logits, k, score_fn)
+        assert torch.equal(ids.cpu(), ref_ids)
+        torch.testing.assert_close(wts.cpu(), ref_w, rtol=2e-6, atol=2e-7)
+    assert ids[:64].cpu().tolist() == [list(range(8))] * 64
+    assert ids[192:256].cpu().tolist() == [[16 * i for i in range(15, 7, -1)]] * 64
+
+
 @pytest.mark.parametrize("case", SMALL, ids=lambda c: c.name)
 def test_route_plan_bit_exact(case):
     from nexttransformer_amd import ops
