@@ -191,19 +191,21 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
       aoff[i] = (uint32_t)(r * ld_a * 2) + cchunk[i & 1];
     }
   };
-  auto issue = [&](int kt, int slot) {
+  // Copy c (of 2 kCopies) of stage kt: the weight rows first, then the token rows.
+  auto copy = [&](int kt, int slot, int c) __attribute__((always_inline)) {
     unsigned char* sa = smem + slot * kStageBytes + wave * 64 * kRowBytes;
     unsigned char* sb = sa + kOperBytes;
-    const char* abase = reinterpret_cast<const char*>(A) + kt * kRowBytes;
-    const char* bbase = wseg + kt * kRowBytes;
+    if (c < kCopies)
+      __builtin_amdgcn_global_load_lds((gvoid*)(wseg + kt * kRowBytes + boff[c]),
+                                       (lvoid*)(sb + c * 1024), 16, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds(
+          (gvoid*)(reinterpret_cast<const char*>(A) + kt * kRowBytes + aoff[c - kCopies]),
+          (lvoid*)(sa + (c - kCopies) * 1024), 16, 0, 0);
+  };
+  auto issue = [&](int kt, int slot) {
 #pragma unroll
-    for (int i = 0; i < kCopies; ++i)
-      __builtin_amdgcn_global_load_lds((gvoid*)(bbase + boff[i]), (lvoid*)(sb + i * 1024), 16, 0,
-                                       0);
-#pragma unroll
-    for (int i = 0; i < kCopies; ++i)
-      __builtin_amdgcn_global_load_lds((gvoid*)(abase + aoff[i]), (lvoid*)(sa + i * 1024), 16, 0,
-                                       0);
+    for (int c = 0; c < 2 * kCopies; ++c) copy(kt, slot, c);
   };
 
   // ---- fragments -----------------------------------------------------------------------
@@ -285,18 +287,38 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
           for (int j = 0; j < NJ; ++j)
             acc[b][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[b], tf[j], acc[b][j], 0, 0, 0);
       };
-      // One K step from slot g & 1; the copies of the next stage were issued just before.
-      auto body = [&](bool read_next) {
+      // The same, with copies c0, c0 + 1, ... of the next stage spread between the MFMAs (one
+      // after every 4 / per products; issued together ahead of them they held back the first).
+      auto mfmas_copies = [&](const bf16x8 (&wf)[4], const bf16x8 (&tf)[4], int kt_next,
+                              int slot_next, int c0) __attribute__((always_inline)) {
+        constexpr int kPer = 2 * kCopies / 2;  // copies per slice (two slices carry them)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if (j < NJ)
+              acc[b][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[b], tf[j], acc[b][j], 0, 0, 0);
+            const int n = b * 4 + j;
+            if (kt_next >= 0 && n % (16 / kPer) == 16 / kPer - 1) {
+              __builtin_amdgcn_sched_barrier(0);
+              copy(kt_next, slot_next, c0 + n / (16 / kPer));
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+      };
+      // One K step from slot g & 1; the copies of the next stage (kt_next, or none with -1) go
+      // out during its first two slices.
+      auto body = [&](bool read_next, int kt_next) {
         const int slot = g & 1;
         __builtin_amdgcn_sched_barrier(0);
         read_frags(slot, 1, wf1, tf1);
         __builtin_amdgcn_sched_barrier(0);
-        mfmas(wf0, tf0);
+        mfmas_copies(wf0, tf0, kt_next, slot ^ 1, 0);
         __builtin_amdgcn_sched_barrier(0);
         frag_wait(wf1, tf1);
         read_frags(slot, 2, wf0, tf0);
         __builtin_amdgcn_sched_barrier(0);
-        mfmas(wf1, tf1);
+        mfmas_copies(wf1, tf1, kt_next, slot ^ 1, kCopies);
         __builtin_amdgcn_sched_barrier(0);
         frag_wait(wf0, tf0);
         read_frags(slot, 3, wf1, tf1);
@@ -313,16 +335,12 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
         __builtin_amdgcn_sched_barrier(0);
         if (read_next) frag_wait(wf0, tf0);
       };
-      for (int kt = 0; kt + 1 < nk; ++kt) {
-        issue(kt + 1, (g & 1) ^ 1);
-        body(true);
-      }
+      for (int kt = 0; kt + 1 < nk; ++kt) body(true, kt + 1);
       if (has_next) {  // the last step copies the next tile's first stage
         set_a(nt_tile);
         set_b(nt_tile);
-        issue(0, (g & 1) ^ 1);
       }
-      body(has_next);
+      body(has_next, has_next ? 0 : -1);
 
       // Epilogue: lane (token j, half h) holds logical block rows 8 h + [0, 8) in elements 0-7
       // and 16 + 8 h + [0, 8) in 8-15: for SwiGLU gate and value of output columns
