@@ -5,14 +5,16 @@
 //   c[r, j] = epilogue(a_src(r) . w_s[j, :])   for every row r of segment s,
 // with plain weights w [S, R, K] (R = 2 n_out for SwiGLU: gate rows, then value rows).
 //
-// Shape: one persistent 4-wave workgroup per CU. A tile is 256 token rows x 256 weight rows;
+// Shape: one persistent 8-wave workgroup per CU. A tile is 256 token rows x 256 weight rows;
 // per 64-wide K step both operands (32 KB each) are copied from global memory straight into LDS
 // (gfx950 global_load_lds_dwordx4), so every weight byte fetched by the CU feeds 256 token rows
-// and every token byte 256 weight rows: 64 KB of global reads per 8.4 MFLOP. Each wave owns a
-// 128 x 128 quarter of the tile (16 32x32 accumulators, 256 accumulator registers), so each
-// 1 KB fragment read from LDS feeds four MFMAs. Two LDS stages (128 KB): the next K step's
-// copies are issued at the start of a step and waited for at its end, where one workgroup
-// barrier per step also frees the slot just read.
+// and every token byte 256 weight rows: 64 KB of global reads per 8.4 MFLOP. Each wave owns 128
+// tokens x 64 weight rows of the tile (8 32x32 accumulators), two waves per SIMD. Two LDS stages
+// (128 KB); one workgroup barrier per K step, after the wait for the next stage's copies, frees
+// the slot just read. A stage's copies go out in two halves spread between MFMAs (issued
+// together ahead of them they held back the first products): its token rows right after the
+// barrier two steps before it, its weight rows during the step before it. With four waves of
+// 128 x 128 (one per SIMD) the kernel measured 96-107 vs 86-93 us at config 2's down projection.
 //
 // LDS rows are 128 bytes (64 bf16 of K) with the 16-byte chunks of row r XOR-swizzled by
 // (r / 2) % 8, which keeps the 16-lane fragment reads free of bank conflicts; each copy
@@ -48,8 +50,6 @@ constexpr int kRowBytes = kTK * 2;             // 128
 constexpr int kOperBytes = kTM * kRowBytes;    // 32 KB per operand per stage
 constexpr int kStageBytes = 2 * kOperBytes;    // 64 KB
 constexpr int kStages = 2;
-constexpr int kThreads = 256;
-constexpr int kCopies = kOperBytes / (kThreads * 16);  // copy instructions per operand per lane (8)
 constexpr int kBlocksPerTile = kTN / 32;                // weight blocks of 32 rows per tile (8)
 static_assert(kTM == kTN, "one copy pattern serves both operands");
 
@@ -81,7 +81,7 @@ __device__ __forceinline__ int weight_row(int nt, int p_tile, int n_out, int R) 
 // (SwiGLU: gate columns then value columns; ReLU^2: the output's columns), rounded from the same
 // fp32 accumulators, for the backward.
 template <int EPI, bool GATHER, bool KEEP = false>
-__global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
+__global__ __launch_bounds__(512, 1) void grouped_gemm_t256_kernel(
     const uint16_t* __restrict__ A, int64_t ld_a, int64_t a_rows,
     const int32_t* __restrict__ src_row, const int32_t* __restrict__ seg_offsets, int S,
     int total_rows, const uint16_t* __restrict__ W, int K, int n_out,
@@ -90,6 +90,10 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
   int* tile_prefix = reinterpret_cast<int*>(smem + kStages * kStageBytes);  // [S+1]
   int* seg_lo = tile_prefix + (S + 1);                                      // [S+1]
 
+  constexpr int NW = 8;                                 // waves
+  constexpr int kCopies = kOperBytes / (64 * NW * 16);  // copy instructions per operand per lane
+  constexpr int kCRows = 8 * kCopies;                   // LDS rows each wave copies per operand
+  constexpr int kWB = 16 / NW;                          // weight blocks per wave
   const int lane = lane_id(), wave = wave_id();
   const int R = EPI == NT_MOE_EPI_SWIGLU ? 2 * n_out : n_out;  // weight rows per segment
   // weight blocks: SwiGLU blocks pair 16 gate with 16 value rows (n_out % 16 == 0); other
@@ -155,9 +159,9 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
   };
 
   // ---- copies --------------------------------------------------------------------------
-  // Copy instruction i of this wave covers LDS rows 64 wave + 8 i + [0, 8) of each operand;
-  // lane l writes row 64 wave + 8 i + l / 8, physical chunk l % 8, i.e. logical chunk
-  // (l % 8) ^ ((row / 2) % 8).
+  // Copy instruction i of this wave covers LDS rows kCRows wave + 8 i + [0, 8) of each operand;
+  // lane l writes row kCRows wave + 8 i + l / 8, physical chunk l % 8, i.e. logical chunk
+  // (l % 8) ^ ((row / 2) % 8) (kCRows is a multiple of 16, so the row parity is that of 8 i).
   const int crow = lane >> 3;
   const uint32_t cchunk[2] = {(uint32_t)(((lane & 7) ^ ((crow >> 1) & 7)) << 4),
                               (uint32_t)(((lane & 7) ^ (((8 + crow) >> 1) & 7)) << 4)};
@@ -170,7 +174,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
     wseg = reinterpret_cast<const char*>(W) + (int64_t)t.s * R * (int64_t)K * 2;
 #pragma unroll
     for (int i = 0; i < kCopies; ++i) {
-      const int p = 64 * wave + 8 * i + crow;
+      const int p = kCRows * wave + 8 * i + crow;
       boff[i] = (uint32_t)weight_row<EPI>(t.nt, p, n_out, R) * (uint32_t)K * 2u + cchunk[i & 1];
     }
   };
@@ -178,7 +182,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
   auto load_idx = [&](const Tile& t) {
 #pragma unroll
     for (int i = 0; i < kCopies; ++i) {
-      const int r = t.m0 + 64 * wave + 8 * i + crow;
+      const int r = t.m0 + kCRows * wave + 8 * i + crow;
       const int rr = r < t.seg_end ? r : t.seg_end - 1;
       nidx[i] = GATHER ? src_row[rr] : rr;
     }
@@ -193,7 +197,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
   };
   // Copy c (of 2 kCopies) of stage kt: the weight rows first, then the token rows.
   auto copy = [&](int kt, int slot, int c) __attribute__((always_inline)) {
-    unsigned char* sa = smem + slot * kStageBytes + wave * 64 * kRowBytes;
+    unsigned char* sa = smem + slot * kStageBytes + wave * kCRows * kRowBytes;
     unsigned char* sb = sa + kOperBytes;
     if (c < kCopies)
       __builtin_amdgcn_global_load_lds((gvoid*)(wseg + kt * kRowBytes + boff[c]),
@@ -209,7 +213,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
   };
 
   // ---- fragments -----------------------------------------------------------------------
-  const int wm = wave >> 1, wn = wave & 1;  // token half, weight half of the tile
+  const int wm = wave / (NW / 2), wn = wave % (NW / 2);  // token half, weight part of the tile
   int frag_off[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q)
@@ -220,28 +224,27 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
   const __amdgpu_buffer_rsrc_t pre_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       KEEP ? Pre : Cout, 0, KEEP ? (int)((int64_t)total_rows * R * 2) : 0, kBufferWord3);
 
-  // Fragment reads of slice q of stage `slot`: the wave's 4 weight blocks and 4 token blocks
+  // Fragment reads of slice q of stage `slot`: the wave's kWB weight blocks and 4 token blocks
   // (all 4 even in a partial tile: reading rows nobody copied is harmless, their products are
   // dropped). Issued as inline assembly so they stay where they are written (ahead of the MFMAs
   // of the previous slice) and land in registers of their own; frag_wait() then waits for them
   // with a count that names those registers.
-  auto read_frags = [&](int slot, int q, bf16x8 (&wf)[4], bf16x8 (&tf)[4]) {
+  auto read_frags = [&](int slot, int q, bf16x8 (&wf)[kWB], bf16x8 (&tf)[4]) {
     const uint32_t a_addr = (uint32_t)(uintptr_t)(smem + slot * kStageBytes) +
                             wm * 128 * kRowBytes + frag_off[q];
-    const uint32_t b_addr = a_addr - wm * 128 * kRowBytes + kOperBytes + wn * 128 * kRowBytes;
+    const uint32_t b_addr =
+        a_addr - wm * 128 * kRowBytes + kOperBytes + wn * (32 * kWB) * kRowBytes;
+    static_assert(kWB == 2, "two weight blocks per wave");
     asm volatile("ds_read_b128 %0, %1" : "=v"(wf[0]) : "v"(b_addr));
     asm volatile("ds_read_b128 %0, %1 offset:4096" : "=v"(wf[1]) : "v"(b_addr));
-    asm volatile("ds_read_b128 %0, %1 offset:8192" : "=v"(wf[2]) : "v"(b_addr));
-    asm volatile("ds_read_b128 %0, %1 offset:12288" : "=v"(wf[3]) : "v"(b_addr));
     asm volatile("ds_read_b128 %0, %1" : "=v"(tf[0]) : "v"(a_addr));
     asm volatile("ds_read_b128 %0, %1 offset:4096" : "=v"(tf[1]) : "v"(a_addr));
     asm volatile("ds_read_b128 %0, %1 offset:8192" : "=v"(tf[2]) : "v"(a_addr));
     asm volatile("ds_read_b128 %0, %1 offset:12288" : "=v"(tf[3]) : "v"(a_addr));
   };
-  auto frag_wait = [](bf16x8 (&wf)[4], bf16x8 (&tf)[4]) {
+  auto frag_wait = [](bf16x8 (&wf)[kWB], bf16x8 (&tf)[4]) {
     asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(wf[0]), "+v"(wf[1]), "+v"(wf[2]), "+v"(wf[3]), "+v"(tf[0]), "+v"(tf[1]),
-                   "+v"(tf[2]), "+v"(tf[3])
+                 : "+v"(wf[0]), "+v"(wf[1]), "+v"(tf[0]), "+v"(tf[1]), "+v"(tf[2]), "+v"(tf[3])
                  :
                  : "memory");
   };
@@ -253,6 +256,8 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
   set_a(ct);
   set_b(ct);
   issue(0, 0);
+#pragma unroll
+  for (int c = kCopies; c < 2 * kCopies; ++c) copy(1, 1, c);  // stage 1's token rows
   Tile nt_tile = ct;
   bool has_next = n_my > 1;
   if (has_next) locate(1, nt_tile);
@@ -263,7 +268,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
   // after it, overlapping the next step's first fragment reads (slice 3's fragments are read
   // before the barrier, so the slot may be refilled meanwhile). fr0 holds slices 0 and 2, fr1
   // slices 1 and 3. The next stage's copies go out at the start of the step.
-  bf16x8 wf0[4], tf0[4], wf1[4], tf1[4];
+  bf16x8 wf0[kWB], tf0[4], wf1[kWB], tf1[4];
   read_frags(0, 0, wf0, tf0);
   frag_wait(wf0, tf0);
   int g = 0;
@@ -275,50 +280,57 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
     // accumulators are local to each variant).
     auto tile_pass = [&](auto nj_c) {
       constexpr int NJ = decltype(nj_c)::value;
-      floatx16 acc[4][NJ > 0 ? NJ : 1];
+      floatx16 acc[kWB][NJ > 0 ? NJ : 1];
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
+      for (int b = 0; b < kWB; ++b)
 #pragma unroll
         for (int j = 0; j < NJ; ++j) acc[b][j] = floatx16{};
-      auto mfmas = [&](const bf16x8 (&wf)[4], const bf16x8 (&tf)[4]) {
+      auto mfmas = [&](const bf16x8 (&wf)[kWB], const bf16x8 (&tf)[4]) {
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int b = 0; b < kWB; ++b)
 #pragma unroll
           for (int j = 0; j < NJ; ++j)
             acc[b][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[b], tf[j], acc[b][j], 0, 0, 0);
       };
-      // The same, with copies c0, c0 + 1, ... of the next stage spread between the MFMAs (one
-      // after every 4 / per products; issued together ahead of them they held back the first).
-      auto mfmas_copies = [&](const bf16x8 (&wf)[4], const bf16x8 (&tf)[4], int kt_next,
+      // The same, with copies c0, c0 + 1, ... of the next stage spread evenly between the MFMAs
+      // (issued together ahead of them they held back the first products).
+      auto mfmas_copies = [&](const bf16x8 (&wf)[kWB], const bf16x8 (&tf)[4], int kt_next,
                               int slot_next, int c0) __attribute__((always_inline)) {
-        constexpr int kPer = 2 * kCopies / 2;  // copies per slice (two slices carry them)
+        constexpr int kPer = kCopies;         // copies per slice (two slices carry them)
+        constexpr int kGap = 4 * kWB / kPer;  // MFMA positions per copy
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int b = 0; b < kWB; ++b)
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             if (j < NJ)
               acc[b][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[b], tf[j], acc[b][j], 0, 0, 0);
             const int n = b * 4 + j;
-            if (kt_next >= 0 && n % (16 / kPer) == 16 / kPer - 1) {
+            if (kt_next >= 0 && n % kGap == kGap - 1) {
               __builtin_amdgcn_sched_barrier(0);
-              copy(kt_next, slot_next, c0 + n / (16 / kPer));
+              copy(kt_next, slot_next, c0 + n / kGap);
               __builtin_amdgcn_sched_barrier(0);
             }
           }
       };
-      // One K step from slot g & 1; the copies of the next stage (kt_next, or none with -1) go
-      // out during its first two slices.
-      auto body = [&](bool read_next, int kt_next) {
+      // K step kt from slot g & 1. Stage s's copies go out in two halves, each spread over one
+      // slice: its token rows (gathered: the longer latency) during slice 3 of step s - 2, right
+      // after the barrier that frees the slot, its weight rows during slice 0 of step s - 1; the
+      // wait before step s - 1's barrier completes both. Past the tile's last stages the halves
+      // are the next tile's stages 0 and 1, whose row offsets are set after step nk - 2's
+      // barrier (every copy of this tile has gone out by then).
+      auto body = [&](int kt, bool read_next, auto set_c) {
+        constexpr bool kSet = decltype(set_c)::value;  // step nk - 2: take the next tile's rows
         const int slot = g & 1;
+        const int kt_w = kt + 1 < nk ? kt + 1 : (has_next ? kt + 1 - nk : -1);
         __builtin_amdgcn_sched_barrier(0);
         read_frags(slot, 1, wf1, tf1);
         __builtin_amdgcn_sched_barrier(0);
-        mfmas_copies(wf0, tf0, kt_next, slot ^ 1, 0);
+        mfmas_copies(wf0, tf0, kt_w, slot ^ 1, 0);  // stage kt + 1: weight rows
         __builtin_amdgcn_sched_barrier(0);
         frag_wait(wf1, tf1);
         read_frags(slot, 2, wf0, tf0);
         __builtin_amdgcn_sched_barrier(0);
-        mfmas_copies(wf1, tf1, kt_next, slot ^ 1, kCopies);
+        mfmas(wf1, tf1);
         __builtin_amdgcn_sched_barrier(0);
         frag_wait(wf0, tf0);
         read_frags(slot, 3, wf1, tf1);
@@ -329,18 +341,22 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         barrier_nofence();
         ++g;
+        if constexpr (kSet) {
+          if (has_next) {  // the next tile's rows (its indices landed above)
+            set_a(nt_tile);
+            set_b(nt_tile);
+          }
+        }
+        const int kt_t = kt + 2 < nk ? kt + 2 : (has_next ? kt + 2 - nk : -1);
         if (read_next) read_frags(g & 1, 0, wf0, tf0);
         __builtin_amdgcn_sched_barrier(0);
-        mfmas(wf1, tf1);
+        mfmas_copies(wf1, tf1, kt_t, slot, kCopies);  // stage kt + 2: token rows
         __builtin_amdgcn_sched_barrier(0);
         if (read_next) frag_wait(wf0, tf0);
       };
-      for (int kt = 0; kt + 1 < nk; ++kt) body(true, kt + 1);
-      if (has_next) {  // the last step copies the next tile's first stage
-        set_a(nt_tile);
-        set_b(nt_tile);
-      }
-      body(has_next, has_next ? 0 : -1);
+      for (int kt = 0; kt + 2 < nk; ++kt) body(kt, true, std::false_type());
+      body(nk - 2, true, std::true_type());
+      body(nk - 1, has_next, std::false_type());
 
       // Epilogue: lane (token j, half h) holds logical block rows 8 h + [0, 8) in elements 0-7
       // and 16 + 8 h + [0, 8) in 8-15: for SwiGLU gate and value of output columns
@@ -348,8 +364,8 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_t256_kernel(
       // Rows past the segment and columns past n_out are dropped by the buffer range check.
       const int hbit = lane >> 5;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int nb = ct.nt * kBlocksPerTile + wn * 4 + b;
+      for (int b = 0; b < kWB; ++b) {
+        const int nb = ct.nt * kBlocksPerTile + wn * kWB + b;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
           const int m = ct.m0 + wm * 128 + j * 32 + (lane & 31);
@@ -427,7 +443,7 @@ hipError_t launch_t256(const uint16_t* a, int64_t ld_a, int64_t a_rows, const in
   auto kern = grouped_gemm_t256_kernel<EPI, GATHER, KEEP>;
   hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), lds, stream, a, ld_a, a_rows,
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(512), lds, stream, a, ld_a, a_rows,
                      src_row, seg_offsets, S, (int)total_rows, w, K, n_out, c, pre);
   return hipGetLastError();
 }
