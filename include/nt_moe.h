@@ -272,6 +272,22 @@ int nt_moe_convert_expert_weights_packed(const float* w, int64_t num_matrices, i
                                          nt_moe_stream_t stream);
 
 /*
+ * The router's operands from its fp32 weight W [num_experts, d] (row stride ld_w), rebuilt after
+ * every weight update in one pass (MasterLinear's per-product cast of the gate weight,
+ * megatron_moe.py:58-78,99): w_router_t = W^T fp32 [dp, num_experts] (dp >= d; rows d .. dp - 1
+ * zero), the layout nt_moe_router_fwd reads, and, when `first` is not NULL, the backward's
+ * concatenated operand first bf16 [dp, Kc]: columns [0, Fs) = S^T for the shared expert's W1
+ * S bf16 [Fs, dp] (row stride ld_s; Fs may be 0), hi = bf16(W^T) at [Fs, Fs + E),
+ * lo = bf16(W^T - hi) at [Fs + Ep, Fs + Ep + E), hi at [Fs + 2 Ep, Fs + 2 Ep + E), every other
+ * column zero (Ep >= E, Kc >= Fs + 3 Ep); rounding to nearest even. No counterpart in the
+ * reference beyond the cast and the autograd of F.linear it prepares.
+ */
+int nt_moe_router_operands(const float* w, int64_t ld_w, int32_t num_experts, int32_t d,
+                           int32_t dp, const uint16_t* shared_w1, int64_t ld_s, int32_t Fs,
+                           float* w_router_t, uint16_t* first, int32_t Ep, int32_t Kc,
+                           nt_moe_stream_t stream);
+
+/*
  * Packed-weight variant of the grouped GEMM. nt_moe_pack_expert_weights_bf16 rearranges
  * w [num_segments, rows, K] once (same bytes, fragment order: 32-row x 64-K blocks in which
  * each lane's 16-byte operand chunk is contiguous with its neighbours', rows inside a block

@@ -681,6 +681,28 @@ int nt_moe_convert_expert_weights_packed(const float* w, int64_t num_matrices, i
                   "convert_expert_weights_packed");
 }
 
+int nt_moe_router_operands(const float* w, int64_t ld_w, int32_t num_experts, int32_t d,
+                           int32_t dp, const uint16_t* shared_w1, int64_t ld_s, int32_t Fs,
+                           float* w_router_t, uint16_t* first, int32_t Ep, int32_t Kc,
+                           nt_moe_stream_t stream) {
+  NT_REQUIRE(num_experts > 0 && d > 0 && dp >= d && ld_w >= d,
+             "router_operands: need num_experts > 0, 0 < d <= dp and ld_w >= d, got E=%d d=%d "
+             "dp=%d ld_w=%lld", num_experts, d, dp, (long long)ld_w);
+  NT_REQUIRE(w && w_router_t, "router_operands: null weight or w_router_t");
+  if (first) {
+    NT_REQUIRE(Ep >= num_experts && Fs >= 0 && (int64_t)Kc >= (int64_t)Fs + 3 * (int64_t)Ep &&
+                   (int64_t)dp * Kc < (int64_t)1 << 31,
+               "router_operands: need Ep >= E, Fs >= 0 and Fs + 3 Ep <= Kc, got E=%d Ep=%d "
+               "Fs=%d Kc=%d", num_experts, Ep, Fs, Kc);
+    NT_REQUIRE(Fs == 0 || (shared_w1 && ld_s >= dp),
+               "router_operands: Fs > 0 needs shared_w1 with row stride >= dp");
+  }
+  return launched(launch_router_operands(w, ld_w, num_experts, d, dp, shared_w1, ld_s,
+                                         first ? Fs : 0, w_router_t, first, first ? Ep : num_experts,
+                                         first ? Kc : 0, reinterpret_cast<hipStream_t>(stream)),
+                  "router_operands");
+}
+
 int nt_moe_pack_expert_weights_bf16(const uint16_t* w, int64_t num_segments, int32_t rows,
                                     int32_t K, int32_t epilogue, uint16_t* packed,
                                     nt_moe_stream_t stream) {

@@ -160,6 +160,9 @@ hipError_t launch_grouped_gemm_bf16_pp(const uint16_t* a, int64_t ld_a, int64_t 
 hipError_t launch_convert_weights(const float* w, int64_t S, int R, int K, uint16_t* out,
                                   uint16_t* out_t, hipStream_t stream, uint16_t* pk = nullptr,
                                   int pk_swiglu_n = 0, uint16_t* pk_t = nullptr);
+hipError_t launch_router_operands(const float* w, int64_t ldw, int E, int d, int dp,
+                                  const uint16_t* sw, int64_t lds, int Fs, float* router_t,
+                                  uint16_t* first, int Ep, int Kc, hipStream_t stream);
 hipError_t launch_grouped_gemm_bf16_t256(const uint16_t* a, int64_t ld_a, int64_t a_rows,
                                          const int32_t* src_row, const int32_t* seg_offsets,
                                          int num_segments, int64_t total_rows, const uint16_t* w,

@@ -98,6 +98,63 @@ __global__ __launch_bounds__(256) void convert_weights_kernel(const float* __res
   }
 }
 
+// The router's operands from its fp32 weight W [E, d] (row stride ldw), one 64 x 64 tile per
+// workgroup through LDS: router_t = W^T fp32 [dp, E] (rows d .. dp - 1 zero) and, when `first`
+// is given, the backward's concatenated operand first bf16 [dp, Kc]: columns [0, Fs) = S^T for
+// the shared expert's W1 S bf16 [Fs, dp] (row stride lds), hi = bf16(W^T) at [Fs, Fs + E),
+// lo = bf16(W^T - hi) at [Fs + Ep, Fs + Ep + E) (the difference is exact in fp32), hi again at
+// [Fs + 2 Ep, Fs + 2 Ep + E), every other column zero. blockIdx.y < ceil(Ep / 64) picks a tile
+// of router columns (those past E read zeros), the rest tiles of S's rows.
+__global__ __launch_bounds__(256) void router_operands_kernel(
+    const float* __restrict__ w, int64_t ldw, int E, int d, int dp,
+    const uint16_t* __restrict__ sw, int64_t lds, int Fs, float* __restrict__ router_t,
+    uint16_t* __restrict__ first, int Ep, int Kc) {
+  __shared__ float tile[kCT][kCT + 1];  // [source row][j - j0]
+  const int tiles_r = (Ep + kCT - 1) / kCT;
+  const bool router = (int)blockIdx.y < tiles_r;
+  const int j0 = (int)blockIdx.x * kCT;
+  const int c0 = ((int)blockIdx.y - (router ? 0 : tiles_r)) * kCT;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll 4
+  for (int i = 0; i < kCT / 4; ++i) {  // coalesced along j
+    const int c = c0 + ty + 4 * i, j = j0 + tx;
+    float v = 0.f;
+    if (router) {
+      if (c < E && j < d) v = w[(int64_t)c * ldw + j];
+    } else if (c < Fs && j < dp) {
+      v = bf16_bits_to_f32(sw[(int64_t)c * lds + j]);
+    }
+    tile[ty + 4 * i][tx] = v;
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int i = 0; i < kCT / 4; ++i) {  // coalesced along the output column c
+    const int j = j0 + ty + 4 * i, c = c0 + tx;
+    if (j >= dp) continue;
+    const float v = tile[tx][ty + 4 * i];
+    if (router) {
+      if (c < E) router_t[(int64_t)j * E + c] = v;
+      if (first && c < Ep) {
+        const uint16_t hi = f32_to_bf16_bits(v);
+        const uint16_t lo = f32_to_bf16_bits(v - bf16_bits_to_f32(hi));
+        uint16_t* row = first + (int64_t)j * Kc + Fs;
+        row[c] = hi;
+        row[Ep + c] = lo;
+        row[2 * Ep + c] = hi;
+      }
+    } else if (c < Fs) {
+      first[(int64_t)j * Kc + c] = f32_to_bf16_bits(v);
+    }
+  }
+  if (first && blockIdx.y == 0) {  // columns [Fs + 3 Ep, Kc): zeros
+    const int z0 = Fs + 3 * Ep, nz = Kc - z0;
+    for (int p = (int)threadIdx.x; p < kCT * nz; p += 256) {
+      const int j = j0 + p / nz;
+      if (j < dp) first[(int64_t)j * Kc + z0 + p % nz] = 0;
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_convert_weights(const float* w, int64_t S, int R, int K, uint16_t* out,
@@ -107,6 +164,16 @@ hipError_t launch_convert_weights(const float* w, int64_t S, int R, int K, uint1
   if (blocks == 0 || (!out && !out_t && !pk && !pk_t)) return hipSuccess;
   hipLaunchKernelGGL(convert_weights_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, w, S,
                      R, K, out, out_t, pk, pk_swiglu_n, pk_t);
+  return hipGetLastError();
+}
+
+hipError_t launch_router_operands(const float* w, int64_t ldw, int E, int d, int dp,
+                                  const uint16_t* sw, int64_t lds, int Fs, float* router_t,
+                                  uint16_t* first, int Ep, int Kc, hipStream_t stream) {
+  const int ty = (Ep + kCT - 1) / kCT + (first ? (Fs + kCT - 1) / kCT : 0);
+  hipLaunchKernelGGL(router_operands_kernel, dim3((unsigned)((dp + kCT - 1) / kCT), (unsigned)ty),
+                     dim3(256), 0, stream, w, ldw, E, d, dp, sw, lds, first ? Fs : 0, router_t,
+                     first, Ep, Kc);
   return hipGetLastError();
 }
 

@@ -397,7 +397,8 @@ class MoELayer(nn.Module):
                                             shared_w2_t=w["shared_w2_t"],
                                             w1_t_packed=w["w1_t_packed"],
                                             w2_t_packed=w["w2_t_packed"],
-                                            shared_w2_t_packed=w["shared_w2_t_packed"])
+                                            shared_w2_t_packed=w["shared_w2_t_packed"],
+                                            first=w.get("first"))
         return w["_bw"]
 
     def _unpadded_grads(self, g):
@@ -528,10 +529,7 @@ class MoELayer(nn.Module):
                         ops.pack_expert_weights_fp8(w2q, nat.EPI_NONE), w2s)
 
             plain = []  # the bf16 [E, rows, cols] stacks before packing (for the backward)
-            router_t = torch.zeros(dp, r.routed_experts, device=self.router.weight.device,
-                                   dtype=torch.float32)
-            router_t[:r.width] = self.router.weight.detach().t()
-            packed = dict(router_t=router_t, shared_w1=None, shared_w2=None,
+            packed = dict(shared_w1=None, shared_w2=None,
                           shared_w1_scale=None, shared_w2_scale=None,
                           packed=True if fp8 else (pk_up, pk_down))
             (packed["w1"], packed["w1_scale"], packed["w2"],
@@ -546,6 +544,24 @@ class MoELayer(nn.Module):
                  packed["w1_t_packed"], packed["w2_t_packed"]) = plain[0]
                 (packed["shared_w1_plain"], packed["shared_w2_plain"], _, packed["shared_w2_t"],
                  _, packed["shared_w2_t_packed"]) = plain[1] if len(plain) > 1 else (None,) * 6
+            # the router's operands after the expert conversions, whose GPU time then covers
+            # this host work: w_router_t and, for the backward, the first operand in one kernel
+            rw = self.router.weight.detach()
+            packed["first"] = None
+            if on_gpu:
+                want_first = keep_plain and not fp8
+                sw1 = packed.get("shared_w1_plain") if want_first else None
+                if rw.dtype != torch.float32 or rw.stride(1) != 1:
+                    rw = rw.float().contiguous()
+                packed["router_t"], first = ops.router_operands.raw(
+                    rw, dp, None if sw1 is None else sw1[0], want_first)
+                if want_first:
+                    packed["first"] = first
+            else:
+                router_t = torch.zeros(dp, r.routed_experts, device=rw.device,
+                                       dtype=torch.float32)
+                router_t[:r.width] = rw.t()
+                packed["router_t"] = router_t
             self._packed = packed
             self._pack_key = key
         return self._packed

@@ -386,6 +386,52 @@ def _(w, want_out, want_t):
             w.new_empty((S, K, R) if want_t else (0,), dtype=torch.bfloat16))
 
 
+def first_layout(E, Fs):
+    """(Ep, Kc) of the backward's concatenated first operand [S^T | hi | lo | hi] for E experts
+    and a shared expert of Fs fc1 rows (0 without one): E padded to 32, the width to 64."""
+    Ep = _round_up(E, 32)
+    return Ep, _round_up(Fs + 3 * Ep, 64)
+
+
+@_custom_op("ntmoe::router_operands")
+def router_operands(w: Tensor, dp: int, shared_w1: Optional[Tensor], want_first: bool
+                    ) -> tuple[Tensor, Tensor]:
+    """From the fp32 router weight w [E, d]: (w_router_t fp32 [dp, E], rows past d zero; and,
+    with want_first, the backward's first operand bf16 [1, dp, Kc] = [S^T | hi | lo | hi | 0]
+    for the shared expert's W1 S bf16 [Fs, dp] (or none), hi / lo the two-term bf16 split of
+    w_router_t, (Ep, Kc) = first_layout(E, Fs); else an empty tensor), in one kernel."""
+    _on_gpu(w, shared_w1)
+    _require(w.dtype == torch.float32 and w.dim() == 2 and w.stride(1) == 1,
+             "router_operands: w must be fp32 [E, d] with contiguous rows")
+    E, d = w.shape
+    _require(dp >= d, "router_operands: dp must be >= d")
+    Fs = 0
+    if want_first and shared_w1 is not None:
+        _require(shared_w1.dtype == torch.bfloat16 and shared_w1.dim() == 2
+                 and shared_w1.shape[1] == dp and shared_w1.stride(1) == 1,
+                 "router_operands: shared_w1 must be bf16 [Fs, dp] with contiguous rows")
+        Fs = shared_w1.shape[0]
+    Ep, Kc = first_layout(E, Fs)
+    rt = torch.empty(dp, E, device=w.device, dtype=torch.float32)
+    first = torch.empty((1, dp, Kc) if want_first else (0,), device=w.device,
+                        dtype=torch.bfloat16)
+    st = nat.load().nt_moe_router_operands(
+        ptr(w), w.stride(0), E, d, dp, ptr(shared_w1) if Fs else None,
+        shared_w1.stride(0) if Fs else 0, Fs, ptr(rt), ptr(first) if want_first else None,
+        Ep, Kc, _stream(w.device))
+    nat.check(st, "ntmoe::router_operands")
+    return rt, first
+
+
+@router_operands.register_fake
+def _(w, dp, shared_w1, want_first):
+    E = w.shape[0]
+    Fs = shared_w1.shape[0] if (want_first and shared_w1 is not None) else 0
+    Kc = first_layout(E, Fs)[1]
+    return (w.new_empty(dp, E), w.new_empty((1, dp, Kc) if want_first else (0,),
+                                            dtype=torch.bfloat16))
+
+
 @_custom_op("ntmoe::convert_pack_expert_weights")
 def convert_pack_expert_weights(w: Tensor, epilogue: int, want_out: bool, want_t: bool,
                                 want_packed: bool, want_packed_t: bool
@@ -992,7 +1038,7 @@ class BackwardWeights:
 
     def __init__(self, w1, w2, shared_w1=None, shared_w2=None, w_router_t=None, w1_t=None,
                  w2_t=None, shared_w2_t=None, w1_t_packed=None, w2_t_packed=None,
-                 shared_w2_t_packed=None):
+                 shared_w2_t_packed=None, first=None):
         self.w1_plain, self.w2_plain = w1, w2
         self.shared_w1, self.shared_w2 = shared_w1, shared_w2
         self.w_router_t = w_router_t
@@ -1012,6 +1058,9 @@ class BackwardWeights:
         # transposes already packed (convert_pack_expert_weights), used as they are
         self._tp = dict(w1=w1_t_packed, w2=w2_t_packed, shared_w2=shared_w2_t_packed)
         self._cache = {}
+        if first is not None:  # already built with w_router_t (router_operands)
+            Fs = 0 if shared_w1 is None else shared_w1.shape[1]
+            self._cache["first"] = (first, (Fs,) + first_layout(w_router_t.shape[1], Fs))
 
     def _transposed(self, name, w):
         t = self._t.get(name)
@@ -1054,9 +1103,8 @@ class BackwardWeights:
         """[1, d, Kc] bf16 (see the class notes) and the column layout (Fs, Ep, Kc)."""
         def make():
             d, E = w_router_t.shape
-            Ep = _round_up(E, 32)
             Fs = 0 if self.shared_w1 is None else self.shared_w1.shape[1]
-            Kc = _round_up(Fs + 3 * Ep, 64)
+            Ep, Kc = first_layout(E, Fs)
             w = torch.zeros(1, d, Kc, device=w_router_t.device, dtype=torch.bfloat16)
             if Fs:
                 w[0, :, :Fs] = self.shared_w1[0].t()

@@ -483,3 +483,35 @@ def test_backward_first_operand_is_the_split_and_concatenation(E, Fs):
     want[:, Fs + Ep:Fs + Ep + E] = hi
     want[:, Fs + 2 * Ep:Fs + 2 * Ep + E] = lo
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("E,d,dp,Fs", [(32, 1024, 1024, 0), (8, 40, 64, 0),
+                                       (256, 1280, 1280, 640), (40, 96, 128, 192)])
+def test_router_operands_match_the_torch_construction(E, d, dp, Fs):
+    """router_operands' w_router_t and first operand, bit for bit against torch: the zero-padded
+    transpose, and [S^T | hi | lo | hi | 0] from split_bf16 (E not a multiple of 32, d padded to
+    dp, values spanning exponents, exact bf16 values, negative zero, with and without a shared
+    expert); without want_first only w_router_t."""
+    from nexttransformer_amd import ops
+    gen = torch.Generator().manual_seed(E + d + Fs)
+    w = torch.randn(E, d, generator=gen) * torch.exp2(
+        torch.randint(-30, 30, (E, d), generator=gen).float())
+    w[0] = w[0].to(torch.bfloat16).float()
+    w[1, :4] = torch.tensor([0.0, -0.0, 1.0, -3.5])
+    s = (torch.randn(Fs, dp, generator=gen).to(torch.bfloat16) if Fs else None)
+    rt, first = ops.router_operands(w.cuda(), dp, None if s is None else s.cuda(), True)
+    want_rt = torch.zeros(dp, E)
+    want_rt[:d] = w.t()
+    assert torch.equal(rt.cpu().view(torch.int32), want_rt.view(torch.int32))
+    Ep, Kc = ops.first_layout(E, Fs)
+    hi, lo = ops.split_bf16(want_rt)
+    want = torch.zeros(1, dp, Kc, dtype=torch.bfloat16)
+    if Fs:
+        want[0, :, :Fs] = s.t()
+    want[0, :, Fs:Fs + E] = hi
+    want[0, :, Fs + Ep:Fs + Ep + E] = lo
+    want[0, :, Fs + 2 * Ep:Fs + 2 * Ep + E] = hi
+    assert first.shape == (1, dp, Kc)
+    assert torch.equal(first.cpu().view(torch.int16), want.view(torch.int16))
+    rt2, none = ops.router_operands(w.cuda(), dp, None, False)
+    assert none.numel() == 0 and torch.equal(rt2.cpu().view(torch.int32), want_rt.view(torch.int32))
