@@ -5,6 +5,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "nt_moe.h"
 
 namespace ntmoe {
@@ -44,6 +46,15 @@ __device__ __forceinline__ int wave_id() {
 }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// f(integral_constant<int, i>) for i = 0 .. N-1, each index a constant expression.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>());
+    static_for<I + 1, N>(f);
+  }
+}
 
 inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 

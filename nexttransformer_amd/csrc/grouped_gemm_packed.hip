@@ -49,14 +49,6 @@
 namespace ntmoe {
 namespace {
 
-// f(integral_constant<int, i>) for i = 0 .. N-1, each index a constant expression.
-template <int I, int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>());
-    static_for<I + 1, N>(f);
-  }
-}
 
 typedef __attribute__((address_space(1))) void gvoid;
 typedef __attribute__((address_space(3))) void lvoid;
