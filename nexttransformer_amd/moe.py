@@ -73,13 +73,24 @@ def set_aux_loss_scale(scale, *, device="cpu"):
     _aux_loss_scale = torch.tensor(float(scale), dtype=torch.float32, device=device)
 
 
+_injected_cache = {}  # device -> (the scale tensor it was made from, its version, gradient)
+
+
 def _injected_aux_grad(device):
-    """{lb + z, lb, z} gradient [3] on `device` that an "inject" backward adds: (scale, 0, 0)."""
+    """{lb + z, lb, z} gradient [3] on `device` that an "inject" backward adds: (scale, 0, 0).
+    Made once per device while the scale set by set_aux_loss_scale stays the same unmodified
+    tensor (two small kernels less per backward); callers must not modify it."""
+    s = _aux_loss_scale
+    ver = None if s is None else s._version
+    hit = _injected_cache.get(device)
+    if hit is not None and hit[0] is s and hit[1] == ver:
+        return hit[2]
     g = torch.zeros(3, device=device, dtype=torch.float32)
-    if _aux_loss_scale is None:
+    if s is None:
         g[0] = 1.0
     else:
-        g[0] = _aux_loss_scale.to(device, non_blocking=True)
+        g[0] = s.to(device, non_blocking=True)
+    _injected_cache[device] = (s, ver, g)
     return g
 
 
@@ -188,6 +199,8 @@ class _MoETrain(torch.autograd.Function):
             want_logits=True, packed=w["packed"], keep=True)
         cfg["counts"] = state["counts"]
         ctx.cfg, ctx.state, ctx.x, ctx.w = cfg, state, x, w
+        # an output the loss does not use gets None, not a zero-filled gradient
+        ctx.set_materialize_grads(False)
         return out, aux
 
     @staticmethod
@@ -264,12 +277,21 @@ class MoELayer(nn.Module):
         # Optional fixed per-expert logit bias [E] fp32 added after the gating GEMM (not a
         # parameter; None = no bias, the reference router): used to impose a routing skew.
         self.register_buffer("logit_bias", None)
-        self.last_load = None
+        self._last_counts = None
         self.last_aux_loss = None
         self.last_aux_parts = None
         self._pack_key = None
         self._packed = None
         self.reset_parameters()
+
+    @property
+    def last_load(self):
+        """Per-expert token counts of the last forward, int64 [E] (None before the first): the
+        kernels' int32 counts, converted on first access rather than in every forward."""
+        c = self._last_counts
+        if c is not None and c.dtype != torch.int64:
+            c = self._last_counts = c.to(torch.int64)
+        return c
 
     # -- initialisation --------------------------------------------------------------------
 
@@ -598,7 +620,7 @@ class MoELayer(nn.Module):
             shared_w2_scale=w["shared_w2_scale"], packed=w["packed"])
         if dp != r.width:
             out = out[:, :r.width]
-        self.last_load = state["counts"].to(torch.int64)
+        self._last_counts = state["counts"]
         self.last_aux_parts = aux
         self.last_aux_loss = aux[0]
         out = out.reshape(hidden.shape).to(hidden.dtype)
@@ -631,7 +653,7 @@ class MoELayer(nn.Module):
         out, aux = _MoETrain.apply(x, cfg, anchor, *masters)
         if dp != r.width:
             out = out[:, :r.width]
-        self.last_load = cfg["counts"].to(torch.int64)
+        self._last_counts = cfg["counts"]
         self.last_aux_parts = aux.detach()
         # "inject": the gradient comes from the backward itself, so the returned value is
         # detached and adding it to a loss changes nothing

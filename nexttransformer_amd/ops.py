@@ -1122,6 +1122,21 @@ def backward_weights(w1, w2, shared_w1=None, shared_w2=None, w_router_t=None, **
     return BackwardWeights(w1, w2, shared_w1, shared_w2, w_router_t, **transposes)
 
 
+_unit_cache = {}
+
+
+def _unit_weights(T, k, device):
+    """Cached fp32 ones [T, k] (the unit combine weights of the input-gradient sum), read only;
+    a fill kernel less per backward. Holds the last few shapes."""
+    key = (T, k, device)
+    t = _unit_cache.get(key)
+    if t is None:
+        if len(_unit_cache) >= 8:
+            _unit_cache.clear()
+        t = _unit_cache[key] = torch.ones(T, k, device=device, dtype=torch.float32)
+    return t
+
+
 def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
                  score_fn=nat.SCORE_SOFTMAX, activation=nat.ACT_SWIGLU, aux_coeff=0.01,
                  z_coeff=0.001, mark=None, weight_grads_fp32=False):
@@ -1195,9 +1210,9 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
     wr = grouped_wgrad.raw(g_cat, x, None, seg, T, wgrad_splits(1, 2 * Ep, d, T, x.device), True)[0]
     res["router"] = wr[:E] + wr[Ep:Ep + E]
     mark("router_bwd")
-    ones = torch.ones(T, k, device=x.device, dtype=torch.float32)
-    res["x"], _ = combine_aux.raw(dxp, cdest, ones, first, state["prob_partial"],
-                              state["z_partial"], state["counts"], 0.0, 0.0)
+    res["x"], _ = combine_aux.raw(dxp, cdest, _unit_weights(T, k, x.device), first,
+                                  state["prob_partial"], state["z_partial"], state["counts"],
+                                  0.0, 0.0)
     mark("dx_sum")
     # expert weight gradients over each expert's rows; the shared expert's over all T rows
     f32 = weight_grads_fp32
