@@ -903,18 +903,20 @@ hipError_t launch_t256(const uint16_t* a, int64_t lda, const uint16_t* b, int64_
   return hipGetLastError();
 }
 
-// Whether the 256 x 256 kernel takes a product: both widths whole 256-wide tiles.
-bool wgrad_t256(int N, int M) { return N % 256 == 0 && M % 256 == 0; }
+// Whether the 256 x 256 kernel takes a product: both widths whole 256-wide tiles, and no split
+// K (a split product has too few tiles to fill the chip with one workgroup per CU at the split
+// count sized for the two-per-CU kernels: the T3 cell's router gradient ran 39 -> 45 us on it).
+bool wgrad_t256(int N, int M, int splits) { return N % 256 == 0 && M % 256 == 0 && splits == 1; }
 
-// The transposing-read kernels: 256 x 256 tiles when both widths are multiples of 256, else
-// 128 x 256 when N <= M, else 256 x 128.
+// The transposing-read kernels: 256 x 256 tiles when both widths are multiples of 256 and K is
+// not split, else 128 x 256 when N <= M, else 256 x 128.
 template <bool OUT_F32>
 hipError_t launch_tr_any(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
                          int64_t b_rows, const int32_t* b_src_row, const int32_t* seg_offsets,
                          int num_segments, int64_t total_rows, int N, int M, int splits, void* c,
                          hipStream_t stream) {
   const bool g = b_src_row != nullptr;
-  if (wgrad_t256(N, M)) {
+  if (wgrad_t256(N, M, splits)) {
     if (g)
       return launch_t256<true, OUT_F32>(a, lda, b, ldb, b_rows, b_src_row, seg_offsets,
                                         num_segments, total_rows, N, M, splits, c, stream);

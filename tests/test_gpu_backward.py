@@ -223,17 +223,17 @@ def test_grouped_wgrad_matches_float64(gather):
 
 WGRAD_SHAPES = [(320, 192, False, 1), (192, 320, True, 1), (64, 64, True, 1),
                 (320, 1280, True, 1), (1280, 320, False, 1), (128, 256, True, 3),
-                (256, 128, False, 4), (256, 256, True, 1), (512, 256, False, 3),
-                (256, 768, True, 2)]
+                (256, 128, False, 4), (256, 256, True, 1), (512, 256, False, 1),
+                (256, 768, True, 1), (256, 768, True, 2)]
 
 
 @pytest.mark.parametrize("N,M,gather,splits", WGRAD_SHAPES,
                          ids=[f"N{n}-M{m}-{'gather' if g else 'rows'}-s{k}"
                               for n, m, g, k in WGRAD_SHAPES])
 def test_grouped_wgrad_shapes_fp32_and_bf16(N, M, gather, splits):
-    """Every tile shape (256 x 256 when N and M are multiples of 256; else N <= M: 128 x 256,
-    else 256 x 128; segments of 1, 2, 3 and 9 slabs against the 256 x 256 kernel's three-slab
-    copy lead), partial tiles in N and M
+    """Every tile shape (256 x 256 when N and M are multiples of 256 and K is not split; else
+    N <= M: 128 x 256, else 256 x 128; segments of 1, 2, 3 and 9 slabs against the 256 x 256
+    kernel's three-slab copy lead), partial tiles in N and M
     (320 = 256 + 64, 192 = 128 + 64), ragged segments (empty, 1 row, not a multiple of the
     32-row slab, several slabs), gathered B rows (with indices past a slab boundary), split K in
     fixed order; fp32 output against float64 at fp32-accumulation tolerance, bf16 output equal
@@ -263,9 +263,9 @@ def test_grouped_wgrad_shapes_fp32_and_bf16(N, M, gather, splits):
 
 @pytest.mark.parametrize("gather,splits", [(False, 1), (True, 1), (True, 2)])
 def test_grouped_wgrad_walks_many_tiles(gather, splits):
-    """Many tiles (64 segments x 8 tiles of 256 x 256, twice that with split K) over ragged
-    segments: empty segments between non-empty ones, one-row and one-slab segments, segments of
-    many slabs; fp32 output against float64."""
+    """Many tiles (64 segments x 8 tiles of 256 x 256; with split K, two chunks of 16 tiles of
+    128 x 256 per segment) over ragged segments: empty segments between non-empty ones, one-row
+    and one-slab segments, segments of many slabs; fp32 output against float64."""
     from nexttransformer_amd import ops
     gen = torch.Generator().manual_seed(7 + 2 * gather + splits)
     S, N, M = 64, 512, 1024
