@@ -445,6 +445,24 @@ int nt_moe_backward_first_operand(const float* grad_logits, int32_t E, const uin
                                   nt_moe_stream_t stream);
 
 /*
+ * The two expert weight gradients of the backward in one call, over the same segments
+ * (autograd of the per-expert products of megatron_moe.py:145, as nt_moe_grouped_wgrad_bf16
+ * computes each): product i is c_i[s] = a_i[rows of s]^T b_i[row_i(r)], e.g. dW1 (a0 = grad_fc1,
+ * b0 = x gathered through b_src_row0) and dW2 (a1 = grad_y, b1 = h, b_src_row1 = NULL); no split
+ * K; c_i fp32 [num_segments, N_i, M_i] when c_fp32, else bf16. Where both products' N and M are
+ * multiples of 256 they run as one launch over both tile lists (one tail instead of two), else one
+ * after the other. Results are bit-identical to two nt_moe_grouped_wgrad_splitk calls with
+ * splits = 1. Arguments as nt_moe_grouped_wgrad_bf16's, for each product.
+ */
+int nt_moe_grouped_wgrad_pair(const uint16_t* a0, int64_t lda0, const uint16_t* b0, int64_t ldb0,
+                              int64_t b_rows0, const int32_t* b_src_row0, int32_t N0, int32_t M0,
+                              void* c0, const uint16_t* a1, int64_t lda1, const uint16_t* b1,
+                              int64_t ldb1, int64_t b_rows1, const int32_t* b_src_row1,
+                              int32_t N1, int32_t M1, void* c1, const int32_t* seg_offsets,
+                              int32_t num_segments, int64_t total_rows, int32_t c_fp32,
+                              nt_moe_stream_t stream);
+
+/*
  * Router backward: grad_logits fp32 [T, E] from grad_w (the routing weights' gradient, top-k
  * slot order) through the k-selected normalisation of score_fn, plus the load-balance and
  * z-loss terms when grad_aux (device fp32 [3], the gradient of nt_moe_combine_aux's

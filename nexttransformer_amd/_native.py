@@ -62,6 +62,9 @@ SIGNATURES = {
     "nt_moe_convert_expert_weights": (_i32, [_p, _i64, _i32, _i32, _p, _p, _p]),
     "nt_moe_convert_expert_weights_packed": (_i32, [_p, _i64, _i32, _i32, _p, _p, _p, _i32, _p,
                                                     _p]),
+    "nt_moe_grouped_wgrad_pair": (_i32, [_p, _i64, _p, _i64, _i64, _p, _i32, _i32, _p, _p, _i64,
+                                          _p, _i64, _i64, _p, _i32, _i32, _p, _p, _i32, _i64,
+                                          _i32, _p]),
     "nt_moe_router_operands": (_i32, [_p, _i64, _i32, _i32, _i32, _p, _i64, _i32, _p, _p, _i32,
                                        _i32, _p]),
     "nt_moe_pack_expert_weights_bf16": (_i32, [_p, _i64, _i32, _i32, _i32, _p, _p]),

@@ -332,6 +332,26 @@ int nt_moe_grouped_wgrad_splitk(const uint16_t* a, int64_t lda, const uint16_t* 
                   "grouped_wgrad_splitk");
 }
 
+int nt_moe_grouped_wgrad_pair(const uint16_t* a0, int64_t lda0, const uint16_t* b0, int64_t ldb0,
+                              int64_t b_rows0, const int32_t* b_src_row0, int32_t N0, int32_t M0,
+                              void* c0, const uint16_t* a1, int64_t lda1, const uint16_t* b1,
+                              int64_t ldb1, int64_t b_rows1, const int32_t* b_src_row1,
+                              int32_t N1, int32_t M1, void* c1, const int32_t* seg_offsets,
+                              int32_t num_segments, int64_t total_rows, int32_t c_fp32,
+                              nt_moe_stream_t stream) {
+  int rc = check_wgrad(a0, lda0, b0, ldb0, b_rows0, b_src_row0, seg_offsets, num_segments,
+                       total_rows, N0, M0, c0);
+  if (rc) return rc;
+  rc = check_wgrad(a1, lda1, b1, ldb1, b_rows1, b_src_row1, seg_offsets, num_segments, total_rows,
+                   N1, M1, c1);
+  if (rc) return rc;
+  return launched(launch_grouped_wgrad_pair(a0, lda0, b0, ldb0, b_rows0, b_src_row0, N0, M0, c0,
+                                            a1, lda1, b1, ldb1, b_rows1, b_src_row1, N1, M1, c1,
+                                            seg_offsets, num_segments, total_rows, c_fp32 != 0,
+                                            reinterpret_cast<hipStream_t>(stream)),
+                  "grouped_wgrad_pair");
+}
+
 int nt_moe_router_bwd(const float* logits, const int32_t* topk_ids, const float* topk_w,
                       const float* grad_w, const int32_t* counts, int64_t T, int32_t E,
                       int32_t k, int32_t score_fn, const float* grad_aux, float aux_coeff,

@@ -101,6 +101,15 @@ hipError_t launch_grouped_wgrad(const uint16_t* a, int64_t lda, const uint16_t* 
                                 const int32_t* seg_offsets, int num_segments, int64_t total_rows,
                                 int N, int M, int splits, float* partial, bool c_f32, void* c,
                                 hipStream_t stream);
+// Two products over the same segments without split K: one launch of the 256 x 256 kernel
+// when both take it, else one launch_grouped_wgrad after the other.
+hipError_t launch_grouped_wgrad_pair(const uint16_t* a0, int64_t lda0, const uint16_t* b0,
+                                     int64_t ldb0, int64_t b_rows0, const int32_t* b_src_row0,
+                                     int N0, int M0, void* c0, const uint16_t* a1, int64_t lda1,
+                                     const uint16_t* b1, int64_t ldb1, int64_t b_rows1,
+                                     const int32_t* b_src_row1, int N1, int M1, void* c1,
+                                     const int32_t* seg_offsets, int num_segments,
+                                     int64_t total_rows, bool c_f32, hipStream_t stream);
 hipError_t launch_combine_bwd(const uint16_t* g, int64_t ld_g, const uint16_t* y,
                               const int32_t* topk_ids, const int32_t* combine_dest,
                               const float* combine_w, int64_t T, int d, int k, uint16_t* dy,

@@ -533,23 +533,52 @@ struct T2Geo {
   static constexpr size_t lds() { return (size_t)kT2Ring * kStage + kT2Idx * kTK * 4; }
 };
 
-template <bool GATHER, bool OUT_F32>
-__global__ __launch_bounds__(256, 1) void grouped_wgrad_t256_kernel(
-    const uint16_t* __restrict__ a, int64_t lda, const uint16_t* __restrict__ b, int64_t ldb,
-    int64_t b_rows, const int32_t* __restrict__ b_src_row, const int32_t* __restrict__ seg_offsets,
-    int num_segments, int64_t total_rows, int N, int M, int splits, void* __restrict__ c) {
+// One product of the kernel below (its workgroups: tiles x splits) and the launch's products,
+// which share the segments: up to two, their tile lists one after the other.
+struct T2Product {
+  const uint16_t* a;
+  const uint16_t* b;
+  const int32_t* b_src_row;  // NULL: no gather
+  void* c;
+  int64_t lda, ldb, b_rows;
+  int N, M, blocks;
+};
+struct T2Args {
+  T2Product p[2];
+  const int32_t* seg_offsets;
+  int64_t total_rows;
+  int num_segments, splits, count;
+};
+
+template <bool OUT_F32>
+__global__ __launch_bounds__(256, 1) void grouped_wgrad_t256_kernel(T2Args args) {
   using G = T2Geo;
   constexpr int TN = 256, TM = 256, kB = 4;  // kB: 32-wide blocks per wave and dimension
   extern __shared__ __align__(16) unsigned char smem[];
   int* idx_ring = reinterpret_cast<int*>(smem + kT2Ring * G::kStage);  // [kT2Idx][kTK]
-  const int ntn = (N + TN - 1) / TN, ntm = (M + TM - 1) / TM;
-  const int per_seg = ntn * ntm;
   int blk;  // XCD-contiguous ranges of the tile list, as above
   {
     const int nb = (int)gridDim.x, q = nb / 8, r = nb % 8;
     const int xcd = (int)blockIdx.x % 8, slot = (int)blockIdx.x / 8;
     blk = xcd * q + (xcd < r ? xcd : r) + slot;
   }
+  // this workgroup's product (fields selected one by one: no indexing of the argument block)
+  const bool second = args.count > 1 && blk >= args.p[0].blocks;
+  if (second) blk -= args.p[0].blocks;
+  const uint16_t* __restrict__ a = second ? args.p[1].a : args.p[0].a;
+  const uint16_t* __restrict__ b = second ? args.p[1].b : args.p[0].b;
+  const int32_t* __restrict__ b_src_row = second ? args.p[1].b_src_row : args.p[0].b_src_row;
+  void* __restrict__ c = second ? args.p[1].c : args.p[0].c;
+  const int64_t lda = second ? args.p[1].lda : args.p[0].lda;
+  const int64_t ldb = second ? args.p[1].ldb : args.p[0].ldb;
+  const int64_t b_rows = second ? args.p[1].b_rows : args.p[0].b_rows;
+  const int N = second ? args.p[1].N : args.p[0].N, M = second ? args.p[1].M : args.p[0].M;
+  const int32_t* __restrict__ seg_offsets = args.seg_offsets;
+  const int num_segments = args.num_segments, splits = args.splits;
+  const int64_t total_rows = args.total_rows;
+  const bool gather = b_src_row != nullptr;
+  const int ntn = (N + TN - 1) / TN, ntm = (M + TM - 1) / TM;
+  const int per_seg = ntn * ntm;
   const int split = blk / (num_segments * per_seg);
   const int rest = blk - split * num_segments * per_seg;
   const int s = rest / per_seg;
@@ -583,232 +612,242 @@ __global__ __launch_bounds__(256, 1) void grouped_wgrad_t256_kernel(
     const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(a + lo * lda), 0, (int)((int64_t)rows * lda * 2), kBufWord3);
     const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(GATHER ? b : b + lo * ldb), 0,
-        (int)(GATHER ? b_rows * ldb * 2 : (int64_t)rows * ldb * 2), kBufWord3);
+        (void*)(gather ? b : b + lo * ldb), 0,
+        (int)(gather ? b_rows * ldb * 2 : (int64_t)rows * ldb * 2), kBufWord3);
     const __amdgpu_buffer_rsrc_t ir = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(GATHER ? b_src_row + lo : seg_offsets), 0, GATHER ? rows * 4 : 0, kBufWord3);
+        (void*)(gather ? b_src_row + lo : seg_offsets), 0, gather ? rows * 4 : 0, kBufWord3);
 
-    // Copy instruction i of this wave covers slab row (wave * kCopies + i) * 2 + lane / 32, chunk
-    // position lane % 32, i.e. global chunk (lane % 32) ^ 4 (row % 4) (columns past N or M
-    // repeat the last 8).
-    auto chunk_col = [&](int row, int col0, int width) {
-      const int cg = (lane % 32) ^ (4 * (row & 3));
-      const int col = col0 + 8 * cg;
-      return col < width ? col : width - 8;
-    };
-    int a_voff[G::kCopies], b_coloff[G::kCopies], b_row[G::kCopies];
-#pragma unroll
-    for (int i = 0; i < G::kCopies; ++i) {
-      const int row = (wave * G::kCopies + i) * 2 + lane / 32;
-      a_voff[i] = row * (int)lda * 2 + chunk_col(row, n0, N) * 2;
-      b_row[i] = row;
-      b_coloff[i] = chunk_col(row, m0, M) * 2;
-    }
-    // Index loads of slab t (GATHER): wave w loads rows 8 w .. 8 w + 7 with lanes 0-7.
-    auto issue_idx = [&](int t) __attribute__((always_inline)) {
-      if constexpr (GATHER) {
-        int* dst = idx_ring + (t % kT2Idx) * kTK + 8 * wave;
-        const int r = t * kTK + 8 * wave + lane;
-        if (lane < 8) buffer_to_lds4(ir, dst, r * 4);
-      }
-    };
-    // Slab t's gathered row indices for this wave's B copies, read from the index ring without a
-    // wait (the caller's next wait for every LDS read covers them), and B's source offsets for
-    // slab t's copies from them (or from the row itself without the gather); rows past the chunk
-    // get an out-of-range offset.
-    const uint32_t idx_lds = (uint32_t)(uintptr_t)idx_ring;
-    auto idx_read = [&](int t, int (&gi)[G::kCopies]) __attribute__((always_inline)) {
-      if constexpr (GATHER) {
-        const uint32_t slot = idx_lds + (uint32_t)((t % kT2Idx) * kTK * 4);
-#pragma unroll
-        for (int i = 0; i < G::kCopies; ++i)
-          asm volatile("ds_read_b32 %0, %1" : "=v"(gi[i]) : "v"(slot + b_row[i] * 4));
-      }
-    };
-    auto idx_fence = [](int (&gi)[G::kCopies]) __attribute__((always_inline)) {
-      if constexpr (GATHER) asm volatile("" : "+v"(gi[0]), "+v"(gi[1]), "+v"(gi[2]), "+v"(gi[3]));
-    };
-    auto b_offsets = [&](int t, const int (&gi)[G::kCopies], int (&bv)[G::kCopies])
-                         __attribute__((always_inline)) {
-#pragma unroll
+    // The slab loop, compiled once per gather kind (gather: one product's rows gathered through
+    // b_src_row, with the index loads and reads; a launch may hold one product of each kind).
+    auto run = [&](auto gather_c) __attribute__((always_inline)) {
+      constexpr bool GATHER = decltype(gather_c)::value;
+      // Copy instruction i of this wave covers slab row (wave * kCopies + i) * 2 + lane / 32, chunk
+      // position lane % 32, i.e. global chunk (lane % 32) ^ 4 (row % 4) (columns past N or M
+      // repeat the last 8).
+      auto chunk_col = [&](int row, int col0, int width) {
+        const int cg = (lane % 32) ^ (4 * (row & 3));
+        const int col = col0 + 8 * cg;
+        return col < width ? col : width - 8;
+      };
+      int a_voff[G::kCopies], b_coloff[G::kCopies], b_row[G::kCopies];
+  #pragma unroll
       for (int i = 0; i < G::kCopies; ++i) {
-        const int r = t * kTK + b_row[i];
-        if (GATHER) {
-          int g = gi[i];
-          g = g < 0 ? 0 : (g >= b_rows ? (int)b_rows - 1 : g);
-          bv[i] = r < rows ? g * (int)ldb * 2 + b_coloff[i] : 0x7fffffff;
-        } else {
-          bv[i] = r < rows ? r * (int)ldb * 2 + b_coloff[i] : 0x7fffffff;
+        const int row = (wave * G::kCopies + i) * 2 + lane / 32;
+        a_voff[i] = row * (int)lda * 2 + chunk_col(row, n0, N) * 2;
+        b_row[i] = row;
+        b_coloff[i] = chunk_col(row, m0, M) * 2;
+      }
+      // Index loads of slab t (GATHER): wave w loads rows 8 w .. 8 w + 7 with lanes 0-7.
+      auto issue_idx = [&](int t) __attribute__((always_inline)) {
+        if constexpr (GATHER) {
+          int* dst = idx_ring + (t % kT2Idx) * kTK + 8 * wave;
+          const int r = t * kTK + 8 * wave + lane;
+          if (lane < 8) buffer_to_lds4(ir, dst, r * 4);
         }
-      }
-    };
-    // Item k of the group published with slab p: A copies, B copies, the index load of slab
-    // p + kT2ILead. The copies of slab t = p + kT2Lead go into the slot slab p - 1 left; every
-    // group is issued, those past the last slab reading only out-of-range offsets (zeros, no
-    // memory traffic), so each wait below counts a fixed number of operations.
-    constexpr int kPer = 2 * G::kCopies + (GATHER ? 1 : 0);  // vector memory operations per group
-    auto group_item = [&](int p, auto k_c, const int (&bv)[G::kCopies]) __attribute__((always_inline)) {
-      constexpr int k = decltype(k_c)::value;
-      const int t = p + kT2Lead;
-      unsigned char* st = smem + (t % kT2Ring) * G::kStage;
-      if constexpr (k < G::kCopies) {
-        buffer_to_lds16(ar, st + (wave * G::kCopies + k) * 1024, a_voff[k] + t * kTK * (int)lda * 2);
-      } else if constexpr (k < 2 * G::kCopies) {
-        constexpr int i = k - G::kCopies;
-        buffer_to_lds16(br, st + G::kSlab + (wave * G::kCopies + i) * 1024, bv[i]);
-      } else {
-        issue_idx(p + kT2ILead);
-      }
-    };
-    auto group = [&](int p, const int (&bv)[G::kCopies]) __attribute__((always_inline)) {
-      static_for<0, kPer>([&](auto k_c) __attribute__((always_inline)) { group_item(p, k_c, bv); });
-    };
-    // Slab p's copies (group p - kT2Lead) have landed once at most the two groups issued after it
-    // are outstanding.
-    auto wait_slab = []() __attribute__((always_inline)) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kPer) : "memory");
-    };
-
-    const int pg = (lane >> 4) & 1, pp = lane & 15, ph = lane >> 5;
-    auto tr_off = [&](int cb) {
-      const int row = 8 * ph + (pp >> 2);
-      const int col = cb + 16 * pg + 4 * (pp & 3);
-      const int chunk = (col >> 3) ^ (4 * (row & 3));
-      return (uint32_t)(row * 256 * 2 + chunk * 16 + (col & 7) * 2);
-    };
-    const uint32_t smem_base = (uint32_t)(uintptr_t)smem;
-    uint32_t offa[kB], offb[kB];
-#pragma unroll
-    for (int i = 0; i < kB; ++i) {
-      offa[i] = smem_base + tr_off(128 * wn + 32 * i);
-      offb[i] = smem_base + G::kSlab + tr_off(128 * wm + 32 * i);
-    }
-    struct Frags {
-      u32x2 a[kB][2], b[kB][2];
-    };
-    // Read r (0-15) of the fragments for K rows 16 kk .. 16 kk + 15 of the slab at stage_off:
-    // A blocks for r < 8, B blocks after.
-    auto read_one = [](uint32_t stage_off, auto kk_c, auto r_c, const uint32_t (&oa)[kB],
-                       const uint32_t (&ob)[kB], Frags& f) __attribute__((always_inline)) {
-      constexpr int kk = decltype(kk_c)::value, r = decltype(r_c)::value;
-      constexpr int blk = (r % 8) / 2, hf = r % 2;
-      constexpr int off = (16 * kk + 4 * hf) * 512;
-      if constexpr (r < 8)
-        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
-                     : "=v"(f.a[blk][hf]) : "v"(oa[blk] + stage_off), "n"(off));
-      else
-        asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
-                     : "=v"(f.b[blk][hf]) : "v"(ob[blk] + stage_off), "n"(off));
-    };
-    // Waits for every LDS read in flight, naming the fragment registers.
-    auto frag_wait = [](Frags& f) __attribute__((always_inline)) {
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(f.a[0][0]), "+v"(f.a[0][1]), "+v"(f.a[1][0]), "+v"(f.a[1][1]),
-                     "+v"(f.a[2][0]), "+v"(f.a[2][1]), "+v"(f.a[3][0]), "+v"(f.a[3][1]),
-                     "+v"(f.b[0][0]), "+v"(f.b[0][1]), "+v"(f.b[1][0]), "+v"(f.b[1][1]),
-                     "+v"(f.b[2][0]), "+v"(f.b[2][1]), "+v"(f.b[3][0]), "+v"(f.b[3][1])
-                   :
-                   : "memory");
-    };
-    // The 16 MFMAs of fragments fc (one wave per SIMD, so nothing else would fill the matrix
-    // core while this wave issued a burst of reads or copies: they go out between the MFMAs).
-    // READ: the 16 reads of fn (stage sn, K half KKN), two after each of the first four MFMAs and
-    // one after each of the next eight, so they land while the last four run. COPY: the items
-    // of group p, one after each of the first kPer MFMAs. IDX: the index reads of slab ti after
-    // the fifth MFMA.
-    auto half = [&](const Frags& fc, Frags& fn, uint32_t sn, auto kkn_c, auto read_c, auto copy_c,
-                    auto idx_c, int p, const int (&bv)[G::kCopies], int ti,
-                    int (&gi)[G::kCopies]) __attribute__((always_inline)) {
-      constexpr bool READ = decltype(read_c)::value, COPY = decltype(copy_c)::value;
-      constexpr bool IDX = decltype(idx_c)::value;
-      static_for<0, 16>([&](auto k_c) __attribute__((always_inline)) {
+      };
+      // Slab t's gathered row indices for this wave's B copies, read from the index ring without a
+      // wait (the caller's next wait for every LDS read covers them), and B's source offsets for
+      // slab t's copies from them (or from the row itself without the gather); rows past the chunk
+      // get an out-of-range offset.
+      const uint32_t idx_lds = (uint32_t)(uintptr_t)idx_ring;
+      auto idx_read = [&](int t, int (&gi)[G::kCopies]) __attribute__((always_inline)) {
+        if constexpr (GATHER) {
+          const uint32_t slot = idx_lds + (uint32_t)((t % kT2Idx) * kTK * 4);
+  #pragma unroll
+          for (int i = 0; i < G::kCopies; ++i)
+            asm volatile("ds_read_b32 %0, %1" : "=v"(gi[i]) : "v"(slot + b_row[i] * 4));
+        }
+      };
+      auto idx_fence = [](int (&gi)[G::kCopies]) __attribute__((always_inline)) {
+        if constexpr (GATHER) asm volatile("" : "+v"(gi[0]), "+v"(gi[1]), "+v"(gi[2]), "+v"(gi[3]));
+      };
+      auto b_offsets = [&](int t, const int (&gi)[G::kCopies], int (&bv)[G::kCopies])
+                           __attribute__((always_inline)) {
+  #pragma unroll
+        for (int i = 0; i < G::kCopies; ++i) {
+          const int r = t * kTK + b_row[i];
+          int src = r;
+          if constexpr (GATHER) {
+            const int g = gi[i];
+            src = g < 0 ? 0 : (g >= b_rows ? (int)b_rows - 1 : g);
+          }
+          bv[i] = r < rows ? src * (int)ldb * 2 + b_coloff[i] : 0x7fffffff;
+        }
+      };
+      // Item k of the group published with slab p: A copies, B copies, the index load of slab
+      // p + kT2ILead. The copies of slab t = p + kT2Lead go into the slot slab p - 1 left; every
+      // group is issued, those past the last slab reading only out-of-range offsets (zeros, no
+      // memory traffic), so each wait below counts a fixed number of operations.
+      constexpr int kPer = 2 * G::kCopies + (GATHER ? 1 : 0);  // vector memory operations per group
+      auto group_item = [&](int p, auto k_c, const int (&bv)[G::kCopies])
+                            __attribute__((always_inline)) {
         constexpr int k = decltype(k_c)::value;
-        constexpr int i = k / kB, j = k % kB;
-        const bf16x8 fa = __builtin_bit_cast(
-            bf16x8, u32x4{fc.a[i][0][0], fc.a[i][0][1], fc.a[i][1][0], fc.a[i][1][1]});
-        const bf16x8 fb = __builtin_bit_cast(
-            bf16x8, u32x4{fc.b[j][0][0], fc.b[j][0][1], fc.b[j][1][0], fc.b[j][1][1]});
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb, fa, acc[i][j], 0, 0, 0);
-        if constexpr (READ) {
-          constexpr int r0 = k < 4 ? 2 * k : (k < 12 ? k + 4 : 16);
-          constexpr int r1 = k < 4 ? 2 * k + 2 : (k < 12 ? k + 5 : 16);
-          static_for<r0, r1>([&](auto r_c) __attribute__((always_inline)) {
-            read_one(sn, kkn_c, r_c, offa, offb, fn);
-          });
+        const int t = p + kT2Lead;
+        unsigned char* st = smem + (t % kT2Ring) * G::kStage;
+        if constexpr (k < G::kCopies) {
+          buffer_to_lds16(ar, st + (wave * G::kCopies + k) * 1024,
+                          a_voff[k] + t * kTK * (int)lda * 2);
+        } else if constexpr (k < 2 * G::kCopies) {
+          constexpr int i = k - G::kCopies;
+          buffer_to_lds16(br, st + G::kSlab + (wave * G::kCopies + i) * 1024, bv[i]);
+        } else {
+          issue_idx(p + kT2ILead);
         }
-        if constexpr (COPY && k < kPer) group_item(p, k_c, bv);
-        if constexpr (IDX && k == 4) idx_read(ti, gi);
-        __builtin_amdgcn_sched_barrier(0);
-      });
-    };
-    auto barrier = []() __attribute__((always_inline)) {
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-    };
-    using I0 = std::integral_constant<int, 0>;
-    using I1 = std::integral_constant<int, 1>;
+      };
+      auto group = [&](int p, const int (&bv)[G::kCopies]) __attribute__((always_inline)) {
+        static_for<0, kPer>([&](auto k_c) __attribute__((always_inline)) {
+          group_item(p, k_c, bv);
+        });
+      };
+      // Slab p's copies (group p - kT2Lead) have landed once at most the two groups issued after it
+      // are outstanding.
+      auto wait_slab = []() __attribute__((always_inline)) {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kPer) : "memory");
+      };
 
-    // Prologue: the index loads of slabs 0 .. 3 published; groups -3, -2, -1 (the copies of
-    // slabs 0, 1, 2); slab 0 published; group 0; slab 0's first fragments.
-    int bv[G::kCopies], gi[G::kCopies];
-    if (GATHER) {
-      issue_idx(0);
-      issue_idx(1);
-      issue_idx(2);
-      issue_idx(3);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      barrier();
-    }
-#pragma unroll
-    for (int p = -kT2Lead; p < 0; ++p) {
-      idx_read(p + kT2Lead, gi);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      idx_fence(gi);
-      b_offsets(p + kT2Lead, gi, bv);
-      group(p, bv);
-    }
-    wait_slab();
-    barrier();
-    idx_read(kT2Lead, gi);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    idx_fence(gi);
-    b_offsets(kT2Lead, gi, bv);
-    group(0, bv);
-    Frags f0, f1;
-    static_for<0, 16>([&](auto r_c) __attribute__((always_inline)) {
-      read_one(0, I0(), r_c, offa, offb, f0);
-    });
-    // Slab t: its first K half, with the second half's reads and the index reads of group t + 1;
-    // slab t + 1 published (its copies landed, every wave past its reads of slab t, whose slot
-    // the next group then refills; the indices of group t + 1 were published with slab t); the
-    // second half, with slab t + 1's first reads and group t + 1.
-    for (int t = 0; t + 1 < n_slabs; ++t) {
-      const uint32_t st = (t % kT2Ring) * G::kStage;
-      frag_wait(f0);
-      __builtin_amdgcn_sched_barrier(0);
-      half(f0, f1, st, I1(), std::true_type(), std::false_type(), std::true_type(), 0, bv,
-           t + 1 + kT2Lead, gi);
+      const int pg = (lane >> 4) & 1, pp = lane & 15, ph = lane >> 5;
+      auto tr_off = [&](int cb) {
+        const int row = 8 * ph + (pp >> 2);
+        const int col = cb + 16 * pg + 4 * (pp & 3);
+        const int chunk = (col >> 3) ^ (4 * (row & 3));
+        return (uint32_t)(row * 256 * 2 + chunk * 16 + (col & 7) * 2);
+      };
+      const uint32_t smem_base = (uint32_t)(uintptr_t)smem;
+      uint32_t offa[kB], offb[kB];
+  #pragma unroll
+      for (int i = 0; i < kB; ++i) {
+        offa[i] = smem_base + tr_off(128 * wn + 32 * i);
+        offb[i] = smem_base + G::kSlab + tr_off(128 * wm + 32 * i);
+      }
+      struct Frags {
+        u32x2 a[kB][2], b[kB][2];
+      };
+      // Read r (0-15) of the fragments for K rows 16 kk .. 16 kk + 15 of the slab at stage_off:
+      // A blocks for r < 8, B blocks after.
+      auto read_one = [](uint32_t stage_off, auto kk_c, auto r_c, const uint32_t (&oa)[kB],
+                         const uint32_t (&ob)[kB], Frags& f) __attribute__((always_inline)) {
+        constexpr int kk = decltype(kk_c)::value, r = decltype(r_c)::value;
+        constexpr int blk = (r % 8) / 2, hf = r % 2;
+        constexpr int off = (16 * kk + 4 * hf) * 512;
+        if constexpr (r < 8)
+          asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                       : "=v"(f.a[blk][hf]) : "v"(oa[blk] + stage_off), "n"(off));
+        else
+          asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                       : "=v"(f.b[blk][hf]) : "v"(ob[blk] + stage_off), "n"(off));
+      };
+      // Waits for every LDS read in flight, naming the fragment registers.
+      auto frag_wait = [](Frags& f) __attribute__((always_inline)) {
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(f.a[0][0]), "+v"(f.a[0][1]), "+v"(f.a[1][0]), "+v"(f.a[1][1]),
+                       "+v"(f.a[2][0]), "+v"(f.a[2][1]), "+v"(f.a[3][0]), "+v"(f.a[3][1]),
+                       "+v"(f.b[0][0]), "+v"(f.b[0][1]), "+v"(f.b[1][0]), "+v"(f.b[1][1]),
+                       "+v"(f.b[2][0]), "+v"(f.b[2][1]), "+v"(f.b[3][0]), "+v"(f.b[3][1])
+                     :
+                     : "memory");
+      };
+      // The 16 MFMAs of fragments fc (one wave per SIMD, so nothing else would fill the matrix
+      // core while this wave issued a burst of reads or copies: they go out between the MFMAs).
+      // READ: the 16 reads of fn (stage sn, K half KKN), two after each of the first four MFMAs and
+      // one after each of the next eight, so they land while the last four run. COPY: the items
+      // of group p, one after each of the first kPer MFMAs. IDX: the index reads of slab ti after
+      // the fifth MFMA.
+      auto half = [&](const Frags& fc, Frags& fn, uint32_t sn, auto kkn_c, auto read_c, auto copy_c,
+                      auto idx_c, int p, const int (&bv)[G::kCopies], int ti,
+                      int (&gi)[G::kCopies]) __attribute__((always_inline)) {
+        constexpr bool READ = decltype(read_c)::value, COPY = decltype(copy_c)::value;
+        constexpr bool IDX = decltype(idx_c)::value;
+        static_for<0, 16>([&](auto k_c) __attribute__((always_inline)) {
+          constexpr int k = decltype(k_c)::value;
+          constexpr int i = k / kB, j = k % kB;
+          const bf16x8 fa = __builtin_bit_cast(
+              bf16x8, u32x4{fc.a[i][0][0], fc.a[i][0][1], fc.a[i][1][0], fc.a[i][1][1]});
+          const bf16x8 fb = __builtin_bit_cast(
+              bf16x8, u32x4{fc.b[j][0][0], fc.b[j][0][1], fc.b[j][1][0], fc.b[j][1][1]});
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb, fa, acc[i][j], 0, 0, 0);
+          if constexpr (READ) {
+            constexpr int r0 = k < 4 ? 2 * k : (k < 12 ? k + 4 : 16);
+            constexpr int r1 = k < 4 ? 2 * k + 2 : (k < 12 ? k + 5 : 16);
+            static_for<r0, r1>([&](auto r_c) __attribute__((always_inline)) {
+              read_one(sn, kkn_c, r_c, offa, offb, fn);
+            });
+          }
+          if constexpr (COPY && k < kPer) group_item(p, k_c, bv);
+          if constexpr (IDX && k == 4) idx_read(ti, gi);
+          __builtin_amdgcn_sched_barrier(0);
+        });
+      };
+      auto barrier = []() __attribute__((always_inline)) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+      };
+      using I0 = std::integral_constant<int, 0>;
+      using I1 = std::integral_constant<int, 1>;
+
+      // Prologue: the index loads of slabs 0 .. 3 published; groups -3, -2, -1 (the copies of
+      // slabs 0, 1, 2); slab 0 published; group 0; slab 0's first fragments.
+      int bv[G::kCopies], gi[G::kCopies] = {0, 0, 0, 0};
+      if (GATHER) {
+        issue_idx(0);
+        issue_idx(1);
+        issue_idx(2);
+        issue_idx(3);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        barrier();
+      }
+  #pragma unroll
+      for (int p = -kT2Lead; p < 0; ++p) {
+        idx_read(p + kT2Lead, gi);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        idx_fence(gi);
+        b_offsets(p + kT2Lead, gi, bv);
+        group(p, bv);
+      }
       wait_slab();
       barrier();
-      frag_wait(f1);
+      idx_read(kT2Lead, gi);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       idx_fence(gi);
-      b_offsets(t + 1 + kT2Lead, gi, bv);
-      __builtin_amdgcn_sched_barrier(0);
-      half(f1, f0, ((t + 1) % kT2Ring) * G::kStage, I0(), std::true_type(), std::true_type(),
-           std::false_type(), t + 1, bv, 0, gi);
-    }
-    {  // the last slab
-      const uint32_t st = ((n_slabs - 1) % kT2Ring) * G::kStage;
-      frag_wait(f0);
-      __builtin_amdgcn_sched_barrier(0);
-      half(f0, f1, st, I1(), std::true_type(), std::false_type(), std::false_type(), 0, bv, 0,
-           gi);
-      frag_wait(f1);
-      __builtin_amdgcn_sched_barrier(0);
-      half(f1, f0, 0, I0(), std::false_type(), std::false_type(), std::false_type(), 0, bv, 0,
-           gi);
-    }
+      b_offsets(kT2Lead, gi, bv);
+      group(0, bv);
+      Frags f0, f1;
+      static_for<0, 16>([&](auto r_c) __attribute__((always_inline)) {
+        read_one(0, I0(), r_c, offa, offb, f0);
+      });
+      // Slab t: its first K half, with the second half's reads and the index reads of group t + 1;
+      // slab t + 1 published (its copies landed, every wave past its reads of slab t, whose slot
+      // the next group then refills; the indices of group t + 1 were published with slab t); the
+      // second half, with slab t + 1's first reads and group t + 1.
+      for (int t = 0; t + 1 < n_slabs; ++t) {
+        const uint32_t st = (t % kT2Ring) * G::kStage;
+        frag_wait(f0);
+        __builtin_amdgcn_sched_barrier(0);
+        half(f0, f1, st, I1(), std::true_type(), std::false_type(), std::true_type(), 0, bv,
+             t + 1 + kT2Lead, gi);
+        wait_slab();
+        barrier();
+        frag_wait(f1);
+        idx_fence(gi);
+        b_offsets(t + 1 + kT2Lead, gi, bv);
+        __builtin_amdgcn_sched_barrier(0);
+        half(f1, f0, ((t + 1) % kT2Ring) * G::kStage, I0(), std::true_type(), std::true_type(),
+             std::false_type(), t + 1, bv, 0, gi);
+      }
+      {  // the last slab
+        const uint32_t st = ((n_slabs - 1) % kT2Ring) * G::kStage;
+        frag_wait(f0);
+        __builtin_amdgcn_sched_barrier(0);
+        half(f0, f1, st, I1(), std::true_type(), std::false_type(), std::false_type(), 0, bv, 0,
+             gi);
+        frag_wait(f1);
+        __builtin_amdgcn_sched_barrier(0);
+        half(f1, f0, 0, I0(), std::false_type(), std::false_type(), std::false_type(), 0, bv, 0,
+             gi);
+      }
+    };
+    if (gather) run(std::true_type());
+    else run(std::false_type());
     // the trailing groups' copies land before the workgroup's LDS is released
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
@@ -887,20 +926,33 @@ hipError_t launch_tr(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t 
   return hipGetLastError();
 }
 
-template <bool GATHER, bool OUT_F32>
-hipError_t launch_t256(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
-                       int64_t b_rows, const int32_t* b_src_row, const int32_t* seg_offsets,
-                       int num_segments, int64_t total_rows, int N, int M, int splits, void* c,
-                       hipStream_t stream) {
-  auto kern = grouped_wgrad_t256_kernel<GATHER, OUT_F32>;
+template <bool OUT_F32>
+hipError_t launch_t256(const T2Args& args, hipStream_t stream) {
+  auto kern = grouped_wgrad_t256_kernel<OUT_F32>;
   const size_t lds = T2Geo::lds();
   hipError_t err = allow_dynamic_lds(reinterpret_cast<const void*>(kern), lds);
   if (err != hipSuccess) return err;
-  const int64_t tiles = (int64_t)num_segments * ((N + 255) / 256) * ((M + 255) / 256);
-  hipLaunchKernelGGL(kern, dim3((unsigned)(tiles * splits)), dim3(256), lds, stream, a, lda, b,
-                     ldb, b_rows, b_src_row, seg_offsets, num_segments, total_rows, N, M, splits,
-                     c);
+  const int64_t blocks = (int64_t)args.p[0].blocks + (args.count > 1 ? args.p[1].blocks : 0);
+  if (blocks == 0) return hipSuccess;
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, stream, args);
   return hipGetLastError();
+}
+
+T2Product t256_product(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb,
+                       int64_t b_rows, const int32_t* b_src_row, int num_segments, int N, int M,
+                       int splits, void* c) {
+  T2Product p;
+  p.a = a;
+  p.b = b;
+  p.b_src_row = b_src_row;
+  p.c = c;
+  p.lda = lda;
+  p.ldb = ldb;
+  p.b_rows = b_rows;
+  p.N = N;
+  p.M = M;
+  p.blocks = num_segments * ((N + 255) / 256) * ((M + 255) / 256) * splits;
+  return p;
 }
 
 // Whether the 256 x 256 kernel takes a product: both widths whole 256-wide tiles, and no split
@@ -917,11 +969,15 @@ hipError_t launch_tr_any(const uint16_t* a, int64_t lda, const uint16_t* b, int6
                          hipStream_t stream) {
   const bool g = b_src_row != nullptr;
   if (wgrad_t256(N, M, splits)) {
-    if (g)
-      return launch_t256<true, OUT_F32>(a, lda, b, ldb, b_rows, b_src_row, seg_offsets,
-                                        num_segments, total_rows, N, M, splits, c, stream);
-    return launch_t256<false, OUT_F32>(a, lda, b, ldb, b_rows, b_src_row, seg_offsets,
-                                       num_segments, total_rows, N, M, splits, c, stream);
+    T2Args args;
+    args.p[0] = t256_product(a, lda, b, ldb, b_rows, b_src_row, num_segments, N, M, splits, c);
+    args.p[1] = args.p[0];
+    args.seg_offsets = seg_offsets;
+    args.total_rows = total_rows;
+    args.num_segments = num_segments;
+    args.splits = splits;
+    args.count = 1;
+    return launch_t256<OUT_F32>(args, stream);
   }
 #define NT_TR(TN, TM, GG)                                                                      \
   return launch_tr<TN, TM, GG, OUT_F32>(a, lda, b, ldb, b_rows, b_src_row, seg_offsets,         \
@@ -978,6 +1034,41 @@ hipError_t launch_grouped_wgrad(const uint16_t* a, int64_t lda, const uint16_t* 
   hipLaunchKernelGGL(sum, dim3((unsigned)((count / 4 + 255) / 256)), dim3(256), 0, stream,
                      partial, splits, count, c);
   return hipGetLastError();
+}
+
+hipError_t launch_grouped_wgrad_pair(const uint16_t* a0, int64_t lda0, const uint16_t* b0,
+                                     int64_t ldb0, int64_t b_rows0, const int32_t* b_src_row0,
+                                     int N0, int M0, void* c0, const uint16_t* a1, int64_t lda1,
+                                     const uint16_t* b1, int64_t ldb1, int64_t b_rows1,
+                                     const int32_t* b_src_row1, int N1, int M1, void* c1,
+                                     const int32_t* seg_offsets, int num_segments,
+                                     int64_t total_rows, bool c_f32, hipStream_t stream) {
+  if (num_segments == 0) return hipSuccess;
+  const int64_t lim = (int64_t)1 << 31;
+  auto fits = [&](int64_t lda, int64_t ldb, int64_t b_rows, const int32_t* src, int N, int M) {
+    return wgrad_t256(N, M, 1) && total_rows * lda * 2 < lim &&
+           (src ? b_rows : total_rows) * ldb * 2 < lim;
+  };
+  if (!wgrad_regs_override() && fits(lda0, ldb0, b_rows0, b_src_row0, N0, M0) &&
+      fits(lda1, ldb1, b_rows1, b_src_row1, N1, M1)) {
+    // one launch over both tile lists: the second product's tiles start as CUs free up from the
+    // first's, and the launch has one tail instead of two
+    T2Args args;
+    args.p[0] = t256_product(a0, lda0, b0, ldb0, b_rows0, b_src_row0, num_segments, N0, M0, 1, c0);
+    args.p[1] = t256_product(a1, lda1, b1, ldb1, b_rows1, b_src_row1, num_segments, N1, M1, 1, c1);
+    args.seg_offsets = seg_offsets;
+    args.total_rows = total_rows;
+    args.num_segments = num_segments;
+    args.splits = 1;
+    args.count = 2;
+    return c_f32 ? launch_t256<true>(args, stream) : launch_t256<false>(args, stream);
+  }
+  hipError_t err = launch_grouped_wgrad(a0, lda0, b0, ldb0, b_rows0, b_src_row0, seg_offsets,
+                                        num_segments, total_rows, N0, M0, 1, nullptr, c_f32, c0,
+                                        stream);
+  if (err != hipSuccess) return err;
+  return launch_grouped_wgrad(a1, lda1, b1, ldb1, b_rows1, b_src_row1, seg_offsets, num_segments,
+                              total_rows, N1, M1, 1, nullptr, c_f32, c1, stream);
 }
 
 }  // namespace ntmoe

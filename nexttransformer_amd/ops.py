@@ -978,6 +978,45 @@ def _(a, b, b_src_row, seg_offsets, total_rows, splits=1, out_fp32=False):
                        dtype=torch.float32 if out_fp32 else torch.bfloat16)
 
 
+@_custom_op("ntmoe::grouped_wgrad_pair")
+def grouped_wgrad_pair(a0: Tensor, b0: Tensor, b_src_row0: Optional[Tensor], a1: Tensor,
+                       b1: Tensor, b_src_row1: Optional[Tensor], seg_offsets: Tensor,
+                       total_rows: int, out_fp32: bool = False) -> tuple[Tensor, Tensor]:
+    """(grouped_wgrad(a0, b0, b_src_row0, ...), grouped_wgrad(a1, b1, b_src_row1, ...)) over the
+    same segments without split K, bit for bit; one launch when both take the 256 x 256 kernel
+    (widths multiples of 256)."""
+    _on_gpu(a0, b0, b_src_row0, a1, b1, b_src_row1, seg_offsets)
+    for a, b, src in ((a0, b0, b_src_row0), (a1, b1, b_src_row1)):
+        _require(a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16 and a.dim() == 2
+                 and b.dim() == 2 and a.stride(1) == 1 and b.stride(1) == 1,
+                 "grouped_wgrad_pair: a and b must be bf16 matrices with contiguous rows")
+        if src is not None:
+            _require(src.dtype == torch.int32 and src.is_contiguous(),
+                     "grouped_wgrad_pair: b_src_row must be contiguous int32")
+    _require(seg_offsets.dtype == torch.int32 and seg_offsets.dim() == 1
+             and seg_offsets.is_contiguous(),
+             "grouped_wgrad_pair: seg_offsets must be int32 [S+1]")
+    S = seg_offsets.shape[0] - 1
+    dt = torch.float32 if out_fp32 else torch.bfloat16
+    c0 = torch.empty(S, a0.shape[1], b0.shape[1], device=a0.device, dtype=dt)
+    c1 = torch.empty(S, a1.shape[1], b1.shape[1], device=a0.device, dtype=dt)
+    st = nat.load().nt_moe_grouped_wgrad_pair(
+        ptr(a0), a0.stride(0), ptr(b0), b0.stride(0), b0.shape[0], ptr(b_src_row0), a0.shape[1],
+        b0.shape[1], ptr(c0), ptr(a1), a1.stride(0), ptr(b1), b1.stride(0), b1.shape[0],
+        ptr(b_src_row1), a1.shape[1], b1.shape[1], ptr(c1), ptr(seg_offsets), S, total_rows,
+        int(out_fp32), _stream(a0.device))
+    nat.check(st, "ntmoe::grouped_wgrad_pair")
+    return c0, c1
+
+
+@grouped_wgrad_pair.register_fake
+def _(a0, b0, b_src_row0, a1, b1, b_src_row1, seg_offsets, total_rows, out_fp32=False):
+    S = seg_offsets.shape[0] - 1
+    dt = torch.float32 if out_fp32 else torch.bfloat16
+    return (a0.new_empty(S, a0.shape[1], b0.shape[1], dtype=dt),
+            a0.new_empty(S, a1.shape[1], b1.shape[1], dtype=dt))
+
+
 _CU_COUNT = {}
 
 
@@ -1216,10 +1255,14 @@ def moe_backward(grad_out, grad_aux, x, w_router_t, bw, state, *, top_k,
     mark("dx_sum")
     # expert weight gradients over each expert's rows; the shared expert's over all T rows
     f32 = weight_grads_fp32
-    res["w1"] = grouped_wgrad.raw(dfc1, x, src, offsets, A, wgrad_splits(E, dfc1.shape[1], d, A // E,
-                                                                     x.device), f32)
-    res["w2"] = grouped_wgrad.raw(gy, state["h"], None, offsets, A,
-                              wgrad_splits(E, d, state["h"].shape[1], A // E, x.device), f32)
+    h = state["h"]
+    s1 = wgrad_splits(E, dfc1.shape[1], d, A // E, x.device)
+    s2 = wgrad_splits(E, d, h.shape[1], A // E, x.device)
+    if s1 == 1 and s2 == 1:  # both in one call (one launch where both take the 256-wide tiles)
+        res["w1"], res["w2"] = grouped_wgrad_pair.raw(dfc1, x, src, gy, h, None, offsets, A, f32)
+    else:
+        res["w1"] = grouped_wgrad.raw(dfc1, x, src, offsets, A, s1, f32)
+        res["w2"] = grouped_wgrad.raw(gy, h, None, offsets, A, s2, f32)
     if sh:
         res["shared_w1"] = grouped_wgrad.raw(dfc1s, x, None, seg, T,
                                          wgrad_splits(1, dfc1s.shape[1], d, T, x.device), f32)

@@ -517,3 +517,37 @@ def test_router_operands_match_the_torch_construction(E, d, dp, Fs):
     assert torch.equal(first.cpu().view(torch.int16), want.view(torch.int16))
     rt2, none = ops.router_operands(w.cuda(), dp, None, False)
     assert none.numel() == 0 and torch.equal(rt2.cpu().view(torch.int32), want_rt.view(torch.int32))
+
+
+@pytest.mark.parametrize("N0,M0,N1,M1", [(512, 256, 256, 512), (256, 256, 320, 256)],
+                         ids=["one-launch", "two-launches"])
+def test_grouped_wgrad_pair_equals_two_calls(N0, M0, N1, M1):
+    """grouped_wgrad_pair bit for bit against two grouped_wgrad calls (fp32 and bf16 output) over
+    ragged segments (empty, one row, partial slabs, many slabs), the first product gathered: as
+    one launch of the 256 x 256 kernel over both tile lists, and (a width not a multiple of 256)
+    as two launches; and against float64."""
+    from nexttransformer_amd import ops
+    gen = torch.Generator().manual_seed(N0 + M1)
+    sizes = [0, 1, 33, 96, 0, 257, 64, 700]
+    total = sum(sizes)
+    offsets = torch.tensor([0] + list(torch.tensor(sizes).cumsum(0)), dtype=torch.int32).cuda()
+    b_rows = 131
+    a0 = torch.randn(total, N0, generator=gen).to(torch.bfloat16).cuda()
+    b0 = torch.randn(b_rows, M0, generator=gen).to(torch.bfloat16).cuda()
+    src = torch.randint(0, b_rows, (total,), generator=gen, dtype=torch.int32).cuda()
+    a1 = torch.randn(total, N1, generator=gen).to(torch.bfloat16).cuda()
+    b1 = torch.randn(total, M1, generator=gen).to(torch.bfloat16).cuda()
+    for f32 in (True, False):
+        c0, c1 = ops.grouped_wgrad_pair(a0, b0, src, a1, b1, None, offsets, total, f32)
+        w0 = ops.grouped_wgrad(a0, b0, src, offsets, total, 1, f32)
+        w1 = ops.grouped_wgrad(a1, b1, None, offsets, total, 1, f32)
+        assert torch.equal(c0, w0) and torch.equal(c1, w1)
+    bb0 = b0[src.long()].double().cpu()
+    for s in range(len(sizes)):
+        lo, hi = int(offsets[s]), int(offsets[s + 1])
+        ref0 = a0[lo:hi].double().cpu().t() @ bb0[lo:hi]
+        ref1 = a1[lo:hi].double().cpu().t() @ b1[lo:hi].double().cpu()
+        torch.testing.assert_close(c0[s].double().cpu(), ref0.to(torch.bfloat16).double(),
+                                   rtol=1e-2, atol=1e-2)
+        torch.testing.assert_close(c1[s].double().cpu(), ref1.to(torch.bfloat16).double(),
+                                   rtol=1e-2, atol=1e-2)
