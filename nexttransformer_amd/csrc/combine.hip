@@ -17,13 +17,13 @@ namespace ntmoe {
 namespace {
 
 // One wave per output row at a time; the row is walked in column chunks of 64 lanes x VPC
-// 16-byte vectors (VPC = 2: 1024 bf16 per chunk). Waves are persistent over tokens (t, t + the
+// 16-byte vectors (VPC = 2: 1024 bf16 per chunk, when the row is whole chunks of that; else
+// VPC = 1, so a row of 1280 bf16 is chunks of 64, 64 and 32 vectors rather than 128 and 32:
+// 85 against 96 us for the T3 cell's combine). Waves are persistent over tokens (t, t + the
 // grid's waves, ...) and walk the items (token, chunk) in order, issuing the next item's k row
 // loads (and its shared-expert chunk) before summing the current one, so 2 (k + 1) VPC vectors
 // per lane are in flight. KMAX bounds k (registers are sized by it).
-constexpr int VPC = 2;
-
-template <int KMAX>
+template <int KMAX, int VPC>
 __device__ __forceinline__ void combine_rows(
     const uint16_t* __restrict__ y, const int32_t* __restrict__ combine_dest,
     const float* __restrict__ combine_w, int64_t T, int d, int k,
@@ -195,7 +195,7 @@ struct AuxArgs {
 
 // The combine grid plus, when aux.aux_out is set, one last workgroup that computes the losses
 // (they depend only on the router's partials and the counts, so they run beside the combine).
-template <int KMAX>
+template <int KMAX, int VPC>
 __global__ __launch_bounds__(256) void combine_aux_kernel(
     const uint16_t* __restrict__ y, const int32_t* __restrict__ combine_dest,
     const float* __restrict__ combine_w, int64_t T, int d, int k,
@@ -207,8 +207,8 @@ __global__ __launch_bounds__(256) void combine_aux_kernel(
               aux.aux_coeff, aux.z_coeff, aux.aux_out);
     return;
   }
-  combine_rows<KMAX>(y, combine_dest, combine_w, T, d, k, shared_y, ld_shared, out, ld_out,
-                     combine_blocks);
+  combine_rows<KMAX, VPC>(y, combine_dest, combine_w, T, d, k, shared_y, ld_shared, out, ld_out,
+                          combine_blocks);
 }
 
 }  // namespace
@@ -230,8 +230,13 @@ hipError_t launch_combine_aux(const uint16_t* y, const int32_t* combine_dest,
   if (blocks > cap) blocks = cap;
   if (aux_out) ++blocks;
   if (blocks == 0) return hipSuccess;
-  auto kern = k <= 2 ? combine_aux_kernel<2> : (k <= 4 ? combine_aux_kernel<4>
-                                                        : combine_aux_kernel<NT_MOE_MAX_TOPK>);
+  const bool two = (d / 8) % 128 == 0;  // rows of whole 2-vector chunks
+  auto kern = two ? (k <= 2 ? combine_aux_kernel<2, 2>
+                            : (k <= 4 ? combine_aux_kernel<4, 2>
+                                      : combine_aux_kernel<NT_MOE_MAX_TOPK, 2>))
+                  : (k <= 2 ? combine_aux_kernel<2, 1>
+                            : (k <= 4 ? combine_aux_kernel<4, 1>
+                                      : combine_aux_kernel<NT_MOE_MAX_TOPK, 1>));
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream, y, combine_dest,
                      combine_w, T, d, k, shared_y, ld_shared, out, ld_out, aux);
   hipError_t err = hipGetLastError();
