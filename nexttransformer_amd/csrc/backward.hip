@@ -256,22 +256,49 @@ __global__ __launch_bounds__(256) void first_operand_kernel(
     int Ep, int Kc, uint16_t* __restrict__ out) {
   const int per_row = Kc / 8;
   const int64_t n = T * per_row;
+  const bool narrow = n < ((int64_t)1 << 31);  // 32-bit index arithmetic
+  // 8 columns of g lie wholly inside or wholly past E, 16-byte aligned: two loads
+  const bool vec = E % 8 == 0 && (reinterpret_cast<uintptr_t>(g) & 15) == 0;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t t = i / per_row;
-    const int j0 = (int)(i - t * per_row) * 8;
+    int64_t t;
+    int j0;
+    if (narrow) {
+      const int tt = (int)i / per_row;
+      t = tt;
+      j0 = ((int)i - tt * per_row) * 8;
+    } else {
+      t = i / per_row;
+      j0 = (int)(i - t * per_row) * 8;
+    }
     u32x4 v = {0u, 0u, 0u, 0u};
     if (j0 < Fs) {
       v = *reinterpret_cast<const u32x4*>(dfc1s + t * Fs + j0);
     } else if (j0 < Fs + 3 * Ep) {
       const int part = (j0 - Fs) / Ep, e0 = (j0 - Fs) - part * Ep;
       const float* row = g + t * E;
+      float x[8];
+      if (vec) {
+        floatx4 x0 = {0.f, 0.f, 0.f, 0.f}, x1 = x0;
+        if (e0 < E) {
+          x0 = *reinterpret_cast<const floatx4*>(row + e0);
+          x1 = *reinterpret_cast<const floatx4*>(row + e0 + 4);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          x[q] = x0[q];
+          x[4 + q] = x1[q];
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) x[q] = e0 + q < E ? row[e0 + q] : 0.f;
+      }
       uint16_t h[8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
-        const float x = e0 + q < E ? row[e0 + q] : 0.f;
-        const uint16_t hi = f32_to_bf16_bits(x);
-        h[q] = part < 2 ? hi : f32_to_bf16_bits(x - __builtin_bit_cast(float, (uint32_t)hi << 16));
+        const uint16_t hi = f32_to_bf16_bits(x[q]);
+        h[q] = part < 2 ? hi
+                        : f32_to_bf16_bits(x[q] - __builtin_bit_cast(float, (uint32_t)hi << 16));
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) v[q] = (uint32_t)h[2 * q] | ((uint32_t)h[2 * q + 1] << 16);

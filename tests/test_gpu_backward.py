@@ -460,11 +460,11 @@ def test_module_expert_gradients_accumulate_like_autograd():
     assert torch.equal(params[experts[7]].grad, once[experts[7]])
 
 
-@pytest.mark.parametrize("E,Fs", [(40, 64), (256, 320), (8, 0)])
+@pytest.mark.parametrize("E,Fs", [(40, 64), (256, 320), (8, 0), (37, 16)])
 def test_backward_first_operand_is_the_split_and_concatenation(E, Fs):
     """[dfc1s | g_hi | g_hi | g_lo | 0] bit for bit against split_bf16 and torch slicing: E not a
-    multiple of the 32-wide blocks, values spanning exponents, exact bf16 values (lo = 0),
-    negative zero, no shared expert."""
+    multiple of the 32-wide blocks (nor of 8: element-wise loads instead of vector loads), values
+    spanning exponents, exact bf16 values (lo = 0), negative zero, no shared expert."""
     from nexttransformer_amd import ops
     gen = torch.Generator().manual_seed(E + Fs)
     T = 333
