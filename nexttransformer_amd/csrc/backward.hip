@@ -148,13 +148,15 @@ __global__ __launch_bounds__(256) void act_bwd_kernel(const uint16_t* __restrict
 //   z-loss, z = c_z / T sum_t lse_t^2:  dl_e += g_z c_z 2 lse_t / T softmax_e
 // with c_lb = aux_coeff E / (k T^2), c_z = z_coeff, and g_lb, g_z read from grad_aux (the
 // gradient of the forward's aux = {lb + z, lb, z}; NULL = no aux gradient).
+// PER = experts per lane (E <= 64 PER): the per-token work is sized by E, not by the largest E.
+template <int PER>
 __global__ __launch_bounds__(256) void router_bwd_kernel(
     const float* __restrict__ logits, const int32_t* __restrict__ topk_ids,
     const float* __restrict__ topk_w, const float* __restrict__ dw,
     const int32_t* __restrict__ counts, int64_t T, int E, int k, int score_fn,
     const float* __restrict__ grad_aux, float aux_coeff, float z_coeff,
     float* __restrict__ dlogits) {
-  constexpr int PER = NT_MOE_MAX_EXPERTS / 64;
+  const bool sigmoid = score_fn != NT_MOE_SCORE_SOFTMAX;
   const int lane = lane_id();
   // aux = {lb + z, lb, z}: gradients reach lb through entries 0 and 1, z through 0 and 2
   float g_lb = 0.f, g_z = 0.f;
@@ -183,7 +185,7 @@ __global__ __launch_bounds__(256) void router_bwd_kernel(
     for (int i = 0; i < PER; ++i) {
       const bool in = lane + 64 * i < E;
       ex[i] = in ? expf(l[i] - m) : 0.f;
-      sg[i] = in ? sigmoidf_(l[i]) : 0.f;
+      sg[i] = in && sigmoid ? sigmoidf_(l[i]) : 0.f;  // (the softmax path needs none)
       sum_ex += ex[i];
       sum_sg += sg[i];
     }
@@ -346,9 +348,10 @@ hipError_t launch_router_bwd(const float* logits, const int32_t* topk_ids, const
   int64_t blocks = (T + 3) / 4;
   const int64_t cap = (int64_t)num_cus() * 32;
   if (blocks > cap) blocks = cap;
-  hipLaunchKernelGGL(router_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, logits,
-                     topk_ids, topk_w, dw, counts, T, E, k, score_fn, grad_aux, aux_coeff, z_coeff,
-                     dlogits);
+  auto kern = E <= 64 ? router_bwd_kernel<1>
+                      : (E <= 128 ? router_bwd_kernel<2> : router_bwd_kernel<NT_MOE_MAX_EXPERTS / 64>);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream, logits, topk_ids, topk_w,
+                     dw, counts, T, E, k, score_fn, grad_aux, aux_coeff, z_coeff, dlogits);
   return hipGetLastError();
 }
 
