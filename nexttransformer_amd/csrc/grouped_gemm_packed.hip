@@ -152,6 +152,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
   // K steps per tile in the pipeline: an odd count gets one more step that loads and waits like
   // the others but multiplies nothing, so every tile keeps whole pairs.
   const int nks = EDGE ? nk + (nk & 1) : nk;
+  constexpr bool kSplit = EDGE && GATHER;  // partial N tiles may be split (below)
 
   // Segment table and tile prefix (as in the unpacked kernel): clamped, non-decreasing.
   for (int i = threadIdx.x; i <= S; i += blockDim.x) {
@@ -223,12 +224,23 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
       t.seg_end = half ? tile_end : (tile_end < t.m0 + kBM / 2 ? tile_end : t.m0 + kBM / 2);
     }
   };
-  // The idx-th tile of this workgroup.
+  // The idx-th tile of this workgroup. In each round the two workgroups that share a CU
+  // (local l and l + per_xcd / 2) take neighbouring tiles, 2 l' and 2 l' + 1 (l' = l mod
+  // per_xcd / 2), and each workgroup alternates between the even and the odd one from round to
+  // round: where a row tile's N tiles alternate full and partial (the T3 cell's 320-wide
+  // outputs), every CU then runs one of each at a time instead of two of a kind (T3 up
+  // projection 166 -> 155 us with the split partial tiles above; other shapes unchanged).
   auto locate_static = [&](int idx, Tile& t) {
-    if (split_tail && idx == full_rounds)
+    if (split_tail && idx == full_rounds) {
       locate_tl(t_begin + full_rounds * per_xcd + (local >> 1), local & 1, t);
-    else
-      locate_tl(t_begin + local + idx * per_xcd, -1, t);
+    } else {
+      // (full rounds only: the last, partial round takes the first tiles of its range in order)
+      const int h = per_xcd / 2;
+      const int pos = (per_xcd & 1) || idx >= full_rounds
+                          ? local
+                          : (local < h ? 2 * local + (idx & 1) : 2 * (local - h) + 1 - (idx & 1));
+      locate_tl(t_begin + pos + idx * per_xcd, -1, t);
+    }
   };
 
   // Gather indices of tile t into table slot `slot`: the first kBM / 64 waves load 64 rows each,
@@ -255,9 +267,11 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
   // This wave's packed weight blocks for tile t (clamped in a partial N tile): wave-uniform
   // addresses, to which each lane adds lane * 16 bytes.
   auto w_base = [&](const Tile& t, const uint16_t* (&wb)[kWB]) {
+    // a split partial N tile (below): every wave streams the tile's first kWB blocks
+    const int wv = kSplit && NB - t.nt * kTileBlocks <= kWB ? 0 : wave;
 #pragma unroll
     for (int rb = 0; rb < kWB; ++rb) {
-      int nb = t.nt * kTileBlocks + wave * kWB + rb;
+      int nb = t.nt * kTileBlocks + wv * kWB + rb;
       nb = nb < NB ? nb : NB - 1;
       wb[rb] = Wp + ((int64_t)t.s * NB + nb) * (int64_t)nk * kBlockElems;
     }
@@ -420,6 +434,14 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
   int ti = 0;  // this workgroup's tile number
   for (;;) {
     const int live_m = ct.seg_end - ct.m0;  // token rows of this tile that exist (uniform)
+    // A split partial N tile (EDGE with the gather; without it the kernel's registers are at the
+    // limit and the split spills): when the tile's blocks fit one wave's kWB, every wave takes
+    // those blocks with one 32-token block of its own (wave w: rows 32 w .. 32 w + 31) instead of
+    // one wave taking them with all kNJ token blocks while the others idle (the T3 cell's 320-wide
+    // outputs: the second N tile of each row tile holds 2 of 8 blocks).
+    const bool split = kSplit && NB - ct.nt * kTileBlocks <= kWB;
+    const int jb = split ? wave : 0;    // the wave's first token block
+    const int wv = split ? 0 : wave;    // the wave whose weight blocks this wave takes
     const uint16_t* wb_next[kWB];
 #pragma unroll
     for (int rb = 0; rb < kWB; ++rb) wb_next[rb] = wb[rb];
@@ -465,7 +487,8 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
       }
       // The first PF token fragments go out first, so their latency overlaps the issue of this
       // step's loads instead of idling the matrix core.
-      const unsigned char* st = smem + (g % kSA) * kStage;
+      // (a split tile's wave reads its own token block jb)
+      const unsigned char* st = smem + (g % kSA) * kStage + jb * 32 * kRB;
       // NM token fragments (slice q = n / NJ, token block j = n % NJ), read PF ahead.
       auto frag = [&](int n) {
         return *reinterpret_cast<const bf16x8*>(st + (n % NJd) * 32 * kRB + frag_off[n / NJd]);
@@ -573,11 +596,15 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
     // rows; in a partial N tile a wave whose weight blocks all lie past the last one multiplies
     // nothing (its SIMD's matrix core goes to the other workgroup's wave). The loads are the
     // same in every variant.
-    const bool wave_live = !EDGE || ct.nt * kTileBlocks + wave * kWB < NB;
-    if (EDGE && !wave_live) k_loop(std::integral_constant<int, 0>());
-    else if (live_m > kBM / 2) k_loop(std::integral_constant<int, kNJ>());
-    else if (live_m > kBM / 4) k_loop(std::integral_constant<int, kNJ / 2>());
-    else if (kNJ >= 8 && live_m > kBM / 8) k_loop(std::integral_constant<int, kNJ / 4 ? kNJ / 4 : 1>());
+    const bool wave_live = !EDGE || split || ct.nt * kTileBlocks + wave * kWB < NB;
+    // (a split tile's wave multiplies one token block, or none past the segment's rows)
+    const bool mul_none = EDGE && (!wave_live || (split && live_m <= 32 * wave));
+    const bool mul_one = kSplit && split;
+    if (mul_none) k_loop(std::integral_constant<int, 0>());
+    else if (!mul_one && live_m > kBM / 2) k_loop(std::integral_constant<int, kNJ>());
+    else if (!mul_one && live_m > kBM / 4) k_loop(std::integral_constant<int, kNJ / 2>());
+    else if (!mul_one && kNJ >= 8 && live_m > kBM / 8)
+      k_loop(std::integral_constant<int, kNJ / 4 ? kNJ / 4 : 1>());
     else k_loop(std::integral_constant<int, 1>());
 
     // Epilogue. Lane (token j, half h) holds logical block rows 8 h + [0, 8) in elements 0-7 and
@@ -599,14 +626,16 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
       static_assert(RPH * CPR * 16 <= kXposeBytes && 32 % RPH == 0 && RPH % RPS == 0, "passes");
       // chunk c of row r: the 8 rows that share a 128-byte LDS line pattern get distinct chunks
       auto xoff = [](int r, int c) { return r * CPR * 16 + ((c ^ ((r / (8 / CPR)) % CPR)) << 4); };
-      const int col0 = (ct.nt * kTileBlocks + wave * kWB) * (SW ? 16 : 32);
+      const int col0 = (ct.nt * kTileBlocks + wv * kWB) * (SW ? 16 : 32);
       const int t = lane & 31;
 #pragma unroll
       for (int j = 0; j < kNJ; ++j) {
         // block j's outputs packed first (and its pre-activations stored), so its accumulators
         // are free before the transpose
         u32x4 pk[kWB][Ep<EPI>::kStores];
-        const int m_lane = ct.m0 + j * 32 + t;
+        const int m_lane = ct.m0 + (jb + j) * 32 + t;
+        // a split tile's wave holds one token block: its other blocks store nothing
+        const bool j_ok = !(kSplit && split) || j == 0;
 #pragma unroll
         for (int rb = 0; rb < kWB; ++rb)
 #pragma unroll
@@ -628,9 +657,9 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
             pk[rb][st] = u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
                                pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
             if constexpr (KEEP) {  // the fc1 pre-activations, straight from the accumulator layout
-              const int nb = ct.nt * kTileBlocks + wave * kWB + rb;
+              const int nb = ct.nt * kTileBlocks + wv * kWB + rb;
               const int col = SW ? nb * 16 + 8 * hbit : nb * 32 + 16 * st + 8 * hbit;
-              const bool ok = m_lane < ct.seg_end && nb < NB && col < n_out;
+              const bool ok = j_ok && m_lane < ct.seg_end && nb < NB && col < n_out;
               const int64_t prow = (int64_t)m_lane * kPreW * n_out;
 #pragma unroll
               for (int h = 0; h < (SW ? 2 : 1); ++h) {
@@ -661,9 +690,9 @@ __global__ __launch_bounds__(WAVES * 64, 2) void grouped_gemm_packed_kernel(
           for (int sidx = 0; sidx < RPH / RPS; ++sidx) {
             const int r = sidx * RPS + lane / CPR, q = lane % CPR;
             const u32x4 val = *reinterpret_cast<const u32x4*>(xpose + xoff(r, q));
-            const int m = ct.m0 + j * 32 + pass * RPH + r;
+            const int m = ct.m0 + (jb + j) * 32 + pass * RPH + r;
             const int col = col0 + q * 8;
-            const uint32_t voff = (m < ct.seg_end && col < n_out)
+            const uint32_t voff = (j_ok && m < ct.seg_end && col < n_out)
                                       ? (uint32_t)(((int64_t)m * n_out + col) * 2)
                                       : 0x80000000u;
             __builtin_amdgcn_raw_buffer_store_b128(val, out_rsrc, voff, 0, 0);
