@@ -117,6 +117,18 @@ def test_backward_argument_errors_are_einval(lib):
     st = lib.nt_moe_grouped_gemm_bf16_packed_keep(None, 256, 8, None, None, 1, 8, None, 256, 64,
                                                   nat.EPI_NONE, None, None, None)
     assert st == nat.NT_MOE_EINVAL and "SWIGLU or RELU2" in lib.nt_moe_last_error().decode()
+    # the paired weight gradient checks each product's widths and buffers
+    st = lib.nt_moe_grouped_wgrad_pair(None, 256, None, 256, 8, None, 256, 96, None, None, 256,
+                                       None, 256, 8, None, 256, 256, None, None, 1, 8, 1, None)
+    assert st == nat.NT_MOE_EINVAL and "multiples of 64" in lib.nt_moe_last_error().decode()
+    st = lib.nt_moe_grouped_wgrad_pair(None, 256, None, 256, 8, None, 256, 256, None, None, 256,
+                                       None, 256, 8, None, 256, 256, None, None, 1, 8, 1, None)
+    assert st == nat.NT_MOE_EINVAL and "null buffer" in lib.nt_moe_last_error().decode()
+    # router operands: shapes, then the first operand's layout
+    st = lib.nt_moe_router_operands(None, 64, 8, 64, 32, None, 0, 0, None, None, 32, 128, None)
+    assert st == nat.NT_MOE_EINVAL and "d <= dp" in lib.nt_moe_last_error().decode()
+    st = lib.nt_moe_router_operands(None, 64, 8, 64, 64, None, 0, 0, None, None, 32, 128, None)
+    assert st == nat.NT_MOE_EINVAL and "null" in lib.nt_moe_last_error().decode()
 
 
 def test_ops_reject_cpu_tensors():
