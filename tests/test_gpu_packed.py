@@ -335,3 +335,35 @@ def test_packed_forward_is_deterministic():
     for out, aux in runs[1:]:
         assert torch.equal(out.view(torch.int16), runs[0][0].view(torch.int16))
         assert torch.equal(aux, runs[0][1])
+
+
+@pytest.mark.parametrize("epilogue,n_out", [(1, 288), (2, 288), (1, 320)],
+                         ids=["relu2-one-block", "plain-one-block", "relu2-two-blocks"])
+def test_split_partial_tiles_match_plain(epilogue, n_out):
+    """Gathered products whose last N tile holds one or two weight blocks run it split over the
+    waves by token block (every wave takes those blocks with its own 32 rows): outputs and the
+    kept pre-activations bit for bit equal to the plain-weight kernel's, over segments that end
+    inside each wave's rows, with odd and even K-step counts (SwiGLU's split tiles, 160 outputs,
+    are checked against fp32 in test_packed_gemm_matches_fp32: the plain kernel takes no SwiGLU
+    width that is not a multiple of 64)."""
+    from nexttransformer_amd import _native as nat, ops
+    for K in (320, 512):
+        g = torch.Generator().manual_seed(n_out + K + epilogue)
+        counts = torch.tensor([0, 1, 31, 33, 64, 97, 128, 129, 300, 0, 513])
+        seg = torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)]).to(torch.int32).cuda()
+        rows, S = int(counts.sum()), len(counts)
+        R = 2 * n_out if epilogue == 0 else n_out
+        a = torch.randn(2000, K, generator=g).to(torch.bfloat16).cuda()
+        src = torch.randint(0, 2000, (rows,), generator=g, dtype=torch.int32).cuda()
+        w = (torch.randn(S, R, K, generator=g) * 0.05).to(torch.bfloat16).cuda()
+        wp = ops.pack_expert_weights(w, epilogue)
+        packed = ops.grouped_gemm_packed(a, src, seg, wp, epilogue, rows)
+        plain = ops.grouped_gemm(a, src, seg, w, epilogue, rows)
+        torch.cuda.synchronize()
+        assert torch.equal(packed.view(torch.int16), plain.view(torch.int16)), K
+        if epilogue != nat.EPI_NONE:
+            c, pre = ops.grouped_gemm_packed_keep(a, src, seg, wp, epilogue, rows)
+            z = ops.grouped_gemm(a, src, seg, w, nat.EPI_NONE, rows)
+            torch.cuda.synchronize()
+            assert torch.equal(c.view(torch.int16), plain.view(torch.int16)), K
+            assert torch.equal(pre.view(torch.int16), z.view(torch.int16)), K
