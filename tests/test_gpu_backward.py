@@ -196,6 +196,38 @@ def test_combine_backward_is_exact_transpose():
     torch.testing.assert_close(gw.cpu().double(), ref, rtol=1e-5, atol=1e-4)
 
 
+@pytest.mark.parametrize("T,k,shared", [(1, 1, True), (2, 3, False), (37, 8, True),
+                                        (515, 4, True), (4099, 8, False)])
+def test_combine_row_shapes_agree_bit_for_bit(T, k, shared):
+    """The combine walks a row in chunks whose shape depends on d (64-lane chunks, the last
+    one partly idle, at d = 256, 1280 and 1344, whole 64-vector chunks at d = 1536, 128-vector
+    chunks at d = 2048) but sums every column in the same order, so the first d columns of the
+    d = 2048 combine over the same rows equal each narrower one bit for bit; all against
+    float64. The shared rows have a row stride other than d."""
+    from nexttransformer_amd import ops
+    E, D = 16, 2048
+    gen = torch.Generator().manual_seed(31 + T + k)
+    ids = torch.rand(T, E, generator=gen).topk(k, dim=1).indices.int().cuda()
+    w = torch.rand(T, k, generator=gen).cuda()
+    counts, _, _, _, cdest, cw, _ = ops.route_plan(ids, w, E, None, False)
+    nb = (T + 63) // 64
+    pp, zp = torch.rand(nb, E, generator=gen).cuda(), torch.rand(nb, generator=gen).cuda()
+    y = torch.randn(T * k, D, generator=gen).to(torch.bfloat16).cuda()
+    sh = torch.randn(T, D + 64, generator=gen).to(torch.bfloat16).cuda() if shared else None
+    wide, wide_aux = ops.combine_aux(y, cdest, cw, None if sh is None else sh[:, :D], pp, zp,
+                                     counts, 0.01, 0.001)
+    dest = cdest.cpu().long()
+    ref = (cw.cpu().double()[:, :, None] * y.cpu().double()[dest]).sum(1)
+    if shared:
+        ref += sh[:, :D].cpu().double()
+    for d in (256, 1280, 1344, 1536):
+        got, aux = ops.combine_aux(y[:, :d].contiguous(), cdest, cw,
+                                   None if sh is None else sh[:, :d], pp, zp, counts, 0.01, 0.001)
+        assert torch.equal(got, wide[:, :d]), d
+        assert torch.equal(aux, wide_aux), d
+    torch.testing.assert_close(wide.cpu().double(), ref, rtol=1e-2, atol=1e-3)
+
+
 @pytest.mark.parametrize("gather", [False, True])
 def test_grouped_wgrad_matches_float64(gather):
     """Ragged segments (empty, shorter than one 32-row step, not a multiple of it, long)."""
